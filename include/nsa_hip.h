@@ -1,0 +1,161 @@
+/*
+ * C ABI of libnsa_hip.so: the MI355X (gfx950) Native Sparse Attention hot path.
+ *
+ * Each attention entry point takes exactly the argument list of the Triton launch
+ * it replaces in the reference (tensors, sm_scale, L, M, the stride groups, then the
+ * constexpr shape parameters), followed by the element type, a caller-allocated
+ * device workspace and the HIP stream.  Pointers are device pointers, strides are in
+ * elements, exactly as torch reports them.  Nothing is allocated and no state is
+ * kept; every call is asynchronous on `stream`.
+ *
+ * Conventions shared by every attention entry point
+ *   - K is stored [B, G, dk, T] and the caller passes its strides as
+ *     (z, g, time, dk), i.e. k.stride(0), k.stride(1), k.stride(3), k.stride(2).
+ *     K, V, dK, dV accept any strides.
+ *   - Q, Out, dOut and dQ need unit stride on the feature axis and 16-byte aligned
+ *     rows (NSA_ERR_LAYOUT otherwise; the Python shim then passes a compact copy).
+ *   - head_dim_qk / head_dim_v are the real widths.  Pairs without a compiled kernel
+ *     return NSA_ERR_UNSUPPORTED (the shim zero-pads to a supported pair).
+ *   - dK and dV are accumulated into (the caller zero-fills them, as in the
+ *     reference); dQ is overwritten.
+ *   - dtype: NSA_F32 or NSA_BF16 (Q/K/V/Out/dOut/dQ/dK/dV share it; L, M are fp32).
+ *   - Work is deterministic: no floating-point atomics anywhere.
+ * Return value: NSA_OK or an NSA_ERR_* code; nsa_last_error() describes the failure.
+ */
+#ifndef NSA_HIP_H
+#define NSA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* nsa_stream_t; /* == hipStream_t */
+
+enum { NSA_F32 = 0, NSA_BF16 = 1 };
+enum {
+  NSA_OK = 0,
+  NSA_ERR_INVALID = 1,
+  NSA_ERR_UNSUPPORTED = 2,
+  NSA_ERR_LAYOUT = 3,
+  NSA_ERR_WORKSPACE = 4,
+  NSA_ERR_HIP = 5
+};
+
+/* ABI revision of this header. */
+int nsa_abi_version(void);
+/* Text of the last error raised on the calling thread ("" if none). */
+const char* nsa_last_error(void);
+/* 1 if a kernel exists for (dtype, dk, dv). */
+int nsa_head_dims_supported(int dtype, int dk, int dv);
+
+/* ---- workspace sizes (bytes) ------------------------------------------------
+ * branch: 0 sliding, 1 compression, 2 selection.  n_ctx_kv is T for sliding and
+ * selection and N_BLOCKS for compression; n_slots / block_size_selection are only
+ * read for selection. */
+size_t nsa_fwd_workspace_size(int branch, int dtype, int Z, int H, int n_kv_groups, int n_ctx_q, int n_ctx_kv,
+                              int head_dim_qk, int head_dim_v, int n_slots, int block_size_selection);
+size_t nsa_bwd_workspace_size(int branch, int dtype, int Z, int H, int n_kv_groups, int n_ctx_q, int n_ctx_kv,
+                              int head_dim_qk, int head_dim_v, int n_slots, int block_size_selection);
+
+/* ---- sliding window --------------------------------------------------------
+ * Replaces _nsa_sliding_window_fwd_kernel (reference nsa/kernels.py:1151-1191) and
+ * _nsa_sliding_window_bwd_kernel (nsa/kernels.py:1303-1363).  Key j is visible to
+ * query t iff t - window_size < j <= t. */
+int nsa_sliding_window_fwd(const void* Q, const void* K, const void* V, void* Out, float sm_scale, float* L, float* M,
+                           int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_qk,
+                           int64_t stride_kz, int64_t stride_kg, int64_t stride_kn, int64_t stride_kk,
+                           int64_t stride_vz, int64_t stride_vg, int64_t stride_vn, int64_t stride_vk,
+                           int64_t stride_oz, int64_t stride_oh, int64_t stride_om, int64_t stride_ok,
+                           int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t stride_mz,
+                           int64_t stride_mh, int64_t stride_mm, int Z, int H, int n_kv_groups, int n_ctx,
+                           int window_size, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
+                           size_t workspace_bytes, nsa_stream_t stream);
+
+int nsa_sliding_window_bwd(const void* Q, const void* K, const void* V, const void* Out, const void* dOut,
+                           float sm_scale, const float* L, const float* M, int64_t stride_qz, int64_t stride_qh,
+                           int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
+                           int64_t stride_kn, int64_t stride_kk, int64_t stride_vz, int64_t stride_vg,
+                           int64_t stride_vn, int64_t stride_vk, int64_t stride_oz, int64_t stride_oh,
+                           int64_t stride_om, int64_t stride_ok, int64_t stride_lz, int64_t stride_lh,
+                           int64_t stride_lm, int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, void* dQ,
+                           void* dK, void* dV, int64_t stride_dqz, int64_t stride_dqh, int64_t stride_dqm,
+                           int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg, int64_t stride_dkn,
+                           int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg, int64_t stride_dvn,
+                           int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx, int window_size,
+                           int head_dim_qk, int head_dim_v, int dtype, void* workspace, size_t workspace_bytes,
+                           nsa_stream_t stream);
+
+/* ---- compression -----------------------------------------------------------
+ * Replaces _nsa_compression_fwd_kernel (nsa/kernels.py:1533-1574) and
+ * _nsa_compression_bwd_kernel (nsa/kernels.py:1690-1751).  Compressed key i is
+ * visible to query t iff Block_ends[i] <= t; rows with no visible key produce 0,
+ * L = M = -inf.  Block_ends: int32, contiguous, N_BLOCKS entries. */
+int nsa_compression_fwd(const void* Q, const void* K_compressed, const void* V_compressed, const int32_t* Block_ends,
+                        void* Out, float sm_scale, float* L, float* M, int64_t stride_qz, int64_t stride_qh,
+                        int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
+                        int64_t stride_kn, int64_t stride_kk, int64_t stride_vz, int64_t stride_vg,
+                        int64_t stride_vn, int64_t stride_vk, int64_t stride_oz, int64_t stride_oh,
+                        int64_t stride_om, int64_t stride_ok, int64_t stride_lz, int64_t stride_lh,
+                        int64_t stride_lm, int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, int Z, int H,
+                        int n_kv_groups, int n_ctx_q, int n_blocks, int head_dim_qk, int head_dim_v, int dtype,
+                        void* workspace, size_t workspace_bytes, nsa_stream_t stream);
+
+int nsa_compression_bwd(const void* Q, const void* K_blocks, const void* V_blocks, const int32_t* Block_ends,
+                        const void* Out, const void* dOut, float sm_scale, const float* L, const float* M,
+                        int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_qk,
+                        int64_t stride_kz, int64_t stride_kg, int64_t stride_kn, int64_t stride_kk,
+                        int64_t stride_vz, int64_t stride_vg, int64_t stride_vn, int64_t stride_vk,
+                        int64_t stride_oz, int64_t stride_oh, int64_t stride_om, int64_t stride_ok,
+                        int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t stride_mz,
+                        int64_t stride_mh, int64_t stride_mm, void* dQ, void* dK, void* dV, int64_t stride_dqz,
+                        int64_t stride_dqh, int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz,
+                        int64_t stride_dkg, int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz,
+                        int64_t stride_dvg, int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups,
+                        int n_ctx_q, int n_blocks, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
+                        size_t workspace_bytes, nsa_stream_t stream);
+
+/* ---- top-n block selection -------------------------------------------------
+ * Replaces _nsa_sparse_selection_fwd_kernel (nsa/kernels.py:594-654) and
+ * _nsa_sparse_selection_bwd_kernel (nsa/kernels.py:836-906).  Block_indices is
+ * [B, G, Tq, n_slots] (int32, or int64 when index_is_int64), -1 = empty slot.
+ * Key j is visible to query t iff (j <= t when is_causal) and j lies in one of the
+ * row's blocks [idx*l', idx*l'+l').  Repeated indices count once.  With
+ * all_invalid_fallback set, a row whose slots are all -1 uses block t / l' (the
+ * autograd wrapper's rule, nsa/kernels.py:199-205).  block_size_selection must be
+ * a multiple of 16. */
+int nsa_sparse_selection_fwd(const void* Q, const void* K, const void* V, const void* Block_indices, void* Out,
+                             float sm_scale, float* L, float* M, int64_t stride_qz, int64_t stride_qh,
+                             int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
+                             int64_t stride_kn, int64_t stride_kk, int64_t stride_vz, int64_t stride_vg,
+                             int64_t stride_vn, int64_t stride_vk, int64_t stride_oz, int64_t stride_oh,
+                             int64_t stride_om, int64_t stride_ok, int64_t stride_bz, int64_t stride_bg,
+                             int64_t stride_bm, int64_t stride_bn, int64_t stride_lz, int64_t stride_lh,
+                             int64_t stride_lm, int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, int Z, int H,
+                             int n_kv_groups, int n_ctx_q, int n_ctx_kv, int n_slots, int block_size_selection,
+                             int is_causal, int index_is_int64, int all_invalid_fallback, int head_dim_qk,
+                             int head_dim_v, int dtype, void* workspace, size_t workspace_bytes,
+                             nsa_stream_t stream);
+
+int nsa_sparse_selection_bwd(const void* Q, const void* K, const void* V, const void* Block_indices, const void* Out,
+                             const void* dOut, float sm_scale, const float* L, const float* M, int64_t stride_qz,
+                             int64_t stride_qh, int64_t stride_qm, int64_t stride_qk, int64_t stride_kz,
+                             int64_t stride_kg, int64_t stride_kn, int64_t stride_kk, int64_t stride_vz,
+                             int64_t stride_vg, int64_t stride_vn, int64_t stride_vk, int64_t stride_oz,
+                             int64_t stride_oh, int64_t stride_om, int64_t stride_ok, int64_t stride_bz,
+                             int64_t stride_bg, int64_t stride_bm, int64_t stride_bn, int64_t stride_lz,
+                             int64_t stride_lh, int64_t stride_lm, int64_t stride_mz, int64_t stride_mh,
+                             int64_t stride_mm, void* dQ, void* dK, void* dV, int64_t stride_dqz, int64_t stride_dqh,
+                             int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg,
+                             int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
+                             int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
+                             int n_ctx_kv, int n_slots, int block_size_selection, int is_causal, int index_is_int64,
+                             int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
+                             size_t workspace_bytes, nsa_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NSA_HIP_H */

@@ -1,0 +1,443 @@
+// C ABI entry points (declared in include/nsa_hip.h): argument validation, the
+// workspace layout, and the launch sequence of each NSA attention operator.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/nsa_hip.h"
+#include "nsa_attn.h"
+#include "nsa_kernels.h"
+
+using namespace nsa;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_hip(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(NSA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return NSA_OK;
+}
+
+bool dims_supported(int dk, int dv) {
+#define NSA_SUP(A, B) \
+  if (dk == A && dv == B) return true;
+  NSA_HEAD_DIMS(NSA_SUP)
+#undef NSA_SUP
+  return false;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct Shape {
+  int br, dtype, Z, H, G, Tq, Tkv, dk, dv, nslots, lprime;
+  int hpg() const { return H / G; }
+  int Tp() const { return ((Tkv + 63) / 64) * 64 + 64; }
+  int esz() const { return dtype == NSA_F32 ? 4 : 2; }
+  int nblk() const { return br == kSelection ? (Tkv + lprime - 1) / lprime : 0; }
+  int nsubblk() const { return (lprime + 63) / 64; }
+  int items_per_bg() const {
+    if (br == kCompression) return ((Tkv + 63) / 64) * ((Tq + kSegT - 1) / kSegT);
+    if (br == kSelection) return nsubblk() * (nblk() + (int)(((int64_t)Tq * nslots + kSegT - 1) / kSegT));
+    return 0;
+  }
+};
+
+struct Layout {
+  size_t kt = 0, kn = 0, vt = 0, vn = 0, lse2 = 0, delta = 0, clean = 0, chunk = 0, csr_off = 0, csr_t = 0,
+         seg_off = 0, partial = 0, total = 0;
+};
+
+// Offsets into the caller's workspace (every buffer 256-byte aligned).
+Layout make_layout(const Shape& s, bool bwd) {
+  Layout L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = off;
+    off += align256(bytes);
+    return at;
+  };
+  const size_t BG = (size_t)s.Z * s.G;
+  const size_t kbytes = BG * s.Tp() * s.dk * s.esz();
+  const size_t vbytes = BG * s.Tp() * s.dv * s.esz();
+  L.kt = take(kbytes);
+  if (bwd) {
+    L.kn = take(kbytes);
+    L.vn = take(vbytes);
+    L.lse2 = take((size_t)s.Z * s.H * s.Tq * 4);
+    L.delta = take((size_t)s.Z * s.H * s.Tq * 4);
+  } else {
+    L.vt = take(vbytes);
+  }
+  if (s.br == kSelection) {
+    L.clean = take(BG * s.Tq * s.nslots * 4);
+    if (bwd) {
+      L.chunk = take(BG * sel_csr_chunks(s.Tq) * s.nblk() * 4);
+      L.csr_off = take(BG * (s.nblk() + 1) * 4);
+      L.seg_off = take(BG * (s.nblk() + 1) * 4);
+      L.csr_t = take(BG * s.Tq * s.nslots * 4);
+    }
+  }
+  if (bwd && s.br != kSliding) L.partial = take(BG * s.items_per_bg() * 64 * (size_t)(s.dk + s.dv) * 4);
+  L.total = off;
+  return L;
+}
+
+bool row_ok(const void* p, int64_t inner, int64_t s0, int64_t s1, int64_t s2, int esz) {
+  if (inner != 1) return false;
+  if (((uintptr_t)p) % 16) return false;
+  return (s0 * esz) % 16 == 0 && (s1 * esz) % 16 == 0 && (s2 * esz) % 16 == 0;
+}
+
+int validate(const Shape& s) {
+  if (s.dtype != NSA_F32 && s.dtype != NSA_BF16) return fail(NSA_ERR_INVALID, "dtype %d not supported", s.dtype);
+  if (s.Z <= 0 || s.H <= 0 || s.G <= 0 || s.Tq < 0 || s.Tkv < 0)
+    return fail(NSA_ERR_INVALID, "bad shape Z=%d H=%d G=%d Tq=%d Tkv=%d", s.Z, s.H, s.G, s.Tq, s.Tkv);
+  if (s.H % s.G) return fail(NSA_ERR_INVALID, "H=%d not a multiple of n_kv_groups=%d", s.H, s.G);
+  if (!dims_supported(s.dk, s.dv))
+    return fail(NSA_ERR_UNSUPPORTED, "no kernel for head dims dk=%d dv=%d", s.dk, s.dv);
+  if (s.br == kSelection) {
+    if (s.lprime <= 0 || s.lprime % 16) return fail(NSA_ERR_INVALID, "block_size_selection=%d must be a positive multiple of 16", s.lprime);
+    if (s.nslots < 0 || s.nslots > 64) return fail(NSA_ERR_INVALID, "n_slots=%d outside [0, 64]", s.nslots);
+    const int nt = kFwdCols / s.hpg() + 2;
+    if ((int64_t)nt * s.nslots > kSelListMax)
+      return fail(NSA_ERR_UNSUPPORTED, "n_slots=%d too large for %d heads per group", s.nslots, s.hpg());
+    if (s.nblk() > kSelMaxBlocks) return fail(NSA_ERR_UNSUPPORTED, "%d selection blocks exceed %d", s.nblk(), kSelMaxBlocks);
+  }
+  return NSA_OK;
+}
+
+AttnArgs base_args(const Shape& s, float scale) {
+  AttnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.B = s.Z;
+  a.H = s.H;
+  a.G = s.G;
+  a.hpg = s.hpg();
+  a.Tq = s.Tq;
+  a.Tkv = s.Tkv;
+  a.Tp = s.Tp();
+  a.scale = scale;
+  a.lprime = s.lprime > 0 ? s.lprime : 1;
+  a.nslots = s.nslots;
+  a.nblk = s.nblk();
+  a.causal = 1;
+  return a;
+}
+
+template <typename P> P* at(void* ws, size_t off) { return reinterpret_cast<P*>(reinterpret_cast<char*>(ws) + off); }
+
+struct FwdIO {
+  const void *Q, *K, *V;
+  void* Out;
+  float *L, *M;
+  int64_t sq[4], sk[4], sv[4], so[4], sl[3], sm[3];
+};
+
+int run_fwd(const Shape& s, const FwdIO& io, float scale, int window, const int32_t* block_ends, const void* idx,
+            const int64_t* sidx, int idx64, int fallback, int causal, void* ws, size_t ws_bytes, hipStream_t st) {
+  int rc = validate(s);
+  if (rc) return rc;
+  if (!row_ok(io.Q, io.sq[3], io.sq[0], io.sq[1], io.sq[2], s.esz()))
+    return fail(NSA_ERR_LAYOUT, "Q needs unit feature stride and 16-byte aligned rows");
+  if (!row_ok(io.Out, io.so[3], io.so[0], io.so[1], io.so[2], s.esz()))
+    return fail(NSA_ERR_LAYOUT, "Out needs unit feature stride and 16-byte aligned rows");
+  if (s.br == kSliding && window <= 0) return fail(NSA_ERR_INVALID, "window_size=%d must be positive", window);
+  const Layout L = make_layout(s, false);
+  if (ws_bytes < L.total) return fail(NSA_ERR_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, L.total);
+  if (s.Tq == 0) return NSA_OK;
+
+  AttnArgs a = base_args(s, scale);
+  a.q = io.Q;
+  a.sq_b = io.sq[0];
+  a.sq_h = io.sq[1];
+  a.sq_t = io.sq[2];
+  a.o = io.Out;
+  a.so_b = io.so[0];
+  a.so_h = io.so[1];
+  a.so_t = io.so[2];
+  a.L = io.L;
+  a.sl_b = io.sl[0];
+  a.sl_h = io.sl[1];
+  a.sl_t = io.sl[2];
+  a.M = io.M;
+  a.sm_b = io.sm[0];
+  a.sm_h = io.sm[1];
+  a.sm_t = io.sm[2];
+  a.window = window;
+  a.block_ends = block_ends;
+  a.causal = causal;
+  a.kt = at<char>(ws, L.kt);
+  a.vt = at<char>(ws, L.vt);
+
+  launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp,
+                at<char>(ws, L.kt), nullptr, st);
+  launch_repack(s.dtype, io.V, io.sv[0], io.sv[1], io.sv[2], io.sv[3], s.Z, s.G, s.Tkv, s.dv, a.Tp, nullptr,
+                at<char>(ws, L.vt), st);
+  if (s.br == kSelection) {
+    launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
+                     s.Tkv, fallback, causal, at<int>(ws, L.clean), nullptr, s.nblk(), st);
+    a.sel = at<int>(ws, L.clean);
+  }
+  if ((rc = check_hip("prep"))) return rc;
+  if (!dispatch_attn_fwd(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no forward kernel");
+  return check_hip("attention forward");
+}
+
+struct BwdIO {
+  const void *Q, *K, *V, *Out, *dOut;
+  const float *L, *M;
+  void *dQ, *dK, *dV;
+  int64_t sq[4], sk[4], sv[4], so[4], sl[3], sm[3], sdq[4], sdk[4], sdv[4];
+};
+
+int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int32_t* block_ends, const void* idx,
+            const int64_t* sidx, int idx64, int fallback, int causal, void* ws, size_t ws_bytes, hipStream_t st) {
+  int rc = validate(s);
+  if (rc) return rc;
+  if (!row_ok(io.Q, io.sq[3], io.sq[0], io.sq[1], io.sq[2], s.esz()))
+    return fail(NSA_ERR_LAYOUT, "Q needs unit feature stride and 16-byte aligned rows");
+  if (!row_ok(io.dOut, io.so[3], io.so[0], io.so[1], io.so[2], s.esz()))
+    return fail(NSA_ERR_LAYOUT, "dOut (Out strides) needs unit feature stride and 16-byte aligned rows");
+  if (!row_ok(io.dQ, io.sdq[3], io.sdq[0], io.sdq[1], io.sdq[2], s.esz()))
+    return fail(NSA_ERR_LAYOUT, "dQ needs unit feature stride and 16-byte aligned rows");
+  if (s.br == kSliding && window <= 0) return fail(NSA_ERR_INVALID, "window_size=%d must be positive", window);
+  const Layout L = make_layout(s, true);
+  if (ws_bytes < L.total) return fail(NSA_ERR_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, L.total);
+  if (s.Tq == 0) return NSA_OK;
+
+  AttnArgs a = base_args(s, scale);
+  a.q = io.Q;
+  a.sq_b = io.sq[0];
+  a.sq_h = io.sq[1];
+  a.sq_t = io.sq[2];
+  // the reference reads dOut with Out's strides (nsa/kernels.py:1378-1384)
+  a.o = const_cast<void*>(io.Out);
+  a.so_b = io.so[0];
+  a.so_h = io.so[1];
+  a.so_t = io.so[2];
+  a.dout = io.dOut;
+  a.sdo_b = io.so[0];
+  a.sdo_h = io.so[1];
+  a.sdo_t = io.so[2];
+  a.L = const_cast<float*>(io.L);
+  a.sl_b = io.sl[0];
+  a.sl_h = io.sl[1];
+  a.sl_t = io.sl[2];
+  a.M = const_cast<float*>(io.M);
+  a.sm_b = io.sm[0];
+  a.sm_h = io.sm[1];
+  a.sm_t = io.sm[2];
+  a.dq = io.dQ;
+  a.sdq_b = io.sdq[0];
+  a.sdq_h = io.sdq[1];
+  a.sdq_t = io.sdq[2];
+  a.dk = io.dK;
+  a.sdk_b = io.sdk[0];
+  a.sdk_g = io.sdk[1];
+  a.sdk_t = io.sdk[2];
+  a.sdk_d = io.sdk[3];
+  a.dv = io.dV;
+  a.sdv_b = io.sdv[0];
+  a.sdv_g = io.sdv[1];
+  a.sdv_t = io.sdv[2];
+  a.sdv_d = io.sdv[3];
+  a.window = window;
+  a.block_ends = block_ends;
+  a.causal = causal;
+  a.kt = at<char>(ws, L.kt);
+  a.kn = at<char>(ws, L.kn);
+  a.vn = at<char>(ws, L.vn);
+  a.lse2 = at<float>(ws, L.lse2);
+  a.delta = at<float>(ws, L.delta);
+  a.items_per_bg = s.items_per_bg();
+  if (L.partial || s.br != kSliding) a.partial = at<float>(ws, L.partial);
+
+  launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp,
+                at<char>(ws, L.kt), at<char>(ws, L.kn), st);
+  launch_repack(s.dtype, io.V, io.sv[0], io.sv[1], io.sv[2], io.sv[3], s.Z, s.G, s.Tkv, s.dv, a.Tp,
+                at<char>(ws, L.vn), nullptr, st);
+  launch_bwd_rowstats(s.dtype, a, s.dv, st);
+  if (s.br == kSelection) {
+    launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
+                     s.Tkv, fallback, causal, at<int>(ws, L.clean), at<int>(ws, L.chunk), s.nblk(), st);
+    launch_sel_csr(at<int>(ws, L.clean), at<int>(ws, L.chunk), s.Z, s.G, s.Tq, s.nslots, s.nblk(),
+                   at<int>(ws, L.csr_off), at<int>(ws, L.csr_t), at<int>(ws, L.seg_off), st);
+    a.sel = at<int>(ws, L.clean);
+    a.csr_off = at<int>(ws, L.csr_off);
+    a.csr_t = at<int>(ws, L.csr_t);
+    a.seg_off = at<int>(ws, L.seg_off);
+  }
+  if ((rc = check_hip("backward prep"))) return rc;
+  if (!dispatch_attn_bwd_dq(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no dQ kernel");
+  if ((rc = check_hip("dQ kernel"))) return rc;
+  if (!dispatch_attn_bwd_dkdv(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no dK/dV kernel");
+  if ((rc = check_hip("dK/dV kernel"))) return rc;
+  if (s.br != kSliding) {
+    launch_partial_reduce(s.dtype, s.dk, s.dv, s.br, a, st);
+    if ((rc = check_hip("dK/dV reduce"))) return rc;
+  }
+  return NSA_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int nsa_abi_version(void) { return 1; }
+const char* nsa_last_error(void) { return g_err; }
+int nsa_head_dims_supported(int dtype, int dk, int dv) {
+  return (dtype == NSA_F32 || dtype == NSA_BF16) && dims_supported(dk, dv);
+}
+
+size_t nsa_fwd_workspace_size(int branch, int dtype, int Z, int H, int G, int Tq, int Tkv, int dk, int dv, int nslots,
+                              int lprime) {
+  Shape s{branch, dtype, Z, H, G, Tq, Tkv, dk, dv, nslots, lprime > 0 ? lprime : 64};
+  if (G <= 0 || H % G) return 0;
+  return make_layout(s, false).total;
+}
+size_t nsa_bwd_workspace_size(int branch, int dtype, int Z, int H, int G, int Tq, int Tkv, int dk, int dv, int nslots,
+                              int lprime) {
+  Shape s{branch, dtype, Z, H, G, Tq, Tkv, dk, dv, nslots, lprime > 0 ? lprime : 64};
+  if (G <= 0 || H % G) return 0;
+  return make_layout(s, true).total;
+}
+
+#define NSA_FWD_IO                                                                                    \
+  FwdIO io{Q, K, V, Out, L, M,                                                                        \
+           {stride_qz, stride_qh, stride_qm, stride_qk}, {stride_kz, stride_kg, stride_kn, stride_kk}, \
+           {stride_vz, stride_vg, stride_vn, stride_vk}, {stride_oz, stride_oh, stride_om, stride_ok}, \
+           {stride_lz, stride_lh, stride_lm}, {stride_mz, stride_mh, stride_mm}};
+#define NSA_BWD_IO                                                                                        \
+  BwdIO io{Q, K, V, Out, dOut, L, M, dQ, dK, dV,                                                          \
+           {stride_qz, stride_qh, stride_qm, stride_qk}, {stride_kz, stride_kg, stride_kn, stride_kk},     \
+           {stride_vz, stride_vg, stride_vn, stride_vk}, {stride_oz, stride_oh, stride_om, stride_ok},     \
+           {stride_lz, stride_lh, stride_lm}, {stride_mz, stride_mh, stride_mm},                           \
+           {stride_dqz, stride_dqh, stride_dqm, stride_dqk}, {stride_dkz, stride_dkg, stride_dkn, stride_dkk}, \
+           {stride_dvz, stride_dvg, stride_dvn, stride_dvk}};
+
+int nsa_sliding_window_fwd(const void* Q, const void* K, const void* V, void* Out, float sm_scale, float* L, float* M,
+                           int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_qk,
+                           int64_t stride_kz, int64_t stride_kg, int64_t stride_kn, int64_t stride_kk,
+                           int64_t stride_vz, int64_t stride_vg, int64_t stride_vn, int64_t stride_vk,
+                           int64_t stride_oz, int64_t stride_oh, int64_t stride_om, int64_t stride_ok,
+                           int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t stride_mz,
+                           int64_t stride_mh, int64_t stride_mm, int Z, int H, int n_kv_groups, int n_ctx,
+                           int window_size, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
+                           size_t workspace_bytes, nsa_stream_t stream) {
+  NSA_FWD_IO
+  Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64};
+  return run_fwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
+                 (hipStream_t)stream);
+}
+
+int nsa_sliding_window_bwd(const void* Q, const void* K, const void* V, const void* Out, const void* dOut,
+                           float sm_scale, const float* L, const float* M, int64_t stride_qz, int64_t stride_qh,
+                           int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
+                           int64_t stride_kn, int64_t stride_kk, int64_t stride_vz, int64_t stride_vg,
+                           int64_t stride_vn, int64_t stride_vk, int64_t stride_oz, int64_t stride_oh,
+                           int64_t stride_om, int64_t stride_ok, int64_t stride_lz, int64_t stride_lh,
+                           int64_t stride_lm, int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, void* dQ,
+                           void* dK, void* dV, int64_t stride_dqz, int64_t stride_dqh, int64_t stride_dqm,
+                           int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg, int64_t stride_dkn,
+                           int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg, int64_t stride_dvn,
+                           int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx, int window_size,
+                           int head_dim_qk, int head_dim_v, int dtype, void* workspace, size_t workspace_bytes,
+                           nsa_stream_t stream) {
+  NSA_BWD_IO
+  Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64};
+  return run_bwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
+                 (hipStream_t)stream);
+}
+
+int nsa_compression_fwd(const void* Q, const void* K, const void* V, const int32_t* Block_ends, void* Out,
+                        float sm_scale, float* L, float* M, int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                        int64_t stride_qk, int64_t stride_kz, int64_t stride_kg, int64_t stride_kn,
+                        int64_t stride_kk, int64_t stride_vz, int64_t stride_vg, int64_t stride_vn,
+                        int64_t stride_vk, int64_t stride_oz, int64_t stride_oh, int64_t stride_om,
+                        int64_t stride_ok, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm,
+                        int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, int Z, int H, int n_kv_groups,
+                        int n_ctx_q, int n_blocks, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
+                        size_t workspace_bytes, nsa_stream_t stream) {
+  NSA_FWD_IO
+  Shape s{kCompression, dtype, Z, H, n_kv_groups, n_ctx_q, n_blocks, head_dim_qk, head_dim_v, 0, 64};
+  if (n_blocks > 0 && !Block_ends) return fail(NSA_ERR_INVALID, "Block_ends is null");
+  return run_fwd(s, io, sm_scale, 0, Block_ends, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
+                 (hipStream_t)stream);
+}
+
+int nsa_compression_bwd(const void* Q, const void* K, const void* V, const int32_t* Block_ends, const void* Out,
+                        const void* dOut, float sm_scale, const float* L, const float* M, int64_t stride_qz,
+                        int64_t stride_qh, int64_t stride_qm, int64_t stride_qk, int64_t stride_kz,
+                        int64_t stride_kg, int64_t stride_kn, int64_t stride_kk, int64_t stride_vz,
+                        int64_t stride_vg, int64_t stride_vn, int64_t stride_vk, int64_t stride_oz,
+                        int64_t stride_oh, int64_t stride_om, int64_t stride_ok, int64_t stride_lz,
+                        int64_t stride_lh, int64_t stride_lm, int64_t stride_mz, int64_t stride_mh,
+                        int64_t stride_mm, void* dQ, void* dK, void* dV, int64_t stride_dqz, int64_t stride_dqh,
+                        int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg,
+                        int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
+                        int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
+                        int n_blocks, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
+                        size_t workspace_bytes, nsa_stream_t stream) {
+  NSA_BWD_IO
+  Shape s{kCompression, dtype, Z, H, n_kv_groups, n_ctx_q, n_blocks, head_dim_qk, head_dim_v, 0, 64};
+  if (n_blocks > 0 && !Block_ends) return fail(NSA_ERR_INVALID, "Block_ends is null");
+  return run_bwd(s, io, sm_scale, 0, Block_ends, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
+                 (hipStream_t)stream);
+}
+
+int nsa_sparse_selection_fwd(const void* Q, const void* K, const void* V, const void* Block_indices, void* Out,
+                             float sm_scale, float* L, float* M, int64_t stride_qz, int64_t stride_qh,
+                             int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
+                             int64_t stride_kn, int64_t stride_kk, int64_t stride_vz, int64_t stride_vg,
+                             int64_t stride_vn, int64_t stride_vk, int64_t stride_oz, int64_t stride_oh,
+                             int64_t stride_om, int64_t stride_ok, int64_t stride_bz, int64_t stride_bg,
+                             int64_t stride_bm, int64_t stride_bn, int64_t stride_lz, int64_t stride_lh,
+                             int64_t stride_lm, int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, int Z, int H,
+                             int n_kv_groups, int n_ctx_q, int n_ctx_kv, int n_slots, int block_size_selection,
+                             int is_causal, int index_is_int64, int all_invalid_fallback, int head_dim_qk,
+                             int head_dim_v, int dtype, void* workspace, size_t workspace_bytes,
+                             nsa_stream_t stream) {
+  NSA_FWD_IO
+  Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
+          block_size_selection};
+  if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
+  const int64_t sidx[4] = {stride_bz, stride_bg, stride_bm, stride_bn};
+  return run_fwd(s, io, sm_scale, 0, nullptr, Block_indices, sidx, index_is_int64, all_invalid_fallback,
+                 is_causal ? 1 : 0, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int nsa_sparse_selection_bwd(const void* Q, const void* K, const void* V, const void* Block_indices, const void* Out,
+                             const void* dOut, float sm_scale, const float* L, const float* M, int64_t stride_qz,
+                             int64_t stride_qh, int64_t stride_qm, int64_t stride_qk, int64_t stride_kz,
+                             int64_t stride_kg, int64_t stride_kn, int64_t stride_kk, int64_t stride_vz,
+                             int64_t stride_vg, int64_t stride_vn, int64_t stride_vk, int64_t stride_oz,
+                             int64_t stride_oh, int64_t stride_om, int64_t stride_ok, int64_t stride_bz,
+                             int64_t stride_bg, int64_t stride_bm, int64_t stride_bn, int64_t stride_lz,
+                             int64_t stride_lh, int64_t stride_lm, int64_t stride_mz, int64_t stride_mh,
+                             int64_t stride_mm, void* dQ, void* dK, void* dV, int64_t stride_dqz, int64_t stride_dqh,
+                             int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg,
+                             int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
+                             int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
+                             int n_ctx_kv, int n_slots, int block_size_selection, int is_causal, int index_is_int64,
+                             int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
+                             size_t workspace_bytes, nsa_stream_t stream) {
+  NSA_BWD_IO
+  Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
+          block_size_selection};
+  if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
+  const int64_t sidx[4] = {stride_bz, stride_bg, stride_bm, stride_bn};
+  return run_bwd(s, io, sm_scale, 0, nullptr, Block_indices, sidx, index_is_int64, all_invalid_fallback,
+                 is_causal ? 1 : 0, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+}  // extern "C"

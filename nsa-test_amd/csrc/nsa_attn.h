@@ -1,0 +1,80 @@
+// Shared argument blocks and launch helpers for the NSA attention kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nsa {
+
+enum Branch : int { kSliding = 0, kCompression = 1, kSelection = 2 };
+enum DType : int { kF32 = 0, kBF16 = 1 };
+
+// Columns handled by one forward / dQ workgroup (4 waves x NSUB x 16).
+constexpr int kFwdNSub = 2;
+constexpr int kFwdCols = 4 * kFwdNSub * 16;
+constexpr int kDqNSub = 1;
+constexpr int kDqCols = 4 * kDqNSub * 16;
+// Per-workgroup selection bookkeeping limits (timesteps x slots, distinct blocks).
+constexpr int kSelListMax = 2048;
+constexpr int kSelMaxBlocks = 4096;
+// Query rows staged per step of the dK/dV kernels.
+constexpr int kRowChunk = 32;
+// Timesteps per dK/dV work item for branches that split the query axis.
+constexpr int kSegT = 256;
+
+struct AttnArgs {
+  // queries [B,H,Tq,DK], unit stride on the feature axis
+  const void* q;
+  int64_t sq_b, sq_h, sq_t;
+  // group K/V re-packed by the prep kernel (compact, Tp rows, zero padded):
+  //   kt [B,G,Tp,DK]  kn [B,G,DK,Tp]  vt [B,G,DV,Tp]  vn [B,G,Tp,DV]
+  const void* kt;
+  const void* kn;
+  const void* vt;
+  const void* vn;
+  int Tp;
+  // forward outputs / backward inputs
+  void* o;
+  int64_t so_b, so_h, so_t;
+  float* L;
+  int64_t sl_b, sl_h, sl_t;
+  float* M;
+  int64_t sm_b, sm_h, sm_t;
+  // backward
+  const void* dout;
+  int64_t sdo_b, sdo_h, sdo_t;
+  void* dq;
+  int64_t sdq_b, sdq_h, sdq_t;
+  const float* lse2;   // [B,H,Tq] compact: (M+L)*log2(e), +inf for empty rows
+  const float* delta;  // [B,H,Tq] compact: rowsum(O*dO)
+  // dK/dV destination (accumulated into, any strides) or fp32 partials
+  void* dk;
+  int64_t sdk_b, sdk_g, sdk_t, sdk_d;
+  void* dv;
+  int64_t sdv_b, sdv_g, sdv_t, sdv_d;
+  float* partial;  // [items][64][DK+DV]
+  int items_per_bg;
+  // shapes
+  int B, H, G, hpg, Tq, Tkv;
+  float scale;
+  // branch parameters
+  int window;
+  const int* block_ends;  // [Tkv] int32 (compression)
+  const int* sel;         // cleaned selection [B,G,Tq,nslots] int32, ascending, -1 padded
+  int nslots;
+  int lprime;
+  int nblk;               // ceil(Tkv / lprime)
+  int causal;             // selection: mask keys after the query position
+  // selection CSR (backward)
+  const int* csr_off;     // [B,G,nblk+1]
+  const int* csr_t;       // [B,G,Tq*nslots] query timesteps per block, ascending
+  const int* seg_off;     // [B,G,nblk+1] work-item prefix per block
+};
+
+template <typename T, int DK, int DV, int BR>
+void launch_attn_fwd(const AttnArgs& a, hipStream_t s);
+template <typename T, int DK, int DV, int BR>
+void launch_attn_bwd_dq(const AttnArgs& a, hipStream_t s);
+template <typename T, int DK, int DV, int BR>
+void launch_attn_bwd_dkdv(const AttnArgs& a, hipStream_t s);
+
+}  // namespace nsa

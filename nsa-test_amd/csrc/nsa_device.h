@@ -1,0 +1,143 @@
+// Device-side building blocks shared by every NSA kernel on gfx950 (CDNA4).
+//
+// Matrix products run on 16x16 MFMA tiles:
+//   bf16: v_mfma_f32_16x16x32_bf16  (one 16-byte fragment per lane = 8 bf16 along K)
+//   fp32: v_mfma_f32_16x16x4_f32    (one 16-byte fragment per lane = 4 fp32 along K,
+//                                     issued as 4 MFMAs)
+// Operand convention: lane l supplies row/column (l & 15) and the K-slot group
+// g = l >> 4.  Which physical k a (g, slot) pair stands for is free as long as the
+// A and B operands agree, so every product below picks the k-assignment that makes
+// its loads contiguous.  The accumulator layout is fixed by the hardware:
+//   C[row = 4*g + i][col = l & 15]  for i = 0..3.
+// A C tile therefore feeds straight into a later product as the K-side operand when
+// the other operand uses the "C-permuted" k-assignment (see frag_cperm_*).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nsa {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct bf16 {  // storage-only tag type for the template parameter
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+// round-to-nearest-even float -> bf16 bits (NaN kept quiet)
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static constexpr int kPerFrag = 4;   // elements in one 16-byte fragment
+  static constexpr int kKChunk = 16;   // K covered by one fragment across 4 lane groups
+  __device__ static float to_f32(float v) { return v; }
+  __device__ static float from_f32(float v) { return v; }
+};
+template <> struct Elem<bf16> {
+  static constexpr int kPerFrag = 8;
+  static constexpr int kKChunk = 32;
+  __device__ static float to_f32(uint16_t v) { return bf16_bits_to_f32(v); }
+  __device__ static uint16_t from_f32(float v) { return f32_to_bf16_bits(v); }
+};
+
+// storage type of an element
+template <typename T> struct Store { typedef T type; };
+template <> struct Store<bf16> { typedef uint16_t type; };
+
+// One K-chunk product: acc += A_frag * B_frag over kKChunk k values.
+template <typename T> struct Mma;
+template <> struct Mma<bf16> {
+  __device__ __forceinline__ static f32x4 run(f32x4 acc, uint4 a, uint4 b) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+  }
+};
+template <> struct Mma<float> {
+  __device__ __forceinline__ static f32x4 run(f32x4 acc, uint4 a, uint4 b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
+    return acc;
+  }
+};
+
+// Keys (the reduction dimension of a P*V-type product) covered by one C-derived
+// fragment: two C tiles for bf16 (32 keys), one C tile for fp32 (16 keys).
+template <typename T> struct CFrag;
+template <> struct CFrag<float> {
+  static constexpr int kKeys = 16;
+  // c0 holds C rows 4g+i of a 16-row tile: used as-is.
+  __device__ __forceinline__ static uint4 pack(f32x4 c0, f32x4 /*c1*/) {
+    return make_uint4(__float_as_uint(c0[0]), __float_as_uint(c0[1]), __float_as_uint(c0[2]),
+                      __float_as_uint(c0[3]));
+  }
+};
+template <> struct CFrag<bf16> {
+  static constexpr int kKeys = 32;
+  // slots 0..3 <- tile c0 rows 4g+i ; slots 4..7 <- tile c1 rows 16+4g+i
+  __device__ __forceinline__ static uint4 pack(f32x4 c0, f32x4 c1) {
+    uint32_t w0 = (uint32_t)f32_to_bf16_bits(c0[0]) | ((uint32_t)f32_to_bf16_bits(c0[1]) << 16);
+    uint32_t w1 = (uint32_t)f32_to_bf16_bits(c0[2]) | ((uint32_t)f32_to_bf16_bits(c0[3]) << 16);
+    uint32_t w2 = (uint32_t)f32_to_bf16_bits(c1[0]) | ((uint32_t)f32_to_bf16_bits(c1[1]) << 16);
+    uint32_t w3 = (uint32_t)f32_to_bf16_bits(c1[2]) | ((uint32_t)f32_to_bf16_bits(c1[3]) << 16);
+    return make_uint4(w0, w1, w2, w3);
+  }
+};
+
+// Load the "C-permuted" fragment of a row-major [rows][keys] array whose K axis is
+// the key axis: matches CFrag<T>::pack.  `row` points at the first key of the chunk.
+template <typename T> __device__ __forceinline__ uint4 frag_cperm(const typename Store<T>::type* row, int g);
+template <> __device__ __forceinline__ uint4 frag_cperm<float>(const float* row, int g) {
+  return *reinterpret_cast<const uint4*>(row + 4 * g);
+}
+template <> __device__ __forceinline__ uint4 frag_cperm<bf16>(const uint16_t* row, int g) {
+  uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * g);
+  uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * g);
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
+// Standard fragment: 16 contiguous bytes at row[kchunk_base + g * kPerFrag].
+template <typename T>
+__device__ __forceinline__ uint4 frag_std(const typename Store<T>::type* row, int g) {
+  return *reinterpret_cast<const uint4*>(row + g * Elem<T>::kPerFrag);
+}
+
+__device__ __forceinline__ float wave_max16(float v) {  // over lanes sharing (l & 15)
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float wave_sum16(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Store 4 consecutive values (one C-tile column slice) as T.
+template <typename T> __device__ __forceinline__ void store4(typename Store<T>::type* p, f32x4 v);
+template <> __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+template <> __device__ __forceinline__ void store4<bf16>(uint16_t* p, f32x4 v) {
+  uint32_t w0 = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
+  uint32_t w1 = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
+  *reinterpret_cast<uint2*>(p) = make_uint2(w0, w1);
+}
+
+}  // namespace nsa

@@ -1,0 +1,32 @@
+// Host-side launchers behind the C ABI (internal, not exported).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include "nsa_attn.h"
+
+// Head-dimension pairs (DK, DV) with compiled kernels.  Other widths are served by
+// zero-padding to the next pair in the host shim (padding q/k columns with zeros
+// leaves q.k unchanged; padded v columns are dropped).
+#define NSA_HEAD_DIMS(X) X(32, 32) X(64, 64) X(128, 128) X(192, 128)
+
+namespace nsa {
+
+void launch_repack(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t s_r, int64_t s_c, int B, int G,
+                   int R, int C, int Rp, void* rowm, void* colm, hipStream_t st);
+void launch_bwd_rowstats(int dtype, const AttnArgs& a, int DV, hipStream_t st);
+
+// return false when (dtype, dk, dv, branch) has no compiled kernel
+bool dispatch_attn_fwd(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
+bool dispatch_attn_bwd_dq(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
+bool dispatch_attn_bwd_dkdv(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
+void launch_partial_reduce(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
+
+// selection index cleaning and block -> query CSR
+void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g, int64_t si_t, int64_t si_n, int B,
+                      int G, int Tq, int n_in, int nslots, int lprime, int Tkv, int fallback, int causal, int* clean,
+                      int* chunk_cnt, int nblk, hipStream_t st);
+void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int nslots, int nblk, int* csr_off,
+                    int* csr_t, int* seg_off, hipStream_t st);
+int sel_csr_chunks(int Tq);
+
+}  // namespace nsa

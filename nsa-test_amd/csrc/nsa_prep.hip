@@ -1,0 +1,105 @@
+// Layout preparation kernels: re-pack the per-group K/V operands into the compact,
+// zero-padded layouts the attention kernels stage from, and the per-row backward
+// statistics.  All of these are HBM streams over group-sized (not head-sized)
+// tensors, except bwd_rowstats which reads O and dO once.
+#include "nsa_attn.h"
+#include "nsa_device.h"
+#include "nsa_kernels.h"
+
+namespace nsa {
+
+// Source matrix per (b,g): element (r, c) at src + b*s_b + g*s_g + r*s_r + c*s_c,
+// r < R (time), c < C (feature).  Writes, for r < Rp (rows >= R zero-filled):
+//   rowm[bg][r][c]  (if non-null)     colm[bg][c][r]  (if non-null)
+template <typename S>
+__global__ __launch_bounds__(256) void repack_kernel(const S* __restrict__ src, int64_t s_b, int64_t s_g,
+                                                     int64_t s_r, int64_t s_c, int G, int R, int C, int Rp,
+                                                     S* __restrict__ rowm, S* __restrict__ colm) {
+  __shared__ S tile[64][65];
+  const int bg = blockIdx.z;
+  const int b = bg / G, g = bg % G;
+  const int r0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
+  const S* base = src + b * s_b + g * s_g;
+  const int tid = threadIdx.x;
+  // read: walk along whichever source axis is contiguous
+  const bool r_fast = s_r == 1;
+  for (int i = tid; i < 64 * 64; i += 256) {
+    const int rr = r_fast ? (i & 63) : (i >> 6);
+    const int cc = r_fast ? (i >> 6) : (i & 63);
+    const int r = r0 + rr, c = c0 + cc;
+    S v;
+    if (r < R && c < C) {
+      v = base[r * s_r + c * s_c];
+    } else {
+      v = S(0);
+    }
+    tile[rr][cc] = v;
+  }
+  __syncthreads();
+  const int64_t obase = (int64_t)bg * Rp * C;
+  if (rowm) {
+    for (int i = tid; i < 64 * 64; i += 256) {
+      const int rr = i >> 6, cc = i & 63;
+      const int r = r0 + rr, c = c0 + cc;
+      if (r < Rp && c < C) rowm[obase + (int64_t)r * C + c] = tile[rr][cc];
+    }
+  }
+  if (colm) {
+    for (int i = tid; i < 64 * 64; i += 256) {
+      const int cc = i >> 6, rr = i & 63;
+      const int r = r0 + rr, c = c0 + cc;
+      if (r < Rp && c < C) colm[obase + (int64_t)c * Rp + r] = tile[rr][cc];
+    }
+  }
+}
+
+void launch_repack(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t s_r, int64_t s_c, int B, int G,
+                   int R, int C, int Rp, void* rowm, void* colm, hipStream_t st) {
+  dim3 grid((Rp + 63) / 64, (C + 63) / 64, B * G);
+  if (dtype == kF32) {
+    hipLaunchKernelGGL(repack_kernel<float>, grid, dim3(256), 0, st, (const float*)src, s_b, s_g, s_r, s_c, G, R, C,
+                       Rp, (float*)rowm, (float*)colm);
+  } else {
+    hipLaunchKernelGGL(repack_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, s_b, s_g, s_r, s_c, G,
+                       R, C, Rp, (uint16_t*)rowm, (uint16_t*)colm);
+  }
+}
+
+// Backward row statistics: delta = sum_d O*dO (fp32) and lse2 = (M+L)*log2(e)
+// (+inf when L = -inf, i.e. the row saw no key: every probability is then 0).
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_rowstats_kernel(AttnArgs a, int DV) {
+  using S = typename Store<T>::type;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;  // flattened (b, h, t)
+  const int64_t nrows = (int64_t)a.B * a.H * a.Tq;
+  if (row >= nrows) return;
+  const int t = row % a.Tq;
+  const int h = (row / a.Tq) % a.H;
+  const int b = row / ((int64_t)a.Tq * a.H);
+  const S* o = reinterpret_cast<const S*>(a.o) + b * a.so_b + h * a.so_h + (int64_t)t * a.so_t;
+  const S* d = reinterpret_cast<const S*>(a.dout) + b * a.sdo_b + h * a.sdo_h + (int64_t)t * a.sdo_t;
+  float acc = 0.f;
+  for (int j = lane; j < DV; j += 64) acc += Elem<T>::to_f32(o[j]) * Elem<T>::to_f32(d[j]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+  if (lane == 0) {
+    float* delta = const_cast<float*>(a.delta);
+    float* lse2 = const_cast<float*>(a.lse2);
+    delta[row] = acc;
+    const float L = a.L[b * a.sl_b + h * a.sl_h + (int64_t)t * a.sl_t];
+    const float M = a.M[b * a.sm_b + h * a.sm_h + (int64_t)t * a.sm_t];
+    lse2[row] = (L == -INFINITY) ? INFINITY : (M + L) * kLog2e;
+  }
+}
+
+void launch_bwd_rowstats(int dtype, const AttnArgs& a, int DV, hipStream_t st) {
+  const int64_t nrows = (int64_t)a.B * a.H * a.Tq;
+  dim3 grid((unsigned)((nrows + 3) / 4));
+  if (dtype == kF32)
+    hipLaunchKernelGGL(bwd_rowstats_kernel<float>, grid, dim3(256), 0, st, a, DV);
+  else
+    hipLaunchKernelGGL(bwd_rowstats_kernel<bf16>, grid, dim3(256), 0, st, a, DV);
+}
+
+}  // namespace nsa

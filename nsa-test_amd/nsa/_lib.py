@@ -1,0 +1,107 @@
+"""ctypes binding of libnsa_hip.so (the C ABI declared in include/nsa_hip.h).
+
+The library is loaded lazily on first use.  There is no other implementation of
+these operators: if the shared library is missing or cannot be loaded, every call
+raises instead of falling back to anything.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libnsa_hip.so")
+ABI_VERSION = 1
+
+NSA_F32 = 0
+NSA_BF16 = 1
+
+NSA_OK = 0
+NSA_ERR_INVALID = 1
+NSA_ERR_UNSUPPORTED = 2
+NSA_ERR_LAYOUT = 3
+NSA_ERR_WORKSPACE = 4
+NSA_ERR_HIP = 5
+
+_P, _F, _I, _L, _Z = c_void_p, c_float, c_int, c_int64, c_size_t
+
+# name -> (restype, argtypes) for every exported symbol
+_S22 = [_L] * 22
+_S26 = [_L] * 26
+_S12 = [_L] * 12
+SIGNATURES = {
+    "nsa_abi_version": (_I, []),
+    "nsa_last_error": (ctypes.c_char_p, []),
+    "nsa_head_dims_supported": (_I, [_I, _I, _I]),
+    "nsa_fwd_workspace_size": (_Z, [_I] * 11),
+    "nsa_bwd_workspace_size": (_Z, [_I] * 11),
+    "nsa_sliding_window_fwd": (_I, [_P, _P, _P, _P, _F, _P, _P, *_S22, *[_I] * 7, _I, _P, _Z, _P]),
+    "nsa_sliding_window_bwd": (
+        _I, [_P, _P, _P, _P, _P, _F, _P, _P, *_S22, _P, _P, _P, *_S12, *[_I] * 7, _I, _P, _Z, _P]),
+    "nsa_compression_fwd": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, *_S22, *[_I] * 7, _I, _P, _Z, _P]),
+    "nsa_compression_bwd": (
+        _I, [_P, _P, _P, _P, _P, _P, _F, _P, _P, *_S22, _P, _P, _P, *_S12, *[_I] * 7, _I, _P, _Z, _P]),
+    "nsa_sparse_selection_fwd": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, *_S26, *[_I] * 12, _I, _P, _Z, _P]),
+    "nsa_sparse_selection_bwd": (
+        _I, [_P, _P, _P, _P, _P, _P, _F, _P, _P, *_S26, _P, _P, _P, *_S12, *[_I] * 12, _I, _P, _Z, _P]),
+    "nsa_score_topn": (_I, [_P, _P, _P, _P, _P, _P, *[_L] * 12, *[_I] * 13, _F, _P, _Z, _P]),
+    "nsa_score_topn_workspace_size": (_Z, [_I] * 7),
+    "nsa_compress_pool_fwd": (_I, [_P, _P, _P, _P, _P, *[_L] * 8, *[_I] * 8, _P]),
+    "nsa_compress_pool_bwd": (_I, [_P, _P, _P, _P, _P, _P, *[_L] * 4, *[_I] * 8, _P]),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+class NSAKernelError(RuntimeError):
+    """A libnsa_hip.so entry point returned an error code."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed (code {code}): {msg}")
+        self.code = code
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it first (python -c 'import __graft_entry__ as g; g.build()' "
+                f"or python nsa-test_amd/nsa/_build.py)")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name, None)
+            if fn is None:
+                continue
+            fn.restype = res
+            fn.argtypes = args
+        ver = lib.nsa_abi_version()
+        if ver != ABI_VERSION:
+            raise RuntimeError(f"libnsa_hip.so ABI {ver}, expected {ABI_VERSION}: rebuild it")
+        _lib = lib
+        return lib
+
+
+def exported_symbols() -> list[str]:
+    """Symbols of SIGNATURES that the loaded library exports."""
+    lib = load()
+    return [n for n in SIGNATURES if hasattr(lib, n)]
+
+
+def call(name: str, *args) -> None:
+    lib = load()
+    fn = getattr(lib, name)
+    rc = fn(*args)
+    if rc != NSA_OK:
+        msg = lib.nsa_last_error().decode(errors="replace")
+        raise NSAKernelError(name, rc, msg)
+
+
+def size(name: str, *args) -> int:
+    return int(getattr(load(), name)(*args))

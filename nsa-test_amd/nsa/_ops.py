@@ -1,0 +1,194 @@
+"""Tensor-level wrappers over the C ABI of libnsa_hip.so.
+
+All tensors are *logical views* with the reference's meaning:
+    q      [Z, H, Tq, dk]          out / dO / dq  [Z, H, Tq, dv|dk]
+    k      [Z, G, Tkv, dk]  (the (z, g, time, dk) view of a [B, G, dk, T] tensor)
+    v      [Z, G, Tkv, dv]          dk / dv        [Z, G, Tkv, dk|dv]
+    L, M   [Z, H, Tq] fp32
+Views may have any strides; the library honours them where it can, and this module
+supplies compact copies where the kernels need unit-stride rows (Q, Out, dO, dQ).
+Head widths without a compiled kernel are zero-padded to the next compiled pair.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib
+
+SLIDING, COMPRESSION, SELECTION = 0, 1, 2
+HEAD_DIM_PAIRS = ((32, 32), (64, 64), (128, 128), (192, 128))
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    return _lib.NSA_F32 if dt == torch.float32 else _lib.NSA_BF16
+
+
+def compute_dtype(dt: torch.dtype) -> torch.dtype:
+    """Element type the kernels run in for inputs of dtype `dt`."""
+    return dt if dt in (torch.float32, torch.bfloat16) else torch.float32
+
+
+def kernel_dims(dk: int, dv: int) -> tuple[int, int]:
+    for a, b in HEAD_DIM_PAIRS:
+        if a >= dk and b >= dv:
+            return a, b
+    raise ValueError(f"head dims dk={dk} dv={dv} exceed the largest compiled pair {HEAD_DIM_PAIRS[-1]}")
+
+
+def _rows_ok(t: torch.Tensor) -> bool:
+    es = t.element_size()
+    if t.stride(-1) != 1 and t.shape[-1] > 1:
+        return False
+    if t.data_ptr() % 16:
+        return False
+    return all((s * es) % 16 == 0 for s in t.stride()[:-1])
+
+
+def _rows(t: torch.Tensor) -> torch.Tensor:
+    return t if _rows_ok(t) else t.contiguous()
+
+
+def _pad_last(t: torch.Tensor, width: int) -> torch.Tensor:
+    return t if t.shape[-1] == width else F.pad(t, (0, width - t.shape[-1]))
+
+
+def _stream(dev: torch.device) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _check_device(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("NSA kernels run on the GPU only: got a tensor on " + str(t.device))
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _branch_extra(branch, Tkv, block_ends, indices, lprime):
+    """(n_ctx_kv_or_blocks, n_slots, lprime) for the workspace query."""
+    if branch == SELECTION:
+        return indices.shape[-1], lprime
+    return 0, 64
+
+
+def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=None, indices=None,
+             lprime: int = 64, causal: bool = True, fallback: bool = False, out=None, L=None, M=None):
+    """Forward of one NSA branch.  Returns (out, L, M); `out`, `L`, `M` are written in
+    place when given (with their own strides)."""
+    _check_device(q, k, v, block_ends, indices, out, L, M)
+    Z, H, Tq, dk = q.shape
+    G, Tkv = k.shape[1], k.shape[2]
+    dv = v.shape[-1]
+    dev = q.device
+    cdt = compute_dtype(q.dtype)
+    DK, DV = kernel_dims(dk, dv)
+    qk = _rows(_pad_last(q.to(cdt), DK))
+    kk = _pad_last(k.to(cdt), DK)
+    vk = _pad_last(v.to(cdt), DV)
+    direct_out = out is not None and out.dtype == cdt and dv == DV and _rows_ok(out)
+    o = out if direct_out else torch.empty(Z, H, Tq, DV, device=dev, dtype=cdt)
+    Lk = L if L is not None else torch.empty(Z, H, Tq, device=dev, dtype=torch.float32)
+    Mk = M if M is not None else torch.empty(Z, H, Tq, device=dev, dtype=torch.float32)
+    n_slots = indices.shape[-1] if branch == SELECTION else 0
+    ws_bytes = _lib.size("nsa_fwd_workspace_size", branch, _dtype_code(cdt), Z, H, G, Tq, Tkv, DK, DV, n_slots,
+                         lprime)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    dt = _dtype_code(cdt)
+    common_strides = [*qk.stride(), *kk.stride(), *vk.stride(), *o.stride()]
+    lm_strides = [*Lk.stride(), *Mk.stride()]
+    st = _stream(dev)
+    if branch == SLIDING:
+        _lib.call("nsa_sliding_window_fwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(o), float(scale), _ptr(Lk), _ptr(Mk),
+                  *common_strides, *lm_strides, Z, H, G, Tq, int(window), DK, DV, dt, _ptr(ws), ws.numel(), st)
+    elif branch == COMPRESSION:
+        be = block_ends.to(torch.int32).contiguous()
+        _lib.call("nsa_compression_fwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(be), _ptr(o), float(scale), _ptr(Lk),
+                  _ptr(Mk), *common_strides, *lm_strides, Z, H, G, Tq, Tkv, DK, DV, dt, _ptr(ws), ws.numel(), st)
+    else:
+        idx = indices if indices.dtype in (torch.int32, torch.int64) else indices.to(torch.int64)
+        _lib.call("nsa_sparse_selection_fwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(idx), _ptr(o), float(scale),
+                  _ptr(Lk), _ptr(Mk), *common_strides, *idx.stride(), *lm_strides, Z, H, G, Tq, Tkv, n_slots,
+                  int(lprime), int(bool(causal)), int(idx.dtype == torch.int64), int(bool(fallback)), DK, DV, dt,
+                  _ptr(ws), ws.numel(), st)
+    if direct_out:
+        return o, Lk, Mk
+    res = o[..., :dv]
+    if out is not None:
+        out.copy_(res)
+        return out, Lk, Mk
+    return (res if q.dtype == cdt else res.to(q.dtype)), Lk, Mk
+
+
+def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0, block_ends=None, indices=None,
+             lprime: int = 64, causal: bool = True, fallback: bool = False, dq=None, dk=None, dv=None):
+    """Backward of one NSA branch.  dq is overwritten, dk / dv ([Z,G,Tkv,*] logical
+    views) are accumulated into (allocated zeroed when not given).  Returns (dq, dk, dv)."""
+    _check_device(q, k, v, o, do, L, M, block_ends, indices, dq, dk, dv)
+    Z, H, Tq, dkw = q.shape
+    G, Tkv = k.shape[1], k.shape[2]
+    dvw = v.shape[-1]
+    dev = q.device
+    cdt = compute_dtype(q.dtype)
+    DK, DV = kernel_dims(dkw, dvw)
+    qk = _rows(_pad_last(q.to(cdt), DK))
+    kk = _pad_last(k.to(cdt), DK)
+    vk = _pad_last(v.to(cdt), DV)
+    # O and dO are read with one set of strides (as the reference kernels do)
+    ok = _pad_last(o.to(cdt), DV).contiguous()
+    dok = _pad_last(do.to(cdt), DV).contiguous()
+    Lf = L.to(torch.float32)
+    Mf = M.to(torch.float32)
+    direct_dq = dq is not None and dq.dtype == cdt and dkw == DK and _rows_ok(dq)
+    dqk = dq if direct_dq else torch.empty(Z, H, Tq, DK, device=dev, dtype=cdt)
+    direct_dk = dk is not None and dk.dtype == cdt and dkw == DK
+    direct_dv = dv is not None and dv.dtype == cdt and dvw == DV
+    dkk = dk if direct_dk else torch.zeros(Z, G, Tkv, DK, device=dev, dtype=cdt)
+    dvk = dv if direct_dv else torch.zeros(Z, G, Tkv, DV, device=dev, dtype=cdt)
+    n_slots = indices.shape[-1] if branch == SELECTION else 0
+    ws_bytes = _lib.size("nsa_bwd_workspace_size", branch, _dtype_code(cdt), Z, H, G, Tq, Tkv, DK, DV, n_slots,
+                         lprime)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    dt = _dtype_code(cdt)
+    st = _stream(dev)
+    s_main = [*qk.stride(), *kk.stride(), *vk.stride(), *ok.stride()]
+    s_lm = [*Lf.stride(), *Mf.stride()]
+    s_grad = [*dqk.stride(), *dkk.stride(), *dvk.stride()]
+    if branch == SLIDING:
+        _lib.call("nsa_sliding_window_bwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(ok), _ptr(dok), float(scale),
+                  _ptr(Lf), _ptr(Mf), *s_main, *s_lm, _ptr(dqk), _ptr(dkk), _ptr(dvk), *s_grad, Z, H, G, Tq,
+                  int(window), DK, DV, dt, _ptr(ws), ws.numel(), st)
+    elif branch == COMPRESSION:
+        be = block_ends.to(torch.int32).contiguous()
+        _lib.call("nsa_compression_bwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(be), _ptr(ok), _ptr(dok), float(scale),
+                  _ptr(Lf), _ptr(Mf), *s_main, *s_lm, _ptr(dqk), _ptr(dkk), _ptr(dvk), *s_grad, Z, H, G, Tq, Tkv,
+                  DK, DV, dt, _ptr(ws), ws.numel(), st)
+    else:
+        idx = indices if indices.dtype in (torch.int32, torch.int64) else indices.to(torch.int64)
+        _lib.call("nsa_sparse_selection_bwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(idx), _ptr(ok), _ptr(dok),
+                  float(scale), _ptr(Lf), _ptr(Mf), *s_main, *idx.stride(), *s_lm, _ptr(dqk), _ptr(dkk), _ptr(dvk),
+                  *s_grad, Z, H, G, Tq, Tkv, n_slots, int(lprime), int(bool(causal)), int(idx.dtype == torch.int64),
+                  int(bool(fallback)), DK, DV, dt, _ptr(ws), ws.numel(), st)
+    if not direct_dq:
+        r = dqk[..., :dkw]
+        if dq is not None:
+            dq.copy_(r)
+        else:
+            dq = r if q.dtype == cdt else r.to(q.dtype)
+    if not direct_dk:
+        r = dkk[..., :dkw]
+        if dk is not None:
+            dk.add_(r.to(dk.dtype))
+        else:
+            dk = r if q.dtype == cdt else r.to(q.dtype)
+    if not direct_dv:
+        r = dvk[..., :dvw]
+        if dv is not None:
+            dv.add_(r.to(dv.dtype))
+        else:
+            dv = r if q.dtype == cdt else r.to(q.dtype)
+    return dq, dk, dv
