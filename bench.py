@@ -1,0 +1,307 @@
+#!/usr/bin/env python3
+"""NSA fwd+bwd throughput on one MI355X (BASELINE.json metric).
+
+One step = one forward + backward pass of the NSA attention core at the paper
+configuration (B=1, H=64, G=4, T=8192, dk=192, dv=128, bf16):
+compress_tokens (MLP pooling of K, mean pooling of V), the fused Eq. 8 -> 10 top-n
+selection (l=32, d=16, l'=64, n=16 with 3 fixed blocks), the compression / selection /
+sliding-window (w=512) HIP attention branches, the sigmoid-gated mix, and the backward
+of all of it.  Inputs (q, k, v, dO ~ N(0,1)/sqrt(d), gate logits, N(0,0.02) MLP
+weights) are synthetic and resident in HBM before the timed region.
+
+The JSON line also carries the long-context configuration (T=32768, configs[3]) as
+`secondary`, a per-kernel breakdown, the roofline of the dominant kernel (timed with
+HIP events inside the timed region) and a CPU baseline (the C oracle, one core, on a
+sample of query rows, extrapolated linearly: each row's work is independent).
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (str(ROOT / "nsa-test_amd"), str(ROOT)):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    "paper": dict(B=1, H=64, G=4, T=8192, dk=192, dv=128, w=512, n=16, lowrank=False),
+    "long": dict(B=1, H=32, G=2, T=32768, dk=128, dv=128, w=512, n=16, lowrank=True),
+}
+
+KERNELS = {  # id -> name
+    0: "fwd_sliding", 1: "fwd_compression", 2: "fwd_selection",
+    3: "dq_sliding", 4: "dq_compression", 5: "dq_selection",
+    6: "dkdv_sliding", 7: "dkdv_compression", 8: "dkdv_selection",
+    9: "dkdv_reduce", 10: "score_topn", 11: "pool_fwd", 12: "pool_bwd",
+}
+
+
+def make_workload(name, dev, seed=0):
+    import torch
+    from nsa import NSAAttention, NSAConfig
+
+    c = CONFIGS[name]
+    B, H, G, T, dk, dv = c["B"], c["H"], c["G"], c["T"], c["dk"], c["dv"]
+    cfg = NSAConfig(d_model=256, head_dim_qk=dk, head_dim_v=dv, n_heads=H, n_kv_groups=G, l=32, d=16, l_prime=64,
+                    n=c["n"], w=c["w"])
+    g = torch.Generator(device=dev).manual_seed(seed)
+    bf = torch.bfloat16
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, device=dev, generator=g) * scale).to(bf)
+
+    if c["lowrank"]:
+        # low-rank (rank 8) component shared by all heads makes block scores peaked
+        basis = torch.randn(T, 8, device=dev, generator=g)
+        pq = torch.randn(8, dk, device=dev, generator=g)
+        pk = torch.randn(8, dk, device=dev, generator=g)
+        q = (torch.randn(B, H, T, dk, device=dev, generator=g) + basis @ pq).to(bf)
+        kk = [(torch.randn(B, G, T, dk, device=dev, generator=g) + basis @ pk).to(bf) for _ in range(3)]
+    else:
+        q = rnd(B, H, T, dk, scale=1 / math.sqrt(dk))
+        kk = [rnd(B, G, T, dk, scale=1 / math.sqrt(dk)) for _ in range(3)]
+    vv = [rnd(B, G, T, dv, scale=1 / math.sqrt(dv)) for _ in range(3)]
+    mod = NSAAttention(cfg)
+    with torch.no_grad():
+        for p in mod.compress_mlp.parameters():
+            p.normal_(0.0, 0.02)
+        mod.pos_embed.weight.normal_(0.0, 0.02)
+    mod = mod.to(dev, bf)
+    w = {
+        "q": q.requires_grad_(),
+        # reference layouts: selection / sliding K as [B,G,dk,T] (transposed views)
+        "k_cmp_in": kk[0].requires_grad_(), "v_cmp_in": vv[0].requires_grad_(),
+        "k_sel": kk[1].requires_grad_(), "v_sel": vv[1].requires_grad_(),
+        "k_win": kk[2].requires_grad_(), "v_win": vv[2].requires_grad_(),
+        "gate_logits": rnd(B, H, T, 3).requires_grad_(),
+        "dO": rnd(B, H, T, dv, scale=1 / math.sqrt(dv)),
+    }
+    return cfg, mod, w
+
+
+def nsa_step(cfg, mod, w, backward=True):
+    """One NSA forward (+ backward): every kernel of the hot path runs once."""
+    import torch
+    from nsa import CompressionAttention, SelectionAttention, SlidingWindowAttention, score_and_select
+
+    scale = 1.0 / math.sqrt(cfg.head_dim_qk)
+    q = w["q"]
+    kc, vc, be, _ = mod.compress_tokens(w["k_cmp_in"], w["v_cmp_in"])
+    with torch.no_grad():
+        idx = score_and_select(q.detach(), kc.detach(), be, scale, cfg)
+    o_c = CompressionAttention.apply(q, kc, vc, be, scale, cfg)
+    o_s = SelectionAttention.apply(q, w["k_sel"].transpose(-1, -2), w["v_sel"], idx, scale, cfg)
+    o_w = SlidingWindowAttention.apply(q, w["k_win"].transpose(-1, -2), w["v_win"], scale, cfg.w, cfg)
+    gt = torch.sigmoid(w["gate_logits"])
+    o = o_c * gt[..., 0:1] + o_s * gt[..., 1:2] + o_w * gt[..., 2:3]
+    if backward:
+        o.backward(w["dO"])
+        for t in list(w.values()) + list(mod.parameters()):
+            t.grad = None
+    return idx, be
+
+
+def valid_pairs(cfg, idx, be, T, B, H):
+    """(sliding, compression, selection) valid (query, key) pairs summed over heads."""
+    import torch
+
+    t = torch.arange(T, device=idx.device)
+    p_w = int(torch.clamp(t + 1, max=cfg.w).sum()) * B * H
+    n_act = int((be < 999999).sum())
+    bends = torch.arange(n_act, device=idx.device) * cfg.d + cfg.l - 1
+    p_c = int((bends.view(1, -1) <= t.view(-1, 1)).sum()) * B * H
+    lp = cfg.l_prime
+    st = idx * lp
+    keys = torch.clamp(torch.minimum(st + lp, t.view(1, 1, -1, 1) + 1) - st, min=0)
+    keys = torch.where(idx >= 0, keys, torch.zeros_like(keys))
+    p_s = int(keys.sum()) * cfg.heads_per_group
+    return p_w, p_c, p_s
+
+
+def kernel_flops(cfg, pairs):
+    """Algorithmic FLOPs per launch of each attention kernel.  Per valid pair:
+    forward 2(dk+dv); backward 2(3dk+2dv), attributed 2(2dk+2dv) to the dK/dV kernel
+    (S and dP recomputed, dK, dV) and 2dk to the dQ kernel (the dQ product)."""
+    dk, dv = cfg.head_dim_qk, cfg.head_dim_v
+    out = {}
+    for br, p in enumerate(pairs):
+        out[br] = 2 * (dk + dv) * p
+        out[3 + br] = 2 * dk * p
+        out[6 + br] = 2 * (2 * dk + 2 * dv) * p
+    return out
+
+
+def time_steps(cfg, mod, w, steps, warmup, backward=True):
+    import torch
+
+    for _ in range(warmup):
+        nsa_step(cfg, mod, w, backward)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        nsa_step(cfg, mod, w, backward)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def kernel_breakdown(cfg, mod, w):
+    """Device ms per launch of every kernel, one instrumented step per kernel id."""
+    import torch
+    from nsa import _lib
+
+    res = {}
+    for kid, name in KERNELS.items():
+        with _lib.KernelTimer(kid) as tm:
+            nsa_step(cfg, mod, w)
+        torch.cuda.synchronize()
+        if tm.launches:
+            res[name] = {"ms": round(tm.ms / tm.launches, 4), "launches": tm.launches}
+    return res
+
+
+def cpu_baseline(name, samples, seed=0):
+    """The C oracle (one core) on `samples` query timesteps of one KV group plus
+    compress_tokens of that group; extrapolated to the whole workload."""
+    import numpy as np
+    import torch
+
+    import oracle
+    from nsa import NSAConfig
+
+    c = CONFIGS[name]
+    B, H, G, T, dk, dv = c["B"], c["H"], c["G"], c["T"], c["dk"], c["dv"]
+    hpg = H // G
+    rng = np.random.default_rng(seed)
+    cfg = NSAConfig(head_dim_qk=dk, head_dim_v=dv, n_heads=hpg, n_kv_groups=1, n=c["n"], w=c["w"])
+    scale = 1 / math.sqrt(dk)
+    rows = np.sort(rng.choice(T, size=samples, replace=False)).astype(np.int32)
+    q = (rng.standard_normal((1, hpg, samples, dk)) / math.sqrt(dk)).astype(np.float32)
+    k = [(rng.standard_normal((1, 1, T, dk)) / math.sqrt(dk)).astype(np.float32) for _ in range(3)]
+    v = [(rng.standard_normal((1, 1, T, dv)) / math.sqrt(dv)).astype(np.float32) for _ in range(3)]
+    do = (rng.standard_normal((1, hpg, samples, dv)) / math.sqrt(dv)).astype(np.float32)
+    w1 = rng.standard_normal((2 * dk, dk + cfg.l)) * 0.02
+    w2 = rng.standard_normal((dk, 2 * dk)) * 0.02
+    pe = rng.standard_normal((cfg.l, cfg.l)) * 0.02
+    t0 = time.perf_counter()
+    kc, vc, be, _ = oracle.compress_tokens(k[0], v[0], w1, np.zeros(2 * dk), w2, np.zeros(dk), pe, cfg.l, cfg.d)
+    t_group = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    idx = oracle.score_topn(q, kc.astype(np.float32), be, np.float32(scale), l=cfg.l, d=cfg.d, lprime=cfg.l_prime,
+                            n=cfg.n, positions=rows)
+    kct = kc.transpose(0, 1, 3, 2)
+    oracle.attn_fwd(oracle.COMPRESSION, q, kct, vc, scale, block_ends=be, positions=rows)
+    oracle.attn_bwd(oracle.COMPRESSION, q, kct, vc, do, scale, block_ends=be, positions=rows)
+    oracle.attn_fwd(oracle.SELECTION, q, k[1], v[1], scale, indices=idx, lprime=cfg.l_prime, positions=rows)
+    oracle.attn_bwd(oracle.SELECTION, q, k[1], v[1], do, scale, indices=idx, lprime=cfg.l_prime, positions=rows)
+    oracle.attn_fwd(oracle.SLIDING, q, k[2], v[2], scale, window=cfg.w, positions=rows)
+    oracle.attn_bwd(oracle.SLIDING, q, k[2], v[2], do, scale, window=cfg.w, positions=rows)
+    t_rows = time.perf_counter() - t0
+    total = B * G * (t_group + t_rows * T / samples)
+    del torch
+    return {"value": round(B * T / total, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"C oracle (float64 branches, fp32 scoring), 1 thread: {samples} of {T} query timesteps x "
+                      f"{hpg} heads of 1 of {G} KV groups fwd+bwd ({t_rows:.1f}s) + compress_tokens of that group "
+                      f"({t_group:.1f}s), extrapolated x{T / samples:.0f} rows x{G} groups"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="paper", choices=sorted(CONFIGS))
+    ap.add_argument("--no-secondary", action="store_true", help="skip the T=32K configuration")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-samples", type=int, default=1024)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build targets single-GPU "
+              f"boxes; see DESIGN.md for how the path would shard.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from nsa import _lib
+
+    dev = torch.device("cuda:0")
+    c = CONFIGS[args.config]
+    cfg, mod, w = make_workload(args.config, dev)
+    print(f"[bench] workload {args.config} {c}", file=sys.stderr, flush=True)
+
+    # untimed: breakdown, the dominant kernel and the exact valid-pair counts
+    breakdown = kernel_breakdown(cfg, mod, w)
+    idx, be = nsa_step(cfg, mod, w, backward=False)
+    pairs = valid_pairs(cfg, idx, be, c["T"], c["B"], c["H"])
+    flops = kernel_flops(cfg, pairs)
+    attn_ids = [k for k in range(9) if KERNELS[k] in breakdown]
+    dominant = max(attn_ids, key=lambda k: breakdown[KERNELS[k]]["ms"])
+    print(f"[bench] breakdown {json.dumps(breakdown)}", file=sys.stderr, flush=True)
+
+    fwd_s = time_steps(cfg, mod, w, args.steps, args.warmup, backward=False)
+
+    # timed region: K fwd+bwd steps, the dominant kernel timed with HIP events
+    for _ in range(args.warmup):
+        nsa_step(cfg, mod, w)
+    torch.cuda.synchronize()
+    with _lib.KernelTimer(dominant) as tm:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            nsa_step(cfg, mod, w)
+        torch.cuda.synchronize()
+        step_s = (time.perf_counter() - t0) / args.steps
+    tokens = c["B"] * c["T"]
+    per_launch_ms = tm.ms / max(tm.launches, 1)
+    achieved = flops[dominant] / (per_launch_ms * 1e-3) / 1e12
+    total_alg = sum(2 * (4 * cfg.head_dim_qk + 3 * cfg.head_dim_v) * p for p in pairs)
+
+    result = {
+        "metric": "NSA fwd+bwd tokens/sec at T=8K/32K on 1 MI355X; % of bf16 MFMA peak",
+        "value": round(tokens / step_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_s * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: NSA attention core fwd+bwd (compress_tokens, Eq.8-10 top-n, "
+                               f"compression/selection/sliding HIP branches, sigmoid-gated mix)",
+                   "B": c["B"], "H": c["H"], "G": c["G"], "T": c["T"], "dk": cfg.head_dim_qk, "dv": cfg.head_dim_v,
+                   "l": cfg.l, "d": cfg.d, "l_prime": cfg.l_prime, "n": cfg.n, "w": cfg.w,
+                   "global_batch": c["B"], "seq_len": c["T"], "parallelism": "none (1 GPU)"},
+        "fwd_tokens_per_s": round(tokens / fwd_s, 1),
+        "attention_tflops_fwd_bwd": round(total_alg / step_s / 1e12, 2),
+        "mfma_frac_end_to_end": round(total_alg / step_s / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "kernel": KERNELS[dominant], "achieved": round(achieved, 2),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "launch_ms": round(per_launch_ms, 4), "launches": tm.launches, "traffic": None},
+        "valid_pairs": {"sliding": pairs[0], "compression": pairs[1], "selection": pairs[2]},
+        "breakdown_ms": {k: v["ms"] for k, v in breakdown.items()},
+    }
+    if not args.no_secondary and args.config == "paper":
+        cfg2, mod2, w2 = make_workload("long", dev, seed=1)
+        s2 = time_steps(cfg2, mod2, w2, max(2, args.steps // 2), 1)
+        f2 = time_steps(cfg2, mod2, w2, max(2, args.steps // 2), 1, backward=False)
+        t2 = CONFIGS["long"]["T"] * CONFIGS["long"]["B"]
+        result["secondary"] = {"workload": "long: B1 H32 G2 T32768 dk=dv=128 bf16, low-rank peaked q/k",
+                               "value": round(t2 / s2, 1), "fwd_tokens_per_s": round(t2 / f2, 1),
+                               "ms_per_step": round(s2 * 1e3, 3)}
+        del mod2, w2
+    if not args.no_cpu_baseline:
+        print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_samples)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

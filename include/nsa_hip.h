@@ -155,6 +155,47 @@ int nsa_sparse_selection_bwd(const void* Q, const void* K, const void* V, const 
                              int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream);
 
+
+/* ---- kernel timing (no reference counterpart: profiling aid) ----------------
+ * nsa_timing_begin(id) records a HIP event pair on the launch stream around every
+ * subsequent launch of kernel `id` (0-2 forward of sliding/compression/selection,
+ * 3-5 their dQ kernels, 6-8 their dK/dV kernels, 9 dK/dV partial reduce, 10 scoring
+ * top-n, 11/12 compression pooling fwd/bwd); nsa_timing_end() waits for those events
+ * and returns the summed milliseconds and the number of launches, then disarms. */
+int nsa_timing_begin(int kernel_id);
+int nsa_timing_end(double* total_ms, int* launches);
+
+/* ---- selection scoring: Eq. 8 -> 9 -> 10 -> top-n, fused -------------------
+ * Replaces the module's inline Eq. 8 (nsa/kernels.py:2316-2343),
+ * derive_selection_from_compression_per_timestep (nsa/kernels.py:1920-1962) and
+ * select_top_k_blocks_per_query_with_gqa (nsa/kernels.py:1965-2040).
+ * q [Z,H,T,dk] and k_cmp [Z,G,dk,n_blocks] (element (z,g,e,i) at the given strides,
+ * passed in (z, g, dk, block) order) share `dtype`; Block_ends int32 contiguous.
+ * out_idx [Z,G,T,n] int64 (strides in elements).  p_cmp [Z,H,T,n_blocks] and
+ * p_slc [Z,H,T,ceil(n_blocks/(l'/d))] are optional compact fp32 outputs (NULL to
+ * skip).  fp32 arithmetic in a fixed order: indices are reproducible bit for bit.
+ * include_fixed && n_fixed > 0 merges the blocks [0, max(0,(t-l')/l'), t/l'] first. */
+size_t nsa_score_topn_workspace_size(int Z, int H, int n_kv_groups, int n_ctx, int head_dim_qk, int n_blocks, int n);
+int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* Block_ends, int64_t* out_idx, float* p_cmp,
+                   float* p_slc, int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_qk,
+                   int64_t stride_kz, int64_t stride_kg, int64_t stride_kk, int64_t stride_kn, int64_t stride_iz,
+                   int64_t stride_ig, int64_t stride_im, int64_t stride_in, int Z, int H, int n_kv_groups, int n_ctx,
+                   int head_dim_qk, int n_blocks, int l, int d, int l_prime, int n, int include_fixed, int n_fixed,
+                   int dtype, float scale, void* workspace, size_t workspace_bytes, nsa_stream_t stream);
+
+/* ---- compression pooling (compress_tokens, nsa/kernels.py:2119-2208) --------
+ * With the first MLP layer split as W1 = [W1k | W1p]:  Y = k W1k^T  [Z,G,T,width],
+ * C = E W1p^T + b1  [l,width].  Forward writes R[i] = mean_{u<l} relu(Y[d*i+u] + C[u])
+ * [Z,G,n_act,width] and V_cmp[i] = mean_{u<l} v[d*i+u] [Z,G,n_act,dv]; the caller
+ * finishes K_cmp = R W2^T + b2.  Backward overwrites dY, dV (dtype) and dC (fp32).
+ * All tensors compact row-major. */
+int nsa_compress_pool_fwd(const void* Y, const void* C, const void* V, void* R, void* V_cmp, int Z, int n_kv_groups,
+                          int n_ctx, int width, int head_dim_v, int l, int d, int n_act, int dtype,
+                          nsa_stream_t stream);
+int nsa_compress_pool_bwd(const void* Y, const void* C, const void* dR, const void* dV_cmp, void* dY, float* dC,
+                          void* dV, int Z, int n_kv_groups, int n_ctx, int width, int head_dim_v, int l, int d,
+                          int n_act, int dtype, nsa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

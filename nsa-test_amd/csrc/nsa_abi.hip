@@ -189,7 +189,10 @@ int run_fwd(const Shape& s, const FwdIO& io, float scale, int window, const int3
     a.sel = at<int>(ws, L.clean);
   }
   if ((rc = check_hip("prep"))) return rc;
-  if (!dispatch_attn_fwd(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no forward kernel");
+  {
+    TimingScope ts(kIdFwd + s.br, st);
+    if (!dispatch_attn_fwd(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no forward kernel");
+  }
   return check_hip("attention forward");
 }
 
@@ -278,18 +281,26 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
     a.seg_off = at<int>(ws, L.seg_off);
   }
   if ((rc = check_hip("backward prep"))) return rc;
-  if (!dispatch_attn_bwd_dq(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no dQ kernel");
+  {
+    TimingScope ts(kIdDq + s.br, st);
+    if (!dispatch_attn_bwd_dq(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no dQ kernel");
+  }
   if ((rc = check_hip("dQ kernel"))) return rc;
-  if (!dispatch_attn_bwd_dkdv(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no dK/dV kernel");
+  {
+    TimingScope ts(kIdDkdv + s.br, st);
+    if (!dispatch_attn_bwd_dkdv(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no dK/dV kernel");
+  }
   if ((rc = check_hip("dK/dV kernel"))) return rc;
   if (s.br != kSliding) {
-    launch_partial_reduce(s.dtype, s.dk, s.dv, s.br, a, st);
+    { TimingScope ts(kIdReduce, st); launch_partial_reduce(s.dtype, s.dk, s.dv, s.br, a, st); }
     if ((rc = check_hip("dK/dV reduce"))) return rc;
   }
   return NSA_OK;
 }
 
 }  // namespace
+
+int nsa::set_error(int code, const char* msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 

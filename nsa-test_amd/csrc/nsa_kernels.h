@@ -29,4 +29,30 @@ void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int 
                     int* csr_t, int* seg_off, hipStream_t st);
 int sel_csr_chunks(int Tq);
 
+// record an error message for nsa_last_error(); returns `code`
+int set_error(int code, const char* msg);
+
+// Kernel ids for nsa_timing_begin (fwd / dq / dkdv are offset by the branch).
+enum KernelId : int {
+  kIdFwd = 0,    // + branch
+  kIdDq = 3,     // + branch
+  kIdDkdv = 6,   // + branch
+  kIdReduce = 9,
+  kIdScore = 10,
+  kIdPoolFwd = 11,
+  kIdPoolBwd = 12,
+  kIdPrep = 13,  // K/V repack, row statistics, selection index CSR
+};
+
+// Records a HIP event pair around its lifetime when timing of `kind` is armed.
+class TimingScope {
+ public:
+  TimingScope(int kind, hipStream_t st);
+  ~TimingScope();
+
+ private:
+  bool active_;
+  hipStream_t stream_;
+};
+
 }  // namespace nsa

@@ -47,8 +47,10 @@ SIGNATURES = {
         _I, [_P, _P, _P, _P, _P, _P, _F, _P, _P, *_S26, _P, _P, _P, *_S12, *[_I] * 12, _I, _P, _Z, _P]),
     "nsa_score_topn": (_I, [_P, _P, _P, _P, _P, _P, *[_L] * 12, *[_I] * 13, _F, _P, _Z, _P]),
     "nsa_score_topn_workspace_size": (_Z, [_I] * 7),
-    "nsa_compress_pool_fwd": (_I, [_P, _P, _P, _P, _P, *[_L] * 8, *[_I] * 8, _P]),
-    "nsa_compress_pool_bwd": (_I, [_P, _P, _P, _P, _P, _P, *[_L] * 4, *[_I] * 8, _P]),
+    "nsa_timing_begin": (_I, [_I]),
+    "nsa_timing_end": (_I, [_P, _P]),
+    "nsa_compress_pool_fwd": (_I, [_P] * 5 + [_I] * 9 + [_P]),
+    "nsa_compress_pool_bwd": (_I, [_P] * 7 + [_I] * 9 + [_P]),
 }
 
 _lock = threading.Lock()
@@ -105,3 +107,28 @@ def call(name: str, *args) -> None:
 
 def size(name: str, *args) -> int:
     return int(getattr(load(), name)(*args))
+
+
+# kernel ids of nsa_timing_begin
+KID_FWD, KID_DQ, KID_DKDV, KID_REDUCE, KID_SCORE, KID_POOL_FWD, KID_POOL_BWD = 0, 3, 6, 9, 10, 11, 12
+
+
+class KernelTimer:
+    """Sum of the device time of every launch of one kernel inside a `with` block,
+    from HIP events the library records on the launch stream."""
+
+    def __init__(self, kernel_id: int):
+        self.kernel_id = kernel_id
+        self.ms = 0.0
+        self.launches = 0
+
+    def __enter__(self):
+        call("nsa_timing_begin", self.kernel_id)
+        return self
+
+    def __exit__(self, *exc):
+        ms = ctypes.c_double(0.0)
+        n = ctypes.c_int(0)
+        call("nsa_timing_end", ctypes.cast(ctypes.pointer(ms), c_void_p), ctypes.cast(ctypes.pointer(n), c_void_p))
+        self.ms, self.launches = ms.value, n.value
+        return False

@@ -1,0 +1,473 @@
+"""Native Sparse Attention on MI355X: configuration, launch surface, autograd and module.
+
+Drop-in for the reference's ``nsa.kernels`` (Noumena-Network/NSA-Test,
+nsa/kernels.py).  Same public names and argument contracts:
+
+* ``NSAConfig`` (nsa/kernels.py:516-591), including ``gate_mode`` and the
+  ``include_fixed_in_selection`` / ``n_fixed`` normalisation;
+* the six launchable kernels ``_nsa_{sliding_window,compression,sparse_selection}_
+  {fwd,bwd}_kernel``, called as ``KERNEL[grid](*tensors_and_strides, **constexprs)``
+  with the reference's positional order (nsa/kernels.py:594-654, :836-906,
+  :1151-1191, :1303-1363, :1533-1574, :1690-1751), the [B,G,dk,T] K layout with
+  swapped strides and the [B,G,T,dk] dK layout;
+* the autograd wrappers ``CompressionAttention``, ``SelectionAttention``,
+  ``SlidingWindowAttention`` (nsa/kernels.py:34-513);
+* ``derive_selection_from_compression_per_timestep`` and
+  ``select_top_k_blocks_per_query_with_gqa`` (nsa/kernels.py:1920-2040);
+* ``NSAAttention`` (nsa/kernels.py:2043-2507) with the same sub-module names, so
+  state dicts are interchangeable.
+
+Every kernel runs in libnsa_hip.so (hand-written HIP for gfx950).  There is no CPU
+path: tensors must live on the GPU, and a missing library raises.
+
+Deliberate differences from the reference, all toward its own oracle
+(nsa/reference.py):
+* the compression wrapper reads K_cmp with the documented swapped strides (the
+  reference wrapper passes them unswapped, nsa/kernels.py:62-65);
+* head widths that are not powers of two (dk = 192) are handled exactly (the
+  reference's sliding / compression launches read past the row, :85-86, :418-419);
+* a block index repeated in one row counts once (the union of nsa/reference.py:
+  233-246; the reference kernel visits it once per slot);
+* Eq. 8 scores are computed in fp32 whatever the module dtype, and the eval path
+  runs the same GPU kernels as training (they are deterministic) instead of
+  float64 CPU loops (nsa/kernels.py:2366-2398).
+"""
+from __future__ import annotations
+
+import functools
+import math
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from . import _lib, _ops
+from ._ops import COMPRESSION, SELECTION, SLIDING
+
+
+# =============================================================================== config
+@dataclass
+class NSAConfig:
+    """NSA hyper-parameters (paper section 4.1); field-for-field the reference's
+    NSAConfig (nsa/kernels.py:516-591)."""
+
+    d_model: int = 2560
+    head_dim_qk: int = 192
+    head_dim_v: int = 128
+    l: int = 32
+    d: int = 16
+    l_prime: int = 64
+    n: int = 16
+    include_fixed_in_selection: bool = True
+    n_fixed: int = 3
+    n_dynamic: int = 13
+    w: int = 512
+    n_heads: int = 64
+    n_kv_groups: int = 4
+    dropout_p: float = 0.0
+    use_bias: bool = False
+    block_m: int = 32  # accepted for compatibility; the HIP kernels choose their own tiles
+    block_n: int = 32
+    gate_mode: str = "sigmoid"
+
+    def __post_init__(self):
+        assert self.n_heads % self.n_kv_groups == 0
+        assert self.l % self.d == 0
+        assert self.l_prime % self.d == 0
+        assert self.w > 0
+        if not self.include_fixed_in_selection:
+            self.n_fixed = 0
+        self.n_dynamic = max(0, self.n - self.n_fixed)
+        assert self.n_fixed + self.n_dynamic == self.n
+        assert self.gate_mode in ("sigmoid", "softmax")
+
+    @property
+    def heads_per_group(self) -> int:
+        return self.n_heads // self.n_kv_groups
+
+    @property
+    def head_dim_qk_padded(self) -> int:
+        p = 1
+        while p < self.head_dim_qk:
+            p *= 2
+        return p
+
+    @property
+    def head_dim_v_padded(self) -> int:
+        p = 1
+        while p < self.head_dim_v:
+            p *= 2
+        return p
+
+
+# ================================================================ launchable kernels
+def _view(t, size, stride):
+    """The logical tensor a Triton kernel would address: element x at
+    base + sum(x_i * stride_i).  torch checks the view stays inside t's storage."""
+    if t is None:
+        return None
+    return torch.as_strided(t, size, stride, t.storage_offset())
+
+
+class _HipKernel:
+    """``KERNEL[grid](*args, **constexprs)`` front end of one libnsa_hip.so entry point.
+
+    The grid is accepted (tuple or callable of the meta-parameters) and ignored: the
+    HIP kernels pick their own decomposition.  BLOCK_M / BLOCK_N are hints and
+    HEAD_DIM_* may be padded widths; the real widths come from the tensors."""
+
+    def __init__(self, name: str, branch: int, backward: bool):
+        self.__name__ = name
+        self.branch = branch
+        self.backward = backward
+
+    def __repr__(self):
+        return f"<HIP kernel {self.__name__}>"
+
+    def __getitem__(self, grid):
+        if not (callable(grid) or isinstance(grid, (tuple, list))):
+            raise TypeError("grid must be a tuple or a callable of the meta-parameters")
+        return functools.partial(self._launch, grid)
+
+    def _launch(self, grid, *args, **kw):
+        br, bwd = self.branch, self.backward
+        a = list(args)
+        pos = 0
+
+        def take(n):
+            nonlocal pos
+            out = a[pos:pos + n]
+            pos += n
+            return out
+
+        if br == SLIDING:
+            Q, K, V, Out = take(4)
+            Blk = None
+        elif br == COMPRESSION:
+            Q, K, V, Blk, Out = take(5)
+        else:
+            Q, K, V, Blk, Out = take(5)
+        dOut = take(1)[0] if bwd else None
+        scale, L, M = take(3)
+        sq, sk, sv, so = take(4), take(4), take(4), take(4)
+        sb = take(4) if br == SELECTION else None
+        sl, sm = take(3), take(3)
+        if bwd:
+            dQ, dK, dV = take(3)
+            sdq, sdk, sdv = take(4), take(4), take(4)
+        if pos != len(a):
+            raise TypeError(f"{self.__name__}: expected {pos} positional arguments, got {len(a)}")
+        Z, H, G = int(kw["Z"]), int(kw["H"]), int(kw["N_KV_GROUPS"])
+        if br == SLIDING:
+            Tq = Tkv = int(kw["N_CTX"])
+        elif br == COMPRESSION:
+            Tq, Tkv = int(kw["N_CTX_Q"]), int(kw["N_BLOCKS"])
+        else:
+            Tq, Tkv = int(kw["N_CTX_Q"]), int(kw["N_CTX_KV"])
+        dk, dv = Q.shape[-1], V.shape[-1]
+        q = _view(Q, (Z, H, Tq, dk), sq)
+        k = _view(K, (Z, G, Tkv, dk), sk)
+        v = _view(V, (Z, G, Tkv, dv), sv)
+        o = _view(Out, (Z, H, Tq, dv), so)
+        Lv = _view(L, (Z, H, Tq), sl)
+        Mv = _view(M, (Z, H, Tq), sm)
+        extra = {}
+        if br == SLIDING:
+            extra["window"] = int(kw["WINDOW_SIZE"])
+        elif br == COMPRESSION:
+            extra["block_ends"] = Blk.reshape(-1)[:Tkv]
+        else:
+            n = int(kw["N_BLOCKS"])
+            extra["indices"] = _view(Blk, (Z, G, Tq, n), sb)
+            extra["lprime"] = int(kw["BLOCK_SIZE_SELECTION"])
+            extra["causal"] = bool(kw.get("IS_CAUSAL", True))
+        if not bwd:
+            _ops.attn_fwd(br, q, k, v, float(scale), out=o, L=Lv, M=Mv, **extra)
+            return None
+        do = _view(dOut, (Z, H, Tq, dv), so)  # dOut shares Out's strides in the reference
+        dq = _view(dQ, (Z, H, Tq, dk), sdq)
+        dkv = _view(dK, (Z, G, Tkv, dk), sdk)
+        dvv = _view(dV, (Z, G, Tkv, dv), sdv)
+        _ops.attn_bwd(br, q, k, v, o, do, Lv, Mv, float(scale), dq=dq, dk=dkv, dv=dvv, **extra)
+        return None
+
+
+_nsa_sliding_window_fwd_kernel = _HipKernel("_nsa_sliding_window_fwd_kernel", SLIDING, False)
+_nsa_sliding_window_bwd_kernel = _HipKernel("_nsa_sliding_window_bwd_kernel", SLIDING, True)
+_nsa_compression_fwd_kernel = _HipKernel("_nsa_compression_fwd_kernel", COMPRESSION, False)
+_nsa_compression_bwd_kernel = _HipKernel("_nsa_compression_bwd_kernel", COMPRESSION, True)
+_nsa_sparse_selection_fwd_kernel = _HipKernel("_nsa_sparse_selection_fwd_kernel", SELECTION, False)
+_nsa_sparse_selection_bwd_kernel = _HipKernel("_nsa_sparse_selection_bwd_kernel", SELECTION, True)
+
+
+# ==================================================================== autograd wrappers
+def _kt(k):
+    """[B,G,dk,T] -> the (b, g, time, dk) view."""
+    return k.transpose(-1, -2)
+
+
+class CompressionAttention(torch.autograd.Function):
+    """Compression branch (reference nsa/kernels.py:34-171).  k_compressed
+    [B,G,dk,N], v_compressed [B,G,N,dv], block_ends [N]."""
+
+    @staticmethod
+    def forward(ctx, q, k_compressed, v_compressed, block_ends, scale, config):
+        o, L, M = _ops.attn_fwd(COMPRESSION, q, _kt(k_compressed), v_compressed, scale, block_ends=block_ends)
+        ctx.save_for_backward(q, k_compressed, v_compressed, block_ends, o, L, M)
+        ctx.scale = scale
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, kc, vc, be, o, L, M = ctx.saved_tensors
+        dq, dk, dv = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o, do, L, M, ctx.scale, block_ends=be)
+        return dq, dk.transpose(-1, -2), dv, None, None, None
+
+
+class SelectionAttention(torch.autograd.Function):
+    """Selection branch (reference nsa/kernels.py:174-365).  indices [B,G,T,n]
+    (int32 or int64, -1 = empty); a row with no valid index falls back to block t//l'."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, indices, scale, config):
+        lp = config.l_prime
+        o, L, M = _ops.attn_fwd(SELECTION, q, _kt(k), v, scale, indices=indices, lprime=lp, fallback=True)
+        ctx.save_for_backward(q, k, v, indices, o, L, M)
+        ctx.scale = scale
+        ctx.lprime = lp
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, idx, o, L, M = ctx.saved_tensors
+        dq, dk, dv = _ops.attn_bwd(SELECTION, q, _kt(k), v, o, do, L, M, ctx.scale, indices=idx, lprime=ctx.lprime,
+                                   fallback=True)
+        return dq, dk.transpose(-1, -2), dv, None, None, None
+
+
+class SlidingWindowAttention(torch.autograd.Function):
+    """Sliding-window branch (reference nsa/kernels.py:368-513)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, scale, window_size, config):
+        o, L, M = _ops.attn_fwd(SLIDING, q, _kt(k), v, scale, window=window_size)
+        ctx.save_for_backward(q, k, v, o, L, M)
+        ctx.scale = scale
+        ctx.window = window_size
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        q, k, v, o, L, M = ctx.saved_tensors
+        dq, dk, dv = _ops.attn_bwd(SLIDING, q, _kt(k), v, o, do, L, M, ctx.scale, window=ctx.window)
+        return dq, dk.transpose(-1, -2), dv, None, None, None
+
+
+class _CompressPool(torch.autograd.Function):
+    """R[i] = mean_u relu(Y[d*i+u] + C[u]),  V_cmp[i] = mean_u v[d*i+u]  (HIP)."""
+
+    @staticmethod
+    def forward(ctx, Y, C, v, l, d, n_act):
+        cdt = _ops.compute_dtype(Y.dtype)
+        Yc, Cc, vc = Y.to(cdt).contiguous(), C.to(cdt).contiguous(), v.to(cdt).contiguous()
+        B, G, T, W = Yc.shape
+        dv = vc.shape[-1]
+        R = torch.empty(B, G, n_act, W, device=Y.device, dtype=cdt)
+        Vc = torch.empty(B, G, n_act, dv, device=Y.device, dtype=cdt)
+        _lib.call("nsa_compress_pool_fwd", _ops._ptr(Yc), _ops._ptr(Cc), _ops._ptr(vc), _ops._ptr(R), _ops._ptr(Vc),
+                  B, G, T, W, dv, l, d, n_act, _ops._dtype_code(cdt), _ops._stream(Y.device))
+        ctx.save_for_backward(Yc, Cc)
+        ctx.meta = (l, d, n_act, dv, Y.dtype, C.dtype, v.dtype)
+        return R.to(Y.dtype), Vc.to(v.dtype)
+
+    @staticmethod
+    def backward(ctx, dR, dVc):
+        Yc, Cc = ctx.saved_tensors
+        l, d, n_act, dv, ydt, cdt_in, vdt = ctx.meta
+        cdt = Yc.dtype
+        B, G, T, W = Yc.shape
+        dRc = (dR if dR is not None else torch.zeros(B, G, n_act, W, device=Yc.device)).to(cdt).contiguous()
+        dVcc = (dVc if dVc is not None else torch.zeros(B, G, n_act, dv, device=Yc.device)).to(cdt).contiguous()
+        dY = torch.empty_like(Yc)
+        dV = torch.empty(B, G, T, dv, device=Yc.device, dtype=cdt)
+        dC = torch.empty(l, W, device=Yc.device, dtype=torch.float32)
+        _lib.call("nsa_compress_pool_bwd", _ops._ptr(Yc), _ops._ptr(Cc), _ops._ptr(dRc), _ops._ptr(dVcc),
+                  _ops._ptr(dY), _ops._ptr(dC), _ops._ptr(dV), B, G, T, W, dv, l, d, n_act, _ops._dtype_code(cdt),
+                  _ops._stream(Yc.device))
+        return dY.to(ydt), dC.to(cdt_in), dV.to(vdt), None, None, None
+
+
+# ============================================================== selection (Eq. 9 / 10)
+def derive_selection_from_compression_per_timestep(compression_scores: torch.Tensor,
+                                                   config: NSAConfig) -> torch.Tensor:
+    """Eq. 9 (reference nsa/kernels.py:1920-1962): p_slc[j] = sum_{m<l'/d} sum_{n<l/d}
+    p_cmp[s*j+m+n], accumulated in the same (m, n) order, vectorised over j."""
+    B, H, T, nc = compression_scores.shape
+    assert config.l % config.d == 0 and config.l_prime % config.d == 0
+    a = config.l // config.d
+    s = config.l_prime // config.d
+    nsel = (nc + s - 1) // s
+    padded = F.pad(compression_scores, (0, nsel * s + s + a - nc))
+    out = torch.zeros(B, H, T, nsel, device=compression_scores.device, dtype=compression_scores.dtype)
+    for m in range(s):
+        for n in range(a):
+            # p_cmp[s*j + m + n] for all j; entries past nc are the zero padding
+            out += padded[..., m + n: m + n + s * nsel: s][..., :nsel]
+    return out
+
+
+def select_top_k_blocks_per_query_with_gqa(selection_scores: torch.Tensor, config: NSAConfig,
+                                           always_include_blocks: Optional[List[int]] = None) -> torch.Tensor:
+    """Eq. 10 + top-n (reference nsa/kernels.py:1965-2040): head-sum per KV group,
+    stable descending sort (ties -> lower block index), fixed blocks
+    [0, max(0,(t-l')//l'), t//l'] merged in front and de-duplicated in order, -1
+    padding.  Vectorised: no per-row host loop."""
+    B, H, T, nb = selection_scores.shape
+    G = config.n_kv_groups
+    agg = selection_scores.view(B, G, config.heads_per_group, T, nb).sum(dim=2)
+    k = min(config.n, nb)
+    _, order = torch.sort(agg, dim=-1, descending=True, stable=True)
+    top = order[..., :k]
+    dev = selection_scores.device
+    if config.include_fixed_in_selection and config.n_fixed > 0:
+        pos = torch.arange(T, device=dev)
+        fixed = torch.stack([torch.zeros_like(pos), torch.clamp((pos - config.l_prime) // config.l_prime, min=0),
+                             pos // config.l_prime], dim=-1)
+        cand = torch.cat([fixed.view(1, 1, T, 3).expand(B, G, T, 3), top], dim=-1)  # [B,G,T,3+k]
+        c = cand.shape[-1]
+        earlier = torch.triu(torch.ones(c, c, dtype=torch.bool, device=dev), diagonal=1)  # [i, j]: i < j
+        dup = ((cand.unsqueeze(-1) == cand.unsqueeze(-2)) & earlier).any(dim=-2)  # seen at an earlier slot
+        keep = ~dup
+        rank = torch.cumsum(keep.to(torch.int64), dim=-1) - 1
+        out = torch.full((B, G, T, config.n + 1), -1, device=dev, dtype=torch.long)
+        slot = torch.where(keep & (rank < config.n), rank, torch.full_like(rank, config.n))
+        out.scatter_(-1, slot, torch.where(slot < config.n, cand, torch.full_like(cand, -1)))
+        return out[..., :config.n]
+    if top.shape[-1] < config.n:
+        pad = torch.full((B, G, T, config.n - top.shape[-1]), -1, device=dev, dtype=top.dtype)
+        return torch.cat([top, pad], dim=-1)
+    return top[..., :config.n]
+
+
+def score_and_select(q: torch.Tensor, k_compressed: torch.Tensor, block_ends: torch.Tensor, scale: float,
+                     config: NSAConfig, return_scores: bool = False):
+    """Fused Eq. 8 -> 9 -> 10 -> top-n on the GPU (one HIP kernel).
+
+    q [B,H,T,dk], k_compressed [B,G,dk,N], block_ends [N] -> indices [B,G,T,n] int64
+    (and the fp32 p_cmp [B,H,T,N] / p_slc [B,H,T,nsel] when return_scores)."""
+    _ops._check_device(q, k_compressed, block_ends)
+    B, H, T, dk = q.shape
+    G, N = k_compressed.shape[1], k_compressed.shape[-1]
+    cdt = _ops.compute_dtype(q.dtype)
+    qc = q.to(cdt)
+    kc = k_compressed.to(cdt)
+    be = block_ends.to(torch.int32).contiguous()
+    s = config.l_prime // config.d
+    nsel = (N + s - 1) // s
+    out = torch.empty(B, G, T, config.n, device=q.device, dtype=torch.long)
+    pc = torch.empty(B, H, T, N, device=q.device, dtype=torch.float32) if return_scores else None
+    ps = torch.empty(B, H, T, nsel, device=q.device, dtype=torch.float32) if return_scores else None
+    _lib.call("nsa_score_topn", _ops._ptr(qc), _ops._ptr(kc), _ops._ptr(be), _ops._ptr(out), _ops._ptr(pc),
+              _ops._ptr(ps), *qc.stride(), *kc.stride(), *out.stride(), B, H, G, T, dk, N, config.l, config.d,
+              config.l_prime, config.n, int(bool(config.include_fixed_in_selection)), int(config.n_fixed),
+              _ops._dtype_code(cdt), float(scale), _ops._ptr(None), 0, _ops._stream(q.device))
+    if return_scores:
+        return out, pc, ps
+    return out
+
+
+# ========================================================================= the module
+class NSAAttention(torch.nn.Module):
+    """Native Sparse Attention layer (reference nsa/kernels.py:2043-2507): projections,
+    compression with MLP pooling, fused Eq. 8-10 selection, the three HIP attention
+    branches, gated mixing and the output projection."""
+
+    def __init__(self, config: NSAConfig):
+        super().__init__()
+        self.config = config
+        c = config
+        lin = torch.nn.Linear
+        self.q_proj = lin(c.d_model, c.n_heads * c.head_dim_qk, bias=c.use_bias)
+        self.k_compress = lin(c.d_model, c.n_kv_groups * c.head_dim_qk, bias=c.use_bias)
+        self.v_compress = lin(c.d_model, c.n_kv_groups * c.head_dim_v, bias=c.use_bias)
+        self.k_select = lin(c.d_model, c.n_kv_groups * c.head_dim_qk, bias=c.use_bias)
+        self.v_select = lin(c.d_model, c.n_kv_groups * c.head_dim_v, bias=c.use_bias)
+        self.k_sliding = lin(c.d_model, c.n_kv_groups * c.head_dim_qk, bias=c.use_bias)
+        self.v_sliding = lin(c.d_model, c.n_kv_groups * c.head_dim_v, bias=c.use_bias)
+        self.pos_embed = torch.nn.Embedding(c.l, c.l)
+        self.compress_mlp = torch.nn.Sequential(
+            lin(c.head_dim_qk + c.l, c.head_dim_qk * 2), torch.nn.ReLU(), lin(c.head_dim_qk * 2, c.head_dim_qk))
+        self.gate_mlp = torch.nn.Sequential(
+            lin(c.d_model, c.d_model // 2), torch.nn.ReLU(), lin(c.d_model // 2, 3 * c.n_heads))
+        self.o_proj = lin(c.n_heads * c.head_dim_v, c.d_model, bias=c.use_bias)
+        self.dropout = torch.nn.Dropout(c.dropout_p)
+        self.scale = 1.0 / math.sqrt(c.head_dim_qk)
+
+    def compress_tokens(self, keys: torch.Tensor, values: torch.Tensor
+                        ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, int]:
+        """keys [B,G,T,dk], values [B,G,T,dv] -> (K_cmp [B,G,dk,Np], V_cmp [B,G,Np,dv],
+        block_ends [Np] int32, n_actual) with Np the power-of-two padded block count
+        (padding: zero keys/values, block_ends 999999), as nsa/kernels.py:2119-2208."""
+        c = self.config
+        B, G, T, dk = keys.shape
+        dv = values.shape[-1]
+        n_act = (T - c.l) // c.d + 1
+        n_pad = 1
+        while n_pad < n_act:
+            n_pad *= 2
+        dev, dt = keys.device, keys.dtype
+        block_ends = torch.full((n_pad,), 999999, device=dev, dtype=torch.int32)
+        if n_act <= 0:
+            return (torch.zeros(B, G, dk, n_pad, device=dev, dtype=dt), torch.zeros(B, G, n_pad, dv, device=dev, dtype=dt),
+                    block_ends, n_act)
+        block_ends[:n_act] = torch.arange(n_act, device=dev, dtype=torch.int32) * c.d + (c.l - 1)
+        l1, l2 = self.compress_mlp[0], self.compress_mlp[2]
+        W1k, W1p = l1.weight[:, :dk], l1.weight[:, dk:]
+        Y = F.linear(keys, W1k.to(dt))                                            # [B,G,T,2dk]
+        C = F.linear(self.pos_embed.weight.to(dt), W1p.to(dt),
+                     l1.bias.to(dt) if l1.bias is not None else None)             # [l,2dk]
+        R, Vc = _CompressPool.apply(Y, C, values, c.l, c.d, n_act)
+        Kc = F.linear(R, l2.weight.to(dt), l2.bias.to(dt) if l2.bias is not None else None)  # [B,G,n,dk]
+        Kc = F.pad(Kc, (0, 0, 0, n_pad - n_act)).transpose(-1, -2)               # [B,G,dk,Np]
+        Vc = F.pad(Vc, (0, 0, 0, n_pad - n_act))                                 # [B,G,Np,dv]
+        return Kc, Vc, block_ends, n_act
+
+    def forward(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
+                output_attentions: bool = False) -> Tuple[torch.Tensor, Optional[Dict]]:
+        c = self.config
+        B, T, D = hidden_states.shape
+        H, G, dk, dv = c.n_heads, c.n_kv_groups, c.head_dim_qk, c.head_dim_v
+        x = hidden_states
+
+        def heads(proj, n, width):
+            return proj(x).view(B, T, n, width).transpose(1, 2)
+
+        q = heads(self.q_proj, H, dk)
+        k_comp, v_comp = heads(self.k_compress, G, dk), heads(self.v_compress, G, dv)
+        k_sel, v_sel = heads(self.k_select, G, dk), heads(self.v_select, G, dv)
+        k_win, v_win = heads(self.k_sliding, G, dk), heads(self.v_sliding, G, dv)
+
+        k_cmp, v_cmp, block_ends, _ = self.compress_tokens(k_comp, v_comp)
+        with torch.no_grad():
+            sel = score_and_select(q.detach(), k_cmp.detach(), block_ends, self.scale, c, return_scores=output_attentions)
+        if output_attentions:
+            indices, p_cmp, p_slc = sel
+        else:
+            indices, p_cmp, p_slc = sel, None, None
+
+        qk = q.contiguous()
+        o_cmp = CompressionAttention.apply(qk, k_cmp, v_cmp, block_ends, self.scale, c)
+        o_sel = SelectionAttention.apply(qk, k_sel.transpose(-1, -2), v_sel, indices, self.scale, c)
+        o_win = SlidingWindowAttention.apply(qk, k_win.transpose(-1, -2), v_win, self.scale, c.w, c)
+
+        gates = self.gate_mlp(x).view(B, T, H, 3).permute(0, 2, 1, 3)
+        gates = torch.softmax(gates, dim=-1) if c.gate_mode == "softmax" else torch.sigmoid(gates)
+        o = o_cmp * gates[..., 0:1] + o_sel * gates[..., 1:2] + o_win * gates[..., 2:3]
+        o = o.transpose(1, 2).reshape(B, T, H * dv)
+        out = self.dropout(self.o_proj(o))
+        info = None
+        if output_attentions:
+            info = {"compression_scores": p_cmp, "selection_scores": p_slc, "selected_indices": indices,
+                    "gates": gates.permute(0, 2, 1, 3)}
+        return out, info

@@ -1,0 +1,317 @@
+"""GPU parity of the three HIP attention branches (forward and backward) against the
+CPU oracle, on the same seeded inputs.
+
+Tolerances (norm-relative): fp32 outputs 1e-5, fp32 gradients 1e-4 (target 1e-3);
+bf16 outputs and gradients 2e-2, with the oracle fed the bf16-rounded inputs.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import rel_err
+from nsa import _ops
+from nsa.kernels import (NSAConfig, SelectionAttention, _nsa_compression_bwd_kernel, _nsa_compression_fwd_kernel,
+                         _nsa_sliding_window_bwd_kernel, _nsa_sliding_window_fwd_kernel,
+                         _nsa_sparse_selection_bwd_kernel, _nsa_sparse_selection_fwd_kernel)
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: (1e-5, 1e-4), torch.bfloat16: (2e-2, 2e-2)}
+
+
+def _np(t):
+    return t.detach().float().cpu().double().numpy()
+
+
+def _make(seed, B, H, G, Tq, Tkv, dk, dv, dtype, dev):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, H, Tq, dk, generator=g).to(dtype)
+    kp = torch.randn(B, G, dk, Tkv, generator=g).to(dtype)  # reference layout [B,G,dk,T]
+    v = torch.randn(B, G, Tkv, dv, generator=g).to(dtype)
+    do = torch.randn(B, H, Tq, dv, generator=g).to(dtype)
+    return q.to(dev), kp.to(dev), v.to(dev), do.to(dev)
+
+
+def _check(kind, q, kp, v, do, scale, dtype, **kw):
+    """Run fwd + bwd through the tensor-level wrappers and compare with the oracle."""
+    k = kp.transpose(-1, -2)
+    out, L, M = _ops.attn_fwd(kind, q, k, v, scale, **kw)
+    dq, dk, dv = _ops.attn_bwd(kind, q, k, v, out, do, L, M, scale, **kw)
+    torch.cuda.synchronize()
+    okw = {key: (val.cpu().numpy() if torch.is_tensor(val) else val) for key, val in kw.items() if key != "fallback"}
+    ro, rL, rM = oracle.attn_fwd(kind, _np(q), _np(k), _np(v), scale, **okw)
+    rq, rk, rv = oracle.attn_bwd(kind, _np(q), _np(k), _np(v), _np(do), scale, **okw)
+    tol_o, tol_g = TOL[dtype]
+    errs = {"out": rel_err(_np(out), ro), "dq": rel_err(_np(dq), rq), "dk": rel_err(_np(dk), rk),
+            "dv": rel_err(_np(dv), rv)}
+    assert errs["out"] < tol_o and max(errs["dq"], errs["dk"], errs["dv"]) < tol_g, errs
+    # statistics: -inf exactly where the oracle row is empty, close elsewhere
+    Ln, Mn = L.cpu().numpy(), M.cpu().numpy()
+    assert np.array_equal(np.isneginf(Ln), np.isneginf(rL))
+    fin = np.isfinite(rL)
+    np.testing.assert_allclose(Ln[fin] + Mn[fin], rL[fin] + rM[fin], rtol=0, atol=5e-3 if dtype == torch.bfloat16 else 2e-5)
+    return out, (dq, dk, dv)
+
+
+SLIDING_CASES = [
+    # B, H, G, T, dk, dv, window, dtype
+    (1, 8, 2, 512, 64, 64, 256, torch.float32),   # benchmark config 1 shape
+    (2, 8, 2, 64, 32, 32, 16, torch.float32),     # reference tests/test_accuracy.py shape
+    (1, 16, 1, 300, 192, 128, 100, torch.bfloat16),
+    (2, 4, 4, 129, 64, 64, 512, torch.float32),   # window longer than the sequence
+    (1, 4, 2, 77, 128, 128, 1, torch.float32),    # window 1: out = v_t
+    (1, 8, 2, 700, 128, 128, 512, torch.bfloat16),
+    (1, 6, 3, 96, 48, 48, 40, torch.float32),     # head dims zero-padded to a compiled pair
+]
+
+
+@pytest.mark.parametrize("B,H,G,T,dk,dv,w,dtype", SLIDING_CASES)
+def test_sliding_parity(dev, B, H, G, T, dk, dv, w, dtype):
+    q, kp, v, do = _make(1, B, H, G, T, T, dk, dv, dtype, dev)
+    if w > 1:
+        _check(_ops.SLIDING, q, kp, v, do, 1 / math.sqrt(dk), dtype, window=w)
+        return
+    # window 1 (closed form): out = v_t, dV = sum of dO over the group's heads, and the
+    # softmax is constant so dQ = dK = 0 up to fp32 rounding of dP - D
+    k = kp.transpose(-1, -2)
+    out, L, M = _ops.attn_fwd(_ops.SLIDING, q, k, v, 0.1, window=1)
+    dq, dk_, dv_ = _ops.attn_bwd(_ops.SLIDING, q, k, v, out, do, L, M, 0.1, window=1)
+    hpg = H // G
+    torch.testing.assert_close(out, v.repeat_interleave(hpg, 1), rtol=0, atol=0)
+    torch.testing.assert_close(dv_, do.view(B, G, hpg, T, dv).sum(2), rtol=1e-6, atol=1e-6)
+    assert dq.abs().max().item() < 1e-5 and dk_.abs().max().item() < 1e-5
+
+
+COMPRESSION_CASES = [
+    # B, H, G, T, dk, dv, l, d, dtype
+    (1, 8, 2, 512, 64, 64, 32, 16, torch.float32),
+    (2, 8, 2, 64, 32, 32, 8, 8, torch.float32),
+    (1, 16, 1, 1100, 192, 128, 32, 16, torch.bfloat16),
+    (1, 4, 2, 20, 64, 64, 32, 16, torch.float32),  # no row sees a block: all zero, L = -inf
+    (1, 4, 1, 5000, 128, 128, 32, 16, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("B,H,G,T,dk,dv,l,d,dtype", COMPRESSION_CASES)
+def test_compression_parity(dev, B, H, G, T, dk, dv, l, d, dtype):
+    n_act = max((T - l) // d + 1, 0)
+    n_pad = 1
+    while n_pad < max(n_act, 1):
+        n_pad *= 2
+    be = torch.full((n_pad,), 999999, dtype=torch.int32)
+    be[:n_act] = torch.arange(n_act, dtype=torch.int32) * d + l - 1
+    q, kp, v, do = _make(2, B, H, G, T, n_pad, dk, dv, dtype, dev)
+    _check(_ops.COMPRESSION, q, kp, v, do, 1 / math.sqrt(dk), dtype, block_ends=be.to(dev))
+
+
+def _random_indices(seed, B, G, T, Tkv, lp, n, p_empty=0.15):
+    rng = np.random.default_rng(seed)
+    nb = (Tkv + lp - 1) // lp
+    idx = rng.integers(0, nb, size=(B, G, T, n))
+    idx[rng.random(idx.shape) < p_empty] = -1
+    return torch.tensor(idx)
+
+
+SELECTION_CASES = [
+    # B, H, G, T, dk, dv, l', n, dtype
+    (1, 8, 2, 512, 64, 64, 64, 4, torch.float32),
+    (2, 8, 2, 64, 32, 32, 16, 8, torch.float32),   # reference tests/test_selection_reference.py shape
+    (2, 8, 2, 64, 32, 32, 32, 4, torch.float32),   # reference tests/test_branches.py shape
+    (1, 16, 1, 700, 192, 128, 64, 16, torch.bfloat16),
+    (1, 4, 1, 300, 64, 64, 128, 3, torch.float32),  # selection blocks larger than a tile
+    (4, 16, 4, 256, 64, 64, 64, 16, torch.float32),  # n larger than the number of blocks
+    (1, 32, 2, 1024, 128, 128, 64, 16, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("B,H,G,T,dk,dv,lp,n,dtype", SELECTION_CASES)
+def test_selection_parity(dev, B, H, G, T, dk, dv, lp, n, dtype):
+    q, kp, v, do = _make(3, B, H, G, T, T, dk, dv, dtype, dev)
+    idx = _random_indices(4, B, G, T, T, lp, n)
+    idx[0, 0, 1, :] = 0  # repeated block in one row: counted once
+    _check(_ops.SELECTION, q, kp, v, do, 1 / math.sqrt(dk), dtype, indices=idx.to(dev), lprime=lp)
+
+
+def test_selection_int32_indices_and_noncausal(dev):
+    B, H, G, T, d, lp = 1, 4, 2, 128, 32, 32
+    q, kp, v, do = _make(5, B, H, G, T, T, d, d, torch.float32, dev)
+    idx = _random_indices(6, B, G, T, T, lp, 3)
+    _check(_ops.SELECTION, q, kp, v, do, 0.2, torch.float32, indices=idx.to(torch.int32).to(dev), lprime=lp)
+    _check(_ops.SELECTION, q, kp, v, do, 0.2, torch.float32, indices=idx.to(dev), lprime=lp, causal=False)
+
+
+def test_selection_wrapper_fallback(dev):
+    """SelectionAttention: a row whose slots are all -1 attends to its own block t//l'
+    (nsa/kernels.py:199-205)."""
+    B, H, G, T, d, lp, n = 1, 4, 2, 128, 32, 32, 4
+    q, kp, v, do = _make(7, B, H, G, T, T, d, d, torch.float32, dev)
+    idx = _random_indices(8, B, G, T, T, lp, n)
+    idx[:, :, ::5] = -1
+    cfg = NSAConfig(head_dim_qk=d, head_dim_v=d, n_heads=H, n_kv_groups=G, l_prime=lp, n=n)
+    qq, kk, vv = (t.clone().requires_grad_() for t in (q, kp, v))
+    out = SelectionAttention.apply(qq, kk, vv, idx.to(dev), 0.3, cfg)
+    out.backward(do)
+    eff = idx.clone()
+    allneg = (eff < 0).all(-1)
+    eff[allneg] = (torch.arange(T).view(1, 1, T).expand_as(allneg)[allneg] // lp).unsqueeze(-1)
+    k = kp.transpose(-1, -2)
+    ro, _, _ = oracle.attn_fwd(oracle.SELECTION, _np(q), _np(k), _np(v), 0.3, indices=eff.numpy(), lprime=lp)
+    rq, rk, rv = oracle.attn_bwd(oracle.SELECTION, _np(q), _np(k), _np(v), _np(do), 0.3, indices=eff.numpy(),
+                                 lprime=lp)
+    assert rel_err(_np(out), ro) < 1e-5
+    assert rel_err(_np(qq.grad), rq) < 1e-4
+    assert rel_err(_np(kk.grad.transpose(-1, -2)), rk) < 1e-4
+    assert rel_err(_np(vv.grad), rv) < 1e-4
+
+
+def test_backward_is_deterministic(dev):
+    B, H, G, T, dk, dv = 1, 16, 2, 600, 64, 64
+    q, kp, v, do = _make(9, B, H, G, T, T, dk, dv, torch.bfloat16, dev)
+    k = kp.transpose(-1, -2)
+    idx = _random_indices(10, B, G, T, T, 64, 6).to(dev)
+    n_act = (T - 32) // 16 + 1
+    be = (torch.arange(n_act, dtype=torch.int32) * 16 + 31).to(dev)
+    kc, vc = k[:, :, :n_act].contiguous(), v[:, :, :n_act].contiguous()
+    for kind, kk, vv, kw in ((_ops.SLIDING, k, v, dict(window=128)), (_ops.COMPRESSION, kc, vc, dict(block_ends=be)),
+                             (_ops.SELECTION, k, v, dict(indices=idx, lprime=64))):
+        out, L, M = _ops.attn_fwd(kind, q, kk, vv, 0.125, **kw)
+        g1 = _ops.attn_bwd(kind, q, kk, vv, out, do, L, M, 0.125, **kw)
+        g2 = _ops.attn_bwd(kind, q, kk, vv, out, do, L, M, 0.125, **kw)
+        for a, b in zip(g1, g2):
+            assert torch.equal(a, b), kind
+
+
+# ------------------------------------------------------- the raw launch surface
+def test_raw_sliding_launch_matches_reference_contract(dev):
+    """tests/test_kernel_contracts.py:22-172 of the reference: K [B,G,dk,T] with
+    swapped strides, dK allocated [B,G,T,dk] and accumulated, backward from the
+    forward's L/M; wrong (unswapped) strides give a different result."""
+    B, H, G, T, dk, dv, w = 1, 4, 2, 64, 32, 32, 16
+    q, k, v, do = _make(11, B, H, G, T, T, dk, dv, torch.float32, dev)
+    scale = 1 / math.sqrt(dk)
+    out = torch.zeros(B, H, T, dv, device=dev)
+    L = torch.zeros(B, H, T, device=dev)
+    M = torch.zeros(B, H, T, device=dev)
+    grid = lambda META: (triton_cdiv(T, META["BLOCK_M"]), B * H)  # noqa: E731
+    _nsa_sliding_window_fwd_kernel[grid](
+        q, k, v, out, scale, L, M, *q.stride(), k.stride(0), k.stride(1), k.stride(3), k.stride(2), *v.stride(),
+        *out.stride(), *L.stride(), *M.stride(), Z=B, H=H, N_KV_GROUPS=G, N_CTX=T, WINDOW_SIZE=w, HEAD_DIM_QK=dk,
+        HEAD_DIM_V=dv, BLOCK_M=32, BLOCK_N=32)
+    dq = torch.zeros_like(q)
+    dkb = torch.zeros(B, G, T, dk, device=dev)
+    dvb = torch.zeros_like(v)
+    _nsa_sliding_window_bwd_kernel[grid](
+        q, k, v, out, do, scale, L, M, *q.stride(), k.stride(0), k.stride(1), k.stride(3), k.stride(2), *v.stride(),
+        *out.stride(), *L.stride(), *M.stride(), dq, dkb, dvb, *dq.stride(), *dkb.stride(), *dvb.stride(), Z=B, H=H,
+        N_KV_GROUPS=G, N_CTX=T, WINDOW_SIZE=w, HEAD_DIM_QK=dk, HEAD_DIM_V=dv, BLOCK_M=32, BLOCK_N=32)
+    torch.cuda.synchronize()
+    kt = k.transpose(-1, -2)
+    ro, _, _ = oracle.attn_fwd(oracle.SLIDING, _np(q), _np(kt), _np(v), scale, window=w)
+    rq, rk, rv = oracle.attn_bwd(oracle.SLIDING, _np(q), _np(kt), _np(v), _np(do), scale, window=w)
+    assert rel_err(_np(out), ro) < 1e-5
+    assert rel_err(_np(dq), rq) < 1e-4 and rel_err(_np(dkb), rk) < 1e-4 and rel_err(_np(dvb), rv) < 1e-4
+    # dK is accumulated into (callers zero it): a second launch doubles it
+    _nsa_sliding_window_bwd_kernel[grid](
+        q, k, v, out, do, scale, L, M, *q.stride(), k.stride(0), k.stride(1), k.stride(3), k.stride(2), *v.stride(),
+        *out.stride(), *L.stride(), *M.stride(), dq, dkb, dvb, *dq.stride(), *dkb.stride(), *dvb.stride(), Z=B, H=H,
+        N_KV_GROUPS=G, N_CTX=T, WINDOW_SIZE=w, HEAD_DIM_QK=dk, HEAD_DIM_V=dv, BLOCK_M=32, BLOCK_N=32)
+    assert rel_err(_np(dkb), 2 * rk) < 1e-4
+    # a square K ([dk == T]) with unswapped strides stays in bounds but reads the transpose
+    ks = torch.randn(B, G, 32, 32, device=dev)
+    qs = q[:, :, :32, :].contiguous()
+    vs = v[:, :, :32, :].contiguous()
+    o1 = torch.zeros(B, H, 32, dv, device=dev)
+    o2 = torch.zeros(B, H, 32, dv, device=dev)
+    for o, ksd in ((o1, (ks.stride(3), ks.stride(2))), (o2, (ks.stride(2), ks.stride(3)))):
+        _nsa_sliding_window_fwd_kernel[(1, B * H)](
+            qs, ks, vs, o, scale, L, M, *qs.stride(), ks.stride(0), ks.stride(1), *ksd, *vs.stride(), *o.stride(),
+            *L.stride(), *M.stride(), Z=B, H=H, N_KV_GROUPS=G, N_CTX=32, WINDOW_SIZE=8, HEAD_DIM_QK=32,
+            HEAD_DIM_V=32, BLOCK_M=32, BLOCK_N=32)
+    assert ((o1 - o2).abs() / (o1.abs() + 1e-8)).max().item() > 0.1
+
+
+def triton_cdiv(a, b):
+    return (a + b - 1) // b
+
+
+def test_raw_compression_and_selection_launch(dev):
+    B, H, G, T, d = 2, 8, 2, 64, 32
+    q, k, v, do = _make(12, B, H, G, T, T, d, d, torch.float32, dev)
+    scale = 1 / math.sqrt(d)
+    # compression with 8 blocks of 8 (reference tests/test_branches.py:235-252)
+    nb = 8
+    kc = torch.randn(B, G, d, nb, device=dev)
+    vc = torch.randn(B, G, nb, d, device=dev)
+    be = (torch.arange(nb, dtype=torch.int32) * 8 + 7).to(dev)
+    out = torch.zeros(B, H, T, d, device=dev)
+    L = torch.zeros(B, H, T, device=dev)
+    M = torch.zeros(B, H, T, device=dev)
+    _nsa_compression_fwd_kernel[(2, B * H)](
+        q, kc, vc, be, out, scale, L, M, *q.stride(), kc.stride(0), kc.stride(1), kc.stride(3), kc.stride(2),
+        *vc.stride(), *out.stride(), *L.stride(), *M.stride(), Z=B, H=H, N_KV_GROUPS=G, N_CTX_Q=T, N_BLOCKS=nb,
+        HEAD_DIM_QK=d, HEAD_DIM_V=d, BLOCK_M=32, BLOCK_N=32)
+    dq = torch.zeros_like(q)
+    dkc = torch.zeros(B, G, nb, d, device=dev)
+    dvc = torch.zeros_like(vc)
+    _nsa_compression_bwd_kernel[(2, B * H)](
+        q, kc, vc, be, out, do, scale, L, M, *q.stride(), kc.stride(0), kc.stride(1), kc.stride(3), kc.stride(2),
+        *vc.stride(), *out.stride(), *L.stride(), *M.stride(), dq, dkc, dvc, *dq.stride(), *dkc.stride(),
+        *dvc.stride(), Z=B, H=H, N_KV_GROUPS=G, N_CTX_Q=T, N_BLOCKS=nb, HEAD_DIM_QK=d, HEAD_DIM_V=d, BLOCK_M=32,
+        BLOCK_N=32)
+    kct = kc.transpose(-1, -2)
+    ro, _, _ = oracle.attn_fwd(oracle.COMPRESSION, _np(q), _np(kct), _np(vc), scale, block_ends=be.cpu().numpy())
+    rq, rk, rv = oracle.attn_bwd(oracle.COMPRESSION, _np(q), _np(kct), _np(vc), _np(do), scale,
+                                 block_ends=be.cpu().numpy())
+    assert rel_err(_np(out), ro) < 1e-5
+    assert max(rel_err(_np(dq), rq), rel_err(_np(dkc), rk), rel_err(_np(dvc), rv)) < 1e-4
+    # selection with fixed-style indices (reference tests/test_branches.py:474-499), N_CTX_KV > N_CTX_Q
+    lp, n = 32, 4
+    Tkv = 96
+    ks = torch.randn(B, G, d, Tkv, device=dev)
+    vs = torch.randn(B, G, Tkv, d, device=dev)
+    nbk = (Tkv + lp - 1) // lp
+    idx = torch.full((B, G, T, n), -1, dtype=torch.int32)
+    for t in range(T):
+        loc = t // lp
+        cand = []
+        for c in (0, max(0, loc - 1), loc, min(loc + 1, nbk - 1)):
+            if c not in cand:
+                cand.append(c)
+        idx[:, :, t, :len(cand)] = torch.tensor(cand[:n], dtype=torch.int32)
+    idx = idx.to(dev)
+    out = torch.zeros(B, H, T, d, device=dev)
+    _nsa_sparse_selection_fwd_kernel[(2, B * H)](
+        q, ks, vs, idx, out, scale, L, M, *q.stride(), ks.stride(0), ks.stride(1), ks.stride(3), ks.stride(2),
+        *vs.stride(), *out.stride(), *idx.stride(), *L.stride(), *M.stride(), Z=B, H=H, N_KV_GROUPS=G, N_CTX_Q=T,
+        N_CTX_KV=Tkv, N_BLOCKS=n, BLOCK_SIZE_SELECTION=lp, HEAD_DIM_QK=d, HEAD_DIM_V=d, BLOCK_M=32, BLOCK_N=32,
+        IS_CAUSAL=True)
+    dq = torch.zeros_like(q)
+    dks = torch.zeros(B, G, Tkv, d, device=dev)
+    dvs = torch.zeros_like(vs)
+    _nsa_sparse_selection_bwd_kernel[(2, B * H)](
+        q, ks, vs, idx, out, do, scale, L, M, *q.stride(), ks.stride(0), ks.stride(1), ks.stride(3), ks.stride(2),
+        *vs.stride(), *out.stride(), *idx.stride(), *L.stride(), *M.stride(), dq, dks, dvs, *dq.stride(),
+        *dks.stride(), *dvs.stride(), Z=B, H=H, N_KV_GROUPS=G, N_CTX_Q=T, N_CTX_KV=Tkv, N_BLOCKS=n,
+        BLOCK_SIZE_SELECTION=lp, HEAD_DIM_QK=d, HEAD_DIM_V=d, BLOCK_M=32, BLOCK_N=32, IS_CAUSAL=True)
+    kst = ks.transpose(-1, -2)
+    ro, _, _ = oracle.attn_fwd(oracle.SELECTION, _np(q), _np(kst), _np(vs), scale, indices=idx.cpu().numpy(),
+                               lprime=lp)
+    rq, rk, rv = oracle.attn_bwd(oracle.SELECTION, _np(q), _np(kst), _np(vs), _np(do), scale,
+                                 indices=idx.cpu().numpy(), lprime=lp)
+    assert rel_err(_np(out), ro) < 1e-5
+    assert max(rel_err(_np(dq), rq), rel_err(_np(dks), rk), rel_err(_np(dvs), rv)) < 1e-4
+
+
+def test_strided_views(dev):
+    """Non-contiguous q / v / out views and a K whose time axis is not unit-stride."""
+    B, H, G, T, d = 1, 4, 2, 200, 64
+    base = torch.randn(B, T, H, d, device=dev)
+    q = base.transpose(1, 2)  # [B,H,T,d] with strided rows
+    kbig = torch.randn(B, G, T, d + 8, device=dev)
+    kp = kbig[..., :d].transpose(-1, -2)  # [B,G,d,T], time stride = d + 8
+    v = torch.randn(B, G, T, 2 * d, device=dev)[..., ::2]
+    do = torch.randn(B, H, T, d, device=dev)
+    _check(_ops.SLIDING, q, kp, v, do, 0.125, torch.float32, window=50)

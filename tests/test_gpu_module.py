@@ -1,0 +1,122 @@
+"""GPU tests of the NSAAttention module end to end: forward against the reference's
+golden outputs (eval mode) and the oracle, gradients against float64 torch autograd
+of the same computation, and the fused compress_tokens against the oracle."""
+import math
+import types
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import torch_nsa_ref
+from conftest import load_fixture, rel_err
+from nsa import NSAAttention, NSAConfig
+
+pytestmark = pytest.mark.gpu
+
+
+def _cfg_from(f):
+    return NSAConfig(**{k[4:]: f[k].item() for k in f.files if k.startswith("cfg/")})
+
+
+def _module_from(f, dev, dtype=torch.float32):
+    cfg = _cfg_from(f)
+    m = NSAAttention(cfg)
+    m.load_state_dict({k[6:]: torch.tensor(f[k]) for k in f.files if k.startswith("param/")})
+    return m.to(dev, dtype), cfg
+
+
+@pytest.fixture(autouse=True)
+def _ieee_fp32():
+    prev = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    yield
+    torch.backends.cuda.matmul.allow_tf32 = prev
+
+
+@pytest.mark.parametrize("name", ["module_cfg1", "module_odd_softmax", "module_short"])
+def test_module_forward_matches_reference_golden(dev, name):
+    f = load_fixture(name)
+    m, cfg = _module_from(f, dev)
+    m.eval()
+    with torch.no_grad():
+        out, info = m(torch.tensor(f["x"]).to(dev), output_attentions=True)
+    np.testing.assert_array_equal(info["selected_indices"].cpu().numpy(), f["selected_indices"])
+    assert rel_err(out.cpu().numpy(), f["out"]) < 1e-5
+    np.testing.assert_allclose(info["compression_scores"].cpu().numpy(), f["compression_scores"], rtol=0, atol=1e-5)
+    np.testing.assert_allclose(info["selection_scores"].cpu().numpy(), f["selection_scores"], rtol=0, atol=1e-4)
+    np.testing.assert_allclose(info["gates"].cpu().numpy(), f["gates"], rtol=0, atol=1e-6)
+    # and the oracle's float64 restatement with the same weights and indices
+    ro, _ = oracle.nsa_forward(f["x"], {k[6:]: f[k] for k in f.files if k.startswith("param/")}, cfg,
+                               indices=info["selected_indices"].cpu().numpy())
+    assert rel_err(out.cpu().numpy(), ro) < 1e-5
+
+
+@pytest.mark.parametrize("gate_mode,fixed", [("sigmoid", True), ("softmax", False)])
+def test_module_gradients_match_autograd(dev, gate_mode, fixed):
+    torch.manual_seed(0)
+    cfg = NSAConfig(d_model=64, head_dim_qk=64, head_dim_v=64, n_heads=8, n_kv_groups=2, l=32, d=16, l_prime=64,
+                    n=4, w=96, gate_mode=gate_mode, include_fixed_in_selection=fixed, use_bias=True)
+    m = NSAAttention(cfg).to(dev)
+    B, T = 2, 333
+    x = torch.randn(B, T, cfg.d_model, device=dev, requires_grad=True)
+    out, info = m(x, output_attentions=True)
+    gout = torch.randn_like(out)
+    out.backward(gout)
+    idx = info["selected_indices"].cpu()
+    P = {k: v.detach().cpu().double().requires_grad_() for k, v in m.state_dict().items()}
+    xr = x.detach().cpu().double().requires_grad_()
+    ref = torch_nsa_ref.nsa_forward(xr, P, cfg, idx)
+    ref.backward(gout.cpu().double())
+    assert rel_err(out.detach().cpu().numpy(), ref.detach().numpy()) < 1e-5
+    assert rel_err(x.grad.cpu().numpy(), xr.grad.numpy()) < 1e-3
+    grads = dict(m.named_parameters())
+    for k, p in P.items():
+        g, r = grads[k].grad.cpu().numpy(), p.grad.numpy()
+        if np.linalg.norm(r) < 1e-9 * np.sqrt(r.size):
+            # biases of the selection / sliding keys shift every logit of a row
+            # equally: the softmax is invariant, the exact gradient is 0
+            assert np.abs(g).max() < 1e-5, k
+            continue
+        assert rel_err(g, r) < 1e-3, k
+
+
+def test_module_bf16_end_to_end(dev):
+    torch.manual_seed(1)
+    cfg = NSAConfig(d_model=128, head_dim_qk=192, head_dim_v=128, n_heads=16, n_kv_groups=1, n=8, w=128)
+    m = NSAAttention(cfg).to(dev)
+    B, T = 1, 512
+    x = torch.randn(B, T, cfg.d_model, device=dev)
+    out32, info = m(x, output_attentions=True)
+    mb = NSAAttention(cfg).to(dev, torch.bfloat16)
+    mb.load_state_dict(m.state_dict())
+    xb = x.to(torch.bfloat16).requires_grad_()
+    outb, infob = mb(xb, output_attentions=True)
+    outb.float().sum().backward()
+    assert torch.isfinite(xb.grad.float()).all()
+    assert rel_err(outb.float().detach().cpu().numpy(), out32.detach().cpu().numpy()) < 3e-2
+    # the fused scoring runs in fp32 in both cases; the bf16 inputs move only near-ties
+    agree = (infob["selected_indices"] == info["selected_indices"]).float().mean().item()
+    assert agree > 0.9
+
+
+@pytest.mark.parametrize("T,dtype", [(512, torch.float32), (1000, torch.bfloat16), (40, torch.float32)])
+def test_compress_tokens_matches_oracle(dev, T, dtype):
+    torch.manual_seed(2)
+    cfg = NSAConfig(d_model=64, head_dim_qk=64, head_dim_v=32, n_heads=4, n_kv_groups=2)
+    m = NSAAttention(cfg).to(dev, dtype)
+    keys = torch.randn(2, 2, T, 64, device=dev, dtype=dtype)
+    vals = torch.randn(2, 2, T, 32, device=dev, dtype=dtype)
+    with torch.no_grad():
+        kc, vc, be, n_act = m.compress_tokens(keys, vals)
+    P = {k: v.float().cpu().numpy() for k, v in m.state_dict().items()}
+    rk, rv, rbe, rn = oracle.compress_tokens(keys.float().cpu().numpy(), vals.float().cpu().numpy(),
+                                             P["compress_mlp.0.weight"], P["compress_mlp.0.bias"],
+                                             P["compress_mlp.2.weight"], P["compress_mlp.2.bias"],
+                                             P["pos_embed.weight"], cfg.l, cfg.d)
+    assert n_act == rn and kc.shape == rk.shape and vc.shape == rv.shape
+    np.testing.assert_array_equal(be.cpu().numpy(), rbe)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert rel_err(kc.float().cpu().numpy(), rk) < tol
+    assert rel_err(vc.float().cpu().numpy(), rv) < tol

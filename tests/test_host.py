@@ -1,0 +1,155 @@
+"""CPU tests of the host side: configuration semantics, the torch selection helpers,
+the C ABI library (loads, exports every declared symbol) and the launch surface's
+argument handling.  No GPU computation happens here."""
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import nsa
+from nsa import _lib, _ops
+from nsa.kernels import NSAConfig, derive_selection_from_compression_per_timestep, select_top_k_blocks_per_query_with_gqa
+from conftest import ROOT, load_fixture
+
+
+# ------------------------------------------------------------------- config
+def test_config_defaults_and_normalisation():
+    c = NSAConfig()
+    assert (c.head_dim_qk, c.head_dim_v, c.l, c.d, c.l_prime, c.n, c.w) == (192, 128, 32, 16, 64, 16, 512)
+    assert (c.n_fixed, c.n_dynamic, c.gate_mode) == (3, 13, "sigmoid")
+    assert c.heads_per_group == 16 and c.head_dim_qk_padded == 256 and c.head_dim_v_padded == 128
+    c2 = NSAConfig(include_fixed_in_selection=False)
+    assert c2.n_fixed == 0 and c2.n_dynamic == 16
+    assert NSAConfig(n=8, n_fixed=3).n_dynamic == 5
+    for bad in (dict(n_heads=6, n_kv_groups=4), dict(l=30, d=16), dict(l_prime=40, d=16), dict(w=0),
+                dict(gate_mode="tanh")):
+        with pytest.raises(AssertionError):
+            NSAConfig(**bad)
+
+
+def test_exports_match_reference_surface():
+    names = {"NSAConfig", "NSAAttention", "_nsa_sliding_window_fwd_kernel", "_nsa_sliding_window_bwd_kernel",
+             "_nsa_compression_fwd_kernel", "_nsa_compression_bwd_kernel", "_nsa_sparse_selection_fwd_kernel",
+             "_nsa_sparse_selection_bwd_kernel"}
+    assert set(nsa.__all__) == names and nsa.__version__ == "1.0.0"
+    for n in ("CompressionAttention", "SelectionAttention", "SlidingWindowAttention",
+              "derive_selection_from_compression_per_timestep", "select_top_k_blocks_per_query_with_gqa"):
+        assert hasattr(nsa.kernels, n)
+
+
+def test_module_state_dict_keys_match_reference_layout():
+    c = NSAConfig(d_model=64, head_dim_qk=32, head_dim_v=32, n_heads=4, n_kv_groups=2)
+    m = nsa.NSAAttention(c)
+    f = load_fixture("module_odd_softmax")
+    ref_keys = {k[6:] for k in f.files if k.startswith("param/")}
+    assert set(m.state_dict().keys()) == ref_keys
+
+
+# ------------------------------------------------- torch selection helpers
+@pytest.mark.parametrize("name", ["topn_ties_fixed", "topn_ties_nofixed", "topn_causal_nexceeds"])
+def test_select_top_k_golden(name):
+    g = load_fixture(name)
+    G, n, lp, inc, nf = (int(x) for x in g["meta"])
+    H = g["scores"].shape[1]
+    cfg = NSAConfig(n_heads=H, n_kv_groups=G, n=n, l_prime=lp, d=16, l=32, include_fixed_in_selection=bool(inc),
+                    n_fixed=nf)
+    got = select_top_k_blocks_per_query_with_gqa(torch.tensor(g["scores"]), cfg)
+    np.testing.assert_array_equal(got.numpy(), g["indices"])
+
+
+@pytest.mark.parametrize("name", ["module_cfg1", "module_odd_softmax", "module_short"])
+def test_eq9_eq10_golden(name):
+    f = load_fixture(name)
+    kw = {k[4:]: f[k].item() for k in f.files if k.startswith("cfg/")}
+    cfg = NSAConfig(**kw)
+    sel = derive_selection_from_compression_per_timestep(torch.tensor(f["compression_scores"]), cfg)
+    np.testing.assert_array_equal(sel.numpy(), f["selection_scores"])
+    idx = select_top_k_blocks_per_query_with_gqa(torch.tensor(f["selection_scores"]), cfg)
+    np.testing.assert_array_equal(idx.numpy(), f["selected_indices"])
+
+
+def test_select_top_k_known_answers():
+    scores = torch.arange(5, dtype=torch.float32).view(1, 1, 1, 5).repeat(1, 2, 3, 1)
+    cfg = NSAConfig(l_prime=2, d=1, n=3, n_heads=2, n_kv_groups=1, include_fixed_in_selection=False)
+    assert select_top_k_blocks_per_query_with_gqa(scores, cfg)[0, 0, 0].tolist() == [4, 3, 2]
+    cfg = NSAConfig(l_prime=2, d=1, n=3, n_heads=2, n_kv_groups=1, include_fixed_in_selection=True, n_fixed=3)
+    idx = select_top_k_blocks_per_query_with_gqa(scores, cfg)
+    assert idx[0, 0, 0].tolist() == [0, 4, 3] and idx[0, 0, 2].tolist() == [0, 1, 4]
+
+
+# ----------------------------------------------------------- the C ABI library
+def _declared_functions():
+    text = (ROOT / "include" / "nsa_hip.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    decls = re.findall(r"^(?:int|size_t|const char\*)\s+(nsa_\w+)\s*\(([^;]*)\);", text, flags=re.M)
+    return {name: [a.strip() for a in args.split(",") if a.strip() and a.strip() != "void"] for name, args in decls}
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _lib.load()
+    decls = _declared_functions()
+    assert len(decls) >= 15
+    for name in decls:
+        assert hasattr(lib, name), f"{name} declared in include/nsa_hip.h but not exported"
+    assert lib.nsa_abi_version() == _lib.ABI_VERSION
+    assert lib.nsa_head_dims_supported(_lib.NSA_BF16, 192, 128) == 1
+    assert lib.nsa_head_dims_supported(_lib.NSA_F32, 48, 48) == 0
+
+
+def test_ctypes_signatures_match_header():
+    decls = _declared_functions()
+    for name, args in decls.items():
+        assert name in _lib.SIGNATURES, name
+        assert len(_lib.SIGNATURES[name][1]) == len(args), f"{name}: {len(_lib.SIGNATURES[name][1])} != {len(args)}"
+
+
+def test_workspace_sizes():
+    f = _lib.size("nsa_fwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64)
+    b = _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64)
+    assert 0 < f < b
+    s = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 16, 64)
+    assert s > b
+
+
+def test_error_codes_without_gpu_work():
+    # validation happens before any launch: unsupported head dims, bad window
+    lib = _lib.load()
+    rc = lib.nsa_sliding_window_fwd(*([None] * 4), 1.0, None, None, *([0] * 22), 1, 1, 1, 8, 4, 48, 48,
+                                    _lib.NSA_F32, None, 0, None)
+    assert rc == _lib.NSA_ERR_UNSUPPORTED and b"head dims" in lib.nsa_last_error()
+    assert _ops.kernel_dims(48, 48) == (64, 64) and _ops.kernel_dims(192, 128) == (192, 128)
+    with pytest.raises(ValueError):
+        _ops.kernel_dims(512, 64)
+
+
+def test_cpu_tensors_fail_loudly():
+    q = torch.randn(1, 2, 8, 32)
+    k = torch.randn(1, 1, 32, 8)
+    v = torch.randn(1, 1, 8, 32)
+    cfg = NSAConfig(d_model=32, head_dim_qk=32, head_dim_v=32, n_heads=2, n_kv_groups=1)
+    with pytest.raises(RuntimeError, match="GPU"):
+        nsa.SlidingWindowAttention.apply(q, k, v, 0.1, 4, cfg)
+    out = torch.empty(1, 2, 8, 32)
+    L = torch.empty(1, 2, 8)
+    with pytest.raises(RuntimeError, match="GPU"):
+        nsa._nsa_sliding_window_fwd_kernel[(1, 2)](
+            q, k, v, out, 0.1, L, L, *q.stride(), k.stride(0), k.stride(1), k.stride(3), k.stride(2), *v.stride(),
+            *out.stride(), *L.stride(), *L.stride(), Z=1, H=2, N_KV_GROUPS=1, N_CTX=8, WINDOW_SIZE=4,
+            HEAD_DIM_QK=32, HEAD_DIM_V=32, BLOCK_M=32, BLOCK_N=32)
+
+
+def test_launcher_rejects_out_of_storage_strides():
+    """Strides that would address memory outside the tensor are refused before any
+    launch (torch's view bounds check), where the reference would read past it."""
+    q = torch.randn(1, 2, 64, 32)
+    k = torch.randn(1, 2, 32, 64)
+    v = torch.randn(1, 2, 64, 32)
+    out = torch.empty(1, 2, 64, 32)
+    L = torch.empty(1, 2, 64)
+    with pytest.raises(RuntimeError, match="out of bounds"):
+        nsa._nsa_sliding_window_fwd_kernel[(1, 2)](
+            q, k, v, out, 0.1, L, L, *q.stride(), *k.stride(), *v.stride(), *out.stride(), *L.stride(), *L.stride(),
+            Z=1, H=2, N_KV_GROUPS=2, N_CTX=64, WINDOW_SIZE=16, HEAD_DIM_QK=32, HEAD_DIM_V=32, BLOCK_M=32,
+            BLOCK_N=32)
