@@ -58,7 +58,8 @@ int nsa_head_dims_supported(int dtype, int dk, int dv);
 size_t nsa_fwd_workspace_size(int branch, int dtype, int Z, int H, int n_kv_groups, int n_ctx_q, int n_ctx_kv,
                               int head_dim_qk, int head_dim_v, int n_slots, int block_size_selection);
 size_t nsa_bwd_workspace_size(int branch, int dtype, int Z, int H, int n_kv_groups, int n_ctx_q, int n_ctx_kv,
-                              int head_dim_qk, int head_dim_v, int n_slots, int block_size_selection);
+                              int head_dim_qk, int head_dim_v, int n_slots, int block_size_selection,
+                              int window_size);
 
 /* ---- sliding window --------------------------------------------------------
  * Replaces _nsa_sliding_window_fwd_kernel (reference nsa/kernels.py:1151-1191) and

@@ -1,5 +1,5 @@
 // Instantiations: attention bwd_dkdv kernels, element type bf16, every (DK, DV, branch).
-#include "nsa_attn_bwd.h"
+#include "nsa_attn_bwd_dkdv.h"
 #include "nsa_kernels.h"
 
 namespace nsa {

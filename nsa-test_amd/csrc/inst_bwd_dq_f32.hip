@@ -1,5 +1,5 @@
 // Instantiations: attention bwd_dq kernels, element type float, every (DK, DV, branch).
-#include "nsa_attn_bwd.h"
+#include "nsa_attn_bwd_dq.h"
 #include "nsa_kernels.h"
 
 namespace nsa {

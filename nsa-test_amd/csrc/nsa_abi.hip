@@ -6,6 +6,7 @@
 
 #include "../../include/nsa_hip.h"
 #include "nsa_attn.h"
+#include "nsa_attn_bwd_dkdv.h"
 #include "nsa_kernels.h"
 
 using namespace nsa;
@@ -40,15 +41,16 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Shape {
   int br, dtype, Z, H, G, Tq, Tkv, dk, dv, nslots, lprime;
+  int window = 0;
   int hpg() const { return H / G; }
   int Tp() const { return ((Tkv + 63) / 64) * 64 + 64; }
   int esz() const { return dtype == NSA_F32 ? 4 : 2; }
   int nblk() const { return br == kSelection ? (Tkv + lprime - 1) / lprime : 0; }
   int nsubblk() const { return (lprime + 63) / 64; }
+  // dK/dV work items per (b, g): key tiles x query segments
   int items_per_bg() const {
-    if (br == kCompression) return ((Tkv + 63) / 64) * ((Tq + kSegT - 1) / kSegT);
     if (br == kSelection) return nsubblk() * (nblk() + (int)(((int64_t)Tq * nslots + kSegT - 1) / kSegT));
-    return 0;
+    return ((Tkv + 63) / 64) * dkdv_nseg(br, Tq, window);
   }
 };
 
@@ -87,15 +89,18 @@ Layout make_layout(const Shape& s, bool bwd) {
       L.csr_t = take(BG * s.Tq * s.nslots * 4);
     }
   }
-  if (bwd && s.br != kSliding) L.partial = take(BG * s.items_per_bg() * 64 * (size_t)(s.dk + s.dv) * 4);
+  if (bwd) L.partial = take(BG * s.items_per_bg() * 64 * (size_t)(s.dk + s.dv) * 4);
   L.total = off;
   return L;
 }
 
-bool row_ok(const void* p, int64_t inner, int64_t s0, int64_t s1, int64_t s2, int esz) {
+// Unit feature stride and 16-byte aligned rows; the strides of size-1 axes are
+// never used to address memory, so they are not checked.
+bool row_ok(const void* p, int64_t inner, int64_t s0, int64_t s1, int64_t s2, int esz, int n0 = 2, int n1 = 2,
+            int n2 = 2) {
   if (inner != 1) return false;
   if (((uintptr_t)p) % 16) return false;
-  return (s0 * esz) % 16 == 0 && (s1 * esz) % 16 == 0 && (s2 * esz) % 16 == 0;
+  return (n0 == 1 || (s0 * esz) % 16 == 0) && (n1 == 1 || (s1 * esz) % 16 == 0) && (n2 == 1 || (s2 * esz) % 16 == 0);
 }
 
 int validate(const Shape& s) {
@@ -147,9 +152,9 @@ int run_fwd(const Shape& s, const FwdIO& io, float scale, int window, const int3
             const int64_t* sidx, int idx64, int fallback, int causal, void* ws, size_t ws_bytes, hipStream_t st) {
   int rc = validate(s);
   if (rc) return rc;
-  if (!row_ok(io.Q, io.sq[3], io.sq[0], io.sq[1], io.sq[2], s.esz()))
+  if (!row_ok(io.Q, io.sq[3], io.sq[0], io.sq[1], io.sq[2], s.esz(), s.Z, s.H, s.Tq))
     return fail(NSA_ERR_LAYOUT, "Q needs unit feature stride and 16-byte aligned rows");
-  if (!row_ok(io.Out, io.so[3], io.so[0], io.so[1], io.so[2], s.esz()))
+  if (!row_ok(io.Out, io.so[3], io.so[0], io.so[1], io.so[2], s.esz(), s.Z, s.H, s.Tq))
     return fail(NSA_ERR_LAYOUT, "Out needs unit feature stride and 16-byte aligned rows");
   if (s.br == kSliding && window <= 0) return fail(NSA_ERR_INVALID, "window_size=%d must be positive", window);
   const Layout L = make_layout(s, false);
@@ -207,11 +212,11 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
             const int64_t* sidx, int idx64, int fallback, int causal, void* ws, size_t ws_bytes, hipStream_t st) {
   int rc = validate(s);
   if (rc) return rc;
-  if (!row_ok(io.Q, io.sq[3], io.sq[0], io.sq[1], io.sq[2], s.esz()))
+  if (!row_ok(io.Q, io.sq[3], io.sq[0], io.sq[1], io.sq[2], s.esz(), s.Z, s.H, s.Tq))
     return fail(NSA_ERR_LAYOUT, "Q needs unit feature stride and 16-byte aligned rows");
-  if (!row_ok(io.dOut, io.so[3], io.so[0], io.so[1], io.so[2], s.esz()))
+  if (!row_ok(io.dOut, io.so[3], io.so[0], io.so[1], io.so[2], s.esz(), s.Z, s.H, s.Tq))
     return fail(NSA_ERR_LAYOUT, "dOut (Out strides) needs unit feature stride and 16-byte aligned rows");
-  if (!row_ok(io.dQ, io.sdq[3], io.sdq[0], io.sdq[1], io.sdq[2], s.esz()))
+  if (!row_ok(io.dQ, io.sdq[3], io.sdq[0], io.sdq[1], io.sdq[2], s.esz(), s.Z, s.H, s.Tq))
     return fail(NSA_ERR_LAYOUT, "dQ needs unit feature stride and 16-byte aligned rows");
   if (s.br == kSliding && window <= 0) return fail(NSA_ERR_INVALID, "window_size=%d must be positive", window);
   const Layout L = make_layout(s, true);
@@ -263,7 +268,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.lse2 = at<float>(ws, L.lse2);
   a.delta = at<float>(ws, L.delta);
   a.items_per_bg = s.items_per_bg();
-  if (L.partial || s.br != kSliding) a.partial = at<float>(ws, L.partial);
+  a.partial = at<float>(ws, L.partial);
 
   launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp,
                 at<char>(ws, L.kt), at<char>(ws, L.kn), st);
@@ -291,10 +296,11 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
     if (!dispatch_attn_bwd_dkdv(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no dK/dV kernel");
   }
   if ((rc = check_hip("dK/dV kernel"))) return rc;
-  if (s.br != kSliding) {
-    { TimingScope ts(kIdReduce, st); launch_partial_reduce(s.dtype, s.dk, s.dv, s.br, a, st); }
-    if ((rc = check_hip("dK/dV reduce"))) return rc;
+  {
+    TimingScope ts(kIdReduce, st);
+    launch_partial_reduce(s.dtype, s.dk, s.dv, s.br, a, st);
   }
+  if ((rc = check_hip("dK/dV reduce"))) return rc;
   return NSA_OK;
 }
 
@@ -317,8 +323,8 @@ size_t nsa_fwd_workspace_size(int branch, int dtype, int Z, int H, int G, int Tq
   return make_layout(s, false).total;
 }
 size_t nsa_bwd_workspace_size(int branch, int dtype, int Z, int H, int G, int Tq, int Tkv, int dk, int dv, int nslots,
-                              int lprime) {
-  Shape s{branch, dtype, Z, H, G, Tq, Tkv, dk, dv, nslots, lprime > 0 ? lprime : 64};
+                              int lprime, int window_size) {
+  Shape s{branch, dtype, Z, H, G, Tq, Tkv, dk, dv, nslots, lprime > 0 ? lprime : 64, window_size > 0 ? window_size : 1};
   if (G <= 0 || H % G) return 0;
   return make_layout(s, true).total;
 }
@@ -346,7 +352,7 @@ int nsa_sliding_window_fwd(const void* Q, const void* K, const void* V, void* Ou
                            int window_size, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
                            size_t workspace_bytes, nsa_stream_t stream) {
   NSA_FWD_IO
-  Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64};
+  Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64, window_size};
   return run_fwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
                  (hipStream_t)stream);
 }
@@ -365,7 +371,7 @@ int nsa_sliding_window_bwd(const void* Q, const void* K, const void* V, const vo
                            int head_dim_qk, int head_dim_v, int dtype, void* workspace, size_t workspace_bytes,
                            nsa_stream_t stream) {
   NSA_BWD_IO
-  Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64};
+  Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64, window_size};
   return run_bwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
                  (hipStream_t)stream);
 }

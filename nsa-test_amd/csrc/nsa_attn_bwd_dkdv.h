@@ -1,0 +1,354 @@
+// dK / dV for the three NSA branches on gfx950 (key-major).
+//
+// A work item owns 64 keys of one (batch, KV group) -- 16 keys per wave, held in
+// registers as MFMA B operands -- and one segment of the query rows that can see them
+// (rows are (timestep, head) pairs of the group).  The rows are walked in chunks of
+// RC rows, staged in LDS row-major (operand of S = Q K^T and dP = dO V^T) and
+// transposed (operand of dK^T += Q^T dS and dV^T += dO^T P, whose reduction runs over
+// the rows).  The next chunk is loaded into registers while the current one is
+// computed, and the LDS stage is double-buffered, so each chunk costs one barrier.
+// Staging threads own pairs of adjacent rows, so every transposed LDS write stores
+// two rows at once, and the transposed row pitch (RC + 4) keeps those writes free of
+// bank conflicts.
+//
+// Every item writes its fp32 dK/dV partial for its 64 keys; a reduce kernel sums the
+// segments of each key tile in a fixed order and accumulates into the caller's dK/dV.
+// No floating-point atomics: the result is bit-reproducible.
+//
+// Backward algebra (reference nsa/kernels.py:1303-1530): with s = scale q.k,
+//   p = exp(s - M - L),  dS = p (dO.v - D),  dK = scale dS^T Q,  dV = p^T dO.
+#pragma once
+#include "nsa_attn.h"
+#include "nsa_device.h"
+
+namespace nsa {
+
+// number of query segments per key tile (sliding and compression items)
+__host__ __device__ inline int dkdv_nseg(int br, int Tq, int window) {
+  if (br == kSliding) {
+    const int span = min(window + 63, Tq + 63);
+    return (span + kSegT - 1) / kSegT;
+  }
+  return (Tq + kSegT - 1) / kSegT;
+}
+
+// the two-row transposed store of one staged 16-byte piece
+template <typename S> struct PairT;
+template <> struct PairT<uint16_t> {
+  // element u of rows (r, r+1) -> one dword at dst[(e+u)*RP + r]
+  __device__ __forceinline__ static void store(uint16_t* dst, int RP, const uint4& a, const uint4& b) {
+    const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
+    const uint32_t wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      *reinterpret_cast<uint32_t*>(dst + (2 * w) * RP) = (wa[w] & 0xffffu) | (wb[w] << 16);
+      *reinterpret_cast<uint32_t*>(dst + (2 * w + 1) * RP) = (wa[w] >> 16) | (wb[w] & 0xffff0000u);
+    }
+  }
+};
+template <> struct PairT<float> {
+  __device__ __forceinline__ static void store(float* dst, int RP, const uint4& a, const uint4& b) {
+    *reinterpret_cast<uint2*>(dst + 0 * RP) = make_uint2(a.x, b.x);
+    *reinterpret_cast<uint2*>(dst + 1 * RP) = make_uint2(a.y, b.y);
+    *reinterpret_cast<uint2*>(dst + 2 * RP) = make_uint2(a.z, b.z);
+    *reinterpret_cast<uint2*>(dst + 3 * RP) = make_uint2(a.w, b.w);
+  }
+};
+
+template <typename T, int DK, int DV, int BR>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
+  using S = typename Store<T>::type;
+  constexpr int EPF = Elem<T>::kPerFrag;
+  constexpr int KC = Elem<T>::kKChunk;
+  constexpr int NKC = DK / KC;
+  constexpr int NVC = DV / KC;
+  constexpr int RC = sizeof(S) == 4 ? 16 : kRowChunk;  // fp32 stages half the rows (LDS)
+  constexpr int QP = DK + EPF;
+  constexpr int OP = DV + EPF;
+  constexpr int RP = RC + 4;
+  constexpr int CK = CFrag<T>::kKeys;
+  constexpr int CT = CK / 16;
+  constexpr int RPAIRS = RC / 2;
+  constexpr int QPC = RPAIRS * (DK / EPF);  // two-row pieces of one Q chunk
+  constexpr int OPC = RPAIRS * (DV / EPF);
+  constexpr int NQ = (QPC + 255) / 256;
+  constexpr int NO = (OPC + 255) / 256;
+  static_assert(RC % CK == 0, "row chunk");
+
+  __shared__ __attribute__((aligned(16))) S Qs[2][RC * QP];
+  __shared__ __attribute__((aligned(16))) S QTs[2][DK * RP];
+  __shared__ __attribute__((aligned(16))) S Os[2][RC * OP];
+  __shared__ __attribute__((aligned(16))) S OTs[2][DV * RP];
+  __shared__ int s_t[2][RC];
+  __shared__ float s_l2[2][RC];
+  __shared__ float s_dl[2][RC];
+  __shared__ int s_be[64];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int g4 = lane >> 4;
+  const int c16 = lane & 15;
+  const int bg = blockIdx.y;
+  const int b = bg / a.G;
+  const int grp = bg % a.G;
+  const int hpg = a.hpg;
+  const IntDiv hdiv = IntDiv::make(hpg);
+  const float scale2 = a.scale * kLog2e;
+  const int item = blockIdx.x;
+
+  // ---- decode the work item: key tile + segment of rows ----
+  int key0, blk_hi = a.Tkv;
+  int f_lo, f_hi;              // flattened row range (row f -> (t, head))
+  const int* tlist = nullptr;  // selection: row f -> t = tlist[f / hpg]
+  if (BR == kSliding) {
+    const int nseg = dkdv_nseg(kSliding, a.Tq, a.window);
+    const int tile = item / nseg, seg = item % nseg;
+    key0 = tile * 64;
+    const int t_lo = key0 + seg * kSegT;
+    const int t_hi = min(a.Tq, min(key0 + (seg + 1) * kSegT, key0 + 63 + a.window));
+    f_lo = t_lo * hpg;
+    f_hi = t_hi > t_lo ? t_hi * hpg : f_lo;
+  } else if (BR == kCompression) {
+    const int nseg = dkdv_nseg(kCompression, a.Tq, 0);
+    const int tile = item / nseg, seg = item % nseg;
+    key0 = tile * 64;
+    if (tid < 64) {
+      const int key = key0 + tid;
+      s_be[tid] = key < a.Tkv ? a.block_ends[key] : 0x7fffffff;
+    }
+    __syncthreads();
+    int be_min = s_be[lane];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) be_min = min(be_min, __shfl_xor(be_min, o));
+    const int t_lo = max(seg * kSegT, max(be_min, 0));
+    const int t_hi = min(a.Tq, (seg + 1) * kSegT);
+    f_lo = t_lo * hpg;
+    f_hi = t_hi > t_lo ? t_hi * hpg : f_lo;
+  } else {
+    const int nsubblk = (a.lprime + 63) / 64;
+    const int sidx = item / nsubblk, sub = item % nsubblk;
+    const int* so = a.seg_off + (int64_t)bg * (a.nblk + 1);
+    if (sidx >= so[a.nblk]) return;  // beyond this group's work list (uniform)
+    int lo = 0, hi = a.nblk;         // largest j with so[j] <= sidx
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (so[mid] <= sidx) lo = mid;
+      else hi = mid;
+    }
+    const int j = lo;
+    const int k = sidx - so[j];
+    const int* co = a.csr_off + (int64_t)bg * (a.nblk + 1);
+    const int e_lo = co[j] + k * kSegT;
+    const int e_hi = min(co[j + 1], e_lo + kSegT);
+    tlist = a.csr_t + (int64_t)bg * a.Tq * a.nslots;
+    key0 = j * a.lprime + sub * 64;
+    blk_hi = min(j * a.lprime + a.lprime, a.Tkv);
+    f_lo = e_lo * hpg;
+    f_hi = e_hi * hpg;
+    if (key0 >= blk_hi) return;  // sub-tile past the sequence end: no partial is read
+  }
+
+  // ---- this wave's 16 keys: K and V rows as B operands, kept in registers ----
+  const S* kt = reinterpret_cast<const S*>(a.kt) + (int64_t)bg * a.Tp * DK;
+  const S* vn = reinterpret_cast<const S*>(a.vn) + (int64_t)bg * a.Tp * DV;
+  const int kw0 = key0 + wave * 16;
+  const int mykey = kw0 + c16;
+  uint4 kf[NKC], vf[NVC];
+#pragma unroll
+  for (int kc = 0; kc < NKC; ++kc)
+    kf[kc] = *reinterpret_cast<const uint4*>(kt + (int64_t)mykey * DK + kc * KC + g4 * EPF);
+#pragma unroll
+  for (int kc = 0; kc < NVC; ++kc)
+    vf[kc] = *reinterpret_cast<const uint4*>(vn + (int64_t)mykey * DV + kc * KC + g4 * EPF);
+  int mybe = 0x7fffffff, wave_be_min = 0x7fffffff, wave_be_max = 0x7fffffff;
+  if (BR == kCompression) {
+    mybe = s_be[wave * 16 + c16];
+    wave_be_min = mybe;
+    wave_be_max = mybe;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      wave_be_min = min(wave_be_min, __shfl_xor(wave_be_min, o));
+      wave_be_max = max(wave_be_max, __shfl_xor(wave_be_max, o));
+    }
+  }
+
+  f32x4 dka[DK / 16], dva[DV / 16];
+#pragma unroll
+  for (int j = 0; j < DK / 16; ++j) dka[j] = zero4();
+#pragma unroll
+  for (int j = 0; j < DV / 16; ++j) dva[j] = zero4();
+
+  const S* qbase = reinterpret_cast<const S*>(a.q) + b * a.sq_b;
+  const S* obase = reinterpret_cast<const S*>(a.dout) + b * a.sdo_b;
+  auto row_t = [&](int f) -> int {
+    const int e = hdiv.div(f);
+    return tlist ? tlist[e] : e;
+  };
+
+  // ---- register prefetch of one chunk (pairs of adjacent rows) ----
+  uint4 pq[NQ][2], po[NO][2];
+  int pr_t = -1;
+  float pr_l2 = INFINITY, pr_dl = 0.f;
+  auto load_rows = [&](int f, const S* base, int64_t sh, int64_t st, int e, uint4& dst) {
+    dst = make_uint4(0, 0, 0, 0);
+    if (f < f_hi) {
+      const int t = row_t(f);
+      const int h = grp * hpg + hdiv.mod(f);
+      dst = *reinterpret_cast<const uint4*>(base + (int64_t)h * sh + (int64_t)t * st + e);
+    }
+  };
+  auto load_chunk = [&](int fc) {
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int c = tid + 256 * j;
+      if (c < QPC) {
+        const int rp = c % RPAIRS;
+        const int e = (c / RPAIRS) * EPF;
+        load_rows(fc + 2 * rp, qbase, a.sq_h, a.sq_t, e, pq[j][0]);
+        load_rows(fc + 2 * rp + 1, qbase, a.sq_h, a.sq_t, e, pq[j][1]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+      const int c = tid + 256 * j;
+      if (c < OPC) {
+        const int rp = c % RPAIRS;
+        const int e = (c / RPAIRS) * EPF;
+        load_rows(fc + 2 * rp, obase, a.sdo_h, a.sdo_t, e, po[j][0]);
+        load_rows(fc + 2 * rp + 1, obase, a.sdo_h, a.sdo_t, e, po[j][1]);
+      }
+    }
+    if (tid < RC) {
+      const int f = fc + tid;
+      pr_t = -1;
+      pr_l2 = INFINITY;
+      pr_dl = 0.f;
+      if (f < f_hi) {
+        pr_t = row_t(f);
+        const int h = grp * hpg + hdiv.mod(f);
+        const int64_t srow = ((int64_t)b * a.H + h) * a.Tq + pr_t;
+        pr_l2 = a.lse2[srow];
+        pr_dl = a.delta[srow];
+      }
+    }
+  };
+  auto store_chunk = [&](int buf) {
+#pragma unroll
+    for (int j = 0; j < NQ; ++j) {
+      const int c = tid + 256 * j;
+      if (c < QPC) {
+        const int rp = c % RPAIRS;
+        const int e = (c / RPAIRS) * EPF;
+        *reinterpret_cast<uint4*>(&Qs[buf][(2 * rp) * QP + e]) = pq[j][0];
+        *reinterpret_cast<uint4*>(&Qs[buf][(2 * rp + 1) * QP + e]) = pq[j][1];
+        PairT<S>::store(&QTs[buf][e * RP + 2 * rp], RP, pq[j][0], pq[j][1]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+      const int c = tid + 256 * j;
+      if (c < OPC) {
+        const int rp = c % RPAIRS;
+        const int e = (c / RPAIRS) * EPF;
+        *reinterpret_cast<uint4*>(&Os[buf][(2 * rp) * OP + e]) = po[j][0];
+        *reinterpret_cast<uint4*>(&Os[buf][(2 * rp + 1) * OP + e]) = po[j][1];
+        PairT<S>::store(&OTs[buf][e * RP + 2 * rp], RP, po[j][0], po[j][1]);
+      }
+    }
+    if (tid < RC) {
+      s_t[buf][tid] = pr_t;
+      s_l2[buf][tid] = pr_l2;
+      s_dl[buf][tid] = pr_dl;
+    }
+  };
+
+  const int nchunks = (f_hi - f_lo + RC - 1) / RC;
+  if (nchunks > 0) load_chunk(f_lo);
+  for (int c = 0; c < nchunks; ++c) {
+    const int buf = c & 1;
+    const int fc = f_lo + c * RC;
+    store_chunk(buf);
+    if (c + 1 < nchunks) load_chunk(fc + RC);
+    __syncthreads();
+
+    // rows are in ascending t, so the chunk spans [t_min, t_max]
+    const bool full = fc + RC <= f_hi;
+    const int t_min = row_t(fc);
+    const int t_max = row_t(min(fc + RC, f_hi) - 1);
+    bool active, all_visible;
+    if (BR == kSliding) {
+      active = kw0 <= t_max && kw0 + 15 > t_min - a.window;
+      all_visible = full && kw0 + 15 <= t_min && kw0 > t_max - a.window && kw0 + 15 < a.Tkv;
+    } else if (BR == kCompression) {
+      active = wave_be_min <= t_max;
+      all_visible = full && wave_be_max <= t_min;
+    } else {
+      active = (!a.causal || kw0 <= t_max) && kw0 < blk_hi;
+      all_visible = full && (!a.causal || kw0 + 15 <= t_min) && kw0 + 15 < blk_hi;
+    }
+
+    if (active) {
+      f32x4 pt[RC / 16], dst[RC / 16];
+#pragma unroll
+      for (int rs = 0; rs < RC / 16; ++rs) {
+        f32x4 sacc = zero4(), pacc = zero4();
+        const S* qrow = &Qs[buf][(rs * 16 + c16) * QP];
+        const S* orow = &Os[buf][(rs * 16 + c16) * OP];
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) sacc = Mma<T>::run(sacc, frag_std<T>(qrow + kc * KC, g4), kf[kc]);
+#pragma unroll
+        for (int kc = 0; kc < NVC; ++kc) pacc = Mma<T>::run(pacc, frag_std<T>(orow + kc * KC, g4), vf[kc]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = rs * 16 + 4 * g4 + i;
+          float p;
+          if (all_visible) {
+            p = fast_exp2(sacc[i] * scale2 - s_l2[buf][r]);
+          } else {
+            const int t = s_t[buf][r];
+            bool ok;
+            if (BR == kSliding) ok = t >= 0 && mykey <= t && mykey > t - a.window && mykey < a.Tkv;
+            else if (BR == kCompression) ok = t >= 0 && mybe <= t;
+            else ok = t >= 0 && (!a.causal || mykey <= t) && mykey < blk_hi;
+            p = ok ? fast_exp2(sacc[i] * scale2 - s_l2[buf][r]) : 0.f;
+          }
+          pt[rs][i] = p;
+          dst[rs][i] = p * (pacc[i] - s_dl[buf][r]);
+        }
+      }
+#pragma unroll
+      for (int kc2 = 0; kc2 < RC / CK; ++kc2) {
+        const uint4 pf = CFrag<T>::pack(pt[kc2 * CT], pt[kc2 * CT + CT - 1]);
+        const uint4 sf = CFrag<T>::pack(dst[kc2 * CT], dst[kc2 * CT + CT - 1]);
+#pragma unroll
+        for (int j = 0; j < DV / 16; ++j)
+          dva[j] = Mma<T>::run(dva[j], frag_cperm<T>(&OTs[buf][(j * 16 + c16) * RP + kc2 * CK], g4), pf);
+#pragma unroll
+        for (int j = 0; j < DK / 16; ++j)
+          dka[j] = Mma<T>::run(dka[j], frag_cperm<T>(&QTs[buf][(j * 16 + c16) * RP + kc2 * CK], g4), sf);
+      }
+    }
+  }
+
+  // ---- write this item's partial: lane holds dK^T[d = 16j + 4*g4 + i][key = mykey] ----
+  float* pp = a.partial + ((int64_t)bg * a.items_per_bg + item) * 64 * (DK + DV) +
+              (int64_t)(wave * 16 + c16) * (DK + DV);
+#pragma unroll
+  for (int j = 0; j < DK / 16; ++j) {
+    const f32x4 v = dka[j] * a.scale;
+    *reinterpret_cast<float4*>(pp + j * 16 + 4 * g4) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+#pragma unroll
+  for (int j = 0; j < DV / 16; ++j)
+    *reinterpret_cast<float4*>(pp + DK + j * 16 + 4 * g4) = make_float4(dva[j][0], dva[j][1], dva[j][2], dva[j][3]);
+}
+
+template <typename T, int DK, int DV, int BR>
+void launch_attn_bwd_dkdv(const AttnArgs& a, hipStream_t s) {
+  if (a.items_per_bg <= 0) return;
+  dim3 grid(a.items_per_bg, a.B * a.G);
+  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, DK, DV, BR>), grid, dim3(256), 0, s, a);
+}
+
+}  // namespace nsa

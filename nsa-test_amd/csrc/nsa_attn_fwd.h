@@ -21,6 +21,7 @@
 #pragma once
 #include "nsa_attn.h"
 #include "nsa_device.h"
+#include "nsa_attn_sel.h"
 
 namespace nsa {
 
@@ -69,11 +70,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   int colh[NSUB];
   bool colv[NSUB];
   int sub_t0[NSUB], sub_t1[NSUB];
+  bool f0_full[NSUB];
   uint4 qf[NSUB][NKC];
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) {
     const int f0 = col_base + (wave * NSUB + s) * 16;
     const int f = f0 + c16;
+    f0_full[s] = f0 + 16 <= ncols;
     colv[s] = f < ncols;
     colt[s] = colv[s] ? f / hpg : 0;
     colh[s] = colv[s] ? grp * hpg + f % hpg : 0;
@@ -176,11 +179,15 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    int be_min = 0;
+    int be_min = 0, be_max = 0;
     if (BR == kCompression) {
       be_min = s_be[lane];
+      be_max = be_min;
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) be_min = min(be_min, __shfl_xor(be_min, o));
+      for (int o = 1; o < 64; o <<= 1) {
+        be_min = min(be_min, __shfl_xor(be_min, o));
+        be_max = max(be_max, __shfl_xor(be_max, o));
+      }
     }
 
 #pragma unroll
@@ -216,44 +223,64 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       }
 
       const int t = colt[s];
+      // interior tiles (every key visible to every column of the subtile) skip masking
+      bool all_visible = false;
+      if (BR == kSliding)
+        all_visible = f0_full[s] && key0 + 63 <= sub_t0[s] && key0 > sub_t1[s] - a.window && key0 + 63 < a.Tkv;
+      else if (BR == kCompression)
+        all_visible = f0_full[s] && be_max <= sub_t0[s];
       float mx = -INFINITY;
+      if (all_visible) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+        for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int key = key0 + ks * 16 + 4 * g4 + i;
-          bool ok;
-          if (BR == kSliding) {
-            ok = colv[s] && key <= t && key > t - a.window && key < a.Tkv;
-          } else if (BR == kCompression) {
-            ok = colv[s] && s_be[ks * 16 + 4 * g4 + i] <= t;
-          } else {
-            ok = colsel && (!a.causal || key <= t) && key < blk_hi;
+          for (int i = 0; i < 4; ++i) {
+            st[ks][i] *= scale2;
+            mx = fmaxf(mx, st[ks][i]);
           }
-          const float v = ok ? st[ks][i] * scale2 : -INFINITY;
-          st[ks][i] = v;
-          mx = fmaxf(mx, v);
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = key0 + ks * 16 + 4 * g4 + i;
+            bool ok;
+            if (BR == kSliding) {
+              ok = colv[s] && key <= t && key > t - a.window && key < a.Tkv;
+            } else if (BR == kCompression) {
+              ok = colv[s] && s_be[ks * 16 + 4 * g4 + i] <= t;
+            } else {
+              ok = colsel && (!a.causal || key <= t) && key < blk_hi;
+            }
+            const float v = ok ? st[ks][i] * scale2 : -INFINITY;
+            st[ks][i] = v;
+            mx = fmaxf(mx, v);
+          }
         }
       }
       mx = wave_max16(mx);
       const float mnew = fmaxf(m2[s], mx);
       const float mref = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = exp2f(m2[s] - mref);
       float rs = 0.f;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = exp2f(st[ks][i] - mref);
+          const float p = fast_exp2(st[ks][i] - mref);
           st[ks][i] = p;
           rs += p;
         }
       }
       rs = wave_sum16(rs);
-      lsum[s] = lsum[s] * alpha + rs;
-      m2[s] = mnew;
+      // rescale the running output only when some column's maximum moved
+      if (__ballot(mnew > m2[s]) != 0ull) {
+        const float alpha = fast_exp2(m2[s] - mref);
+        lsum[s] *= alpha;
 #pragma unroll
-      for (int j = 0; j < DV / 16; ++j) oacc[s][j] *= alpha;
+        for (int j = 0; j < DV / 16; ++j) oacc[s][j] *= alpha;
+      }
+      lsum[s] += rs;
+      m2[s] = mnew;
 
 #pragma unroll
       for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
@@ -290,7 +317,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 template <typename T, int DK, int DV, int BR>
 void launch_attn_fwd(const AttnArgs& a, hipStream_t s) {
   dim3 grid((a.Tq * a.hpg + kFwdCols - 1) / kFwdCols, a.B * a.G);
-  hipLaunchKernelGGL((attn_fwd_kernel<T, DK, DV, BR>), grid, dim3(256), 0, s, a);
+  if constexpr (BR == kSelection) {
+    launch_attn_sel_fwd<T, DK, DV>(a, s);  // per-wave selection kernel
+  } else {
+    hipLaunchKernelGGL((attn_fwd_kernel<T, DK, DV, BR>), grid, dim3(256), 0, s, a);
+  }
 }
 
 }  // namespace nsa

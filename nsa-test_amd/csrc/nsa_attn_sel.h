@@ -1,0 +1,332 @@
+// Top-n block selection attention, forward and dQ, on gfx950.
+//
+// Each wave is independent: it owns 16 query columns ((timestep, head) pairs of one
+// KV group; with 16 heads per group, one timestep) and walks the union of the blocks
+// its timesteps selected.  K and V fragments are read straight from the re-packed
+// group K/V (kt [T][dk], kn [dk][T], vt [dv][T], vn [T][dv]) into MFMA operand
+// registers -- no LDS staging and no workgroup barrier -- so a wave never waits for
+// blocks another wave's timesteps chose, and blocks shared by neighbouring timesteps
+// (the fixed initial / local blocks, correlated top-n) are served by L2.  Workgroups
+// are mapped XCD-contiguously so that neighbouring timesteps share an L2.
+//
+// Key j is visible to column (t, h) iff j lies in a block the row selected (the
+// cleaned, de-duplicated list), j < N_CTX_KV and (causal) j <= t
+// (reference nsa/reference.py:205-254).
+#pragma once
+#include "nsa_attn.h"
+#include "nsa_device.h"
+
+namespace nsa {
+
+constexpr int kSelWaveCols = 16;
+constexpr int kSelMaxT = 17;  // timesteps a 16-column group can touch (hpg = 1)
+
+// Workgroup id -> logical id such that each XCD (ids dispatched round-robin over 8)
+// receives a contiguous range of logical ids.
+__device__ __forceinline__ int xcd_contiguous(int i, int n) {
+  const int xcd = i & 7, k = i >> 3;
+  const int base = n >> 3, rem = n & 7;
+  return (xcd < rem ? xcd * (base + 1) : rem * (base + 1) + (xcd - rem) * base) + k;
+}
+
+// Per-wave bookkeeping: the timesteps of the wave's columns, their cleaned lists and
+// the union bitmap of their blocks.
+struct SelWave {
+  int t_first, nt;
+};
+
+template <typename T, bool DQ>
+__device__ __forceinline__ void sel_wave_setup(const AttnArgs& a, int bg, int f0, int* lst, uint32_t* bits,
+                                               SelWave& w, int lane) {
+  const int ncols = a.Tq * a.hpg;
+  const int flast = min(f0 + kSelWaveCols, ncols) - 1;
+  w.t_first = f0 / a.hpg;
+  w.nt = flast / a.hpg - w.t_first + 1;
+  const int nwords = (a.nblk + 31) / 32;
+  for (int i = lane; i < nwords; i += 64) bits[i] = 0;
+  __builtin_amdgcn_wave_barrier();
+  const int* selrow = a.sel + ((int64_t)bg * a.Tq + w.t_first) * a.nslots;
+  const int total = w.nt * a.nslots;
+  for (int i = lane; i < total; i += 64) {
+    const int v = selrow[i];
+    lst[i] = v;
+    if (v >= 0) atomicOr(&bits[v >> 5], 1u << (v & 31));
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+}
+
+// does the column's timestep select block `blk`? (its list is ascending, -1 padded)
+__device__ __forceinline__ bool sel_has(const int* l, int nslots, int blk) {
+  bool has = false;
+  for (int j = 0; j < nslots; ++j) {
+    const int v = l[j];
+    if (v == blk) has = true;
+    if (v < 0 || v >= blk) break;
+  }
+  return has;
+}
+
+// ============================================================== forward
+template <typename T, int DK, int DV>
+__global__ __launch_bounds__(256) void attn_sel_fwd_kernel(AttnArgs a, int ncoltiles) {
+  using S = typename Store<T>::type;
+  constexpr int EPF = Elem<T>::kPerFrag;
+  constexpr int KC = Elem<T>::kKChunk;
+  constexpr int NKC = DK / KC;
+  constexpr int CK = CFrag<T>::kKeys;
+  constexpr int CT = CK / 16;
+  __shared__ int s_lst[4][kSelMaxT * 64];
+  __shared__ uint32_t s_bits[4][kSelMaxBlocks / 32];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g4 = lane >> 4, c16 = lane & 15;
+  const int L = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int bg = L / ncoltiles;
+  const int b = bg / a.G, grp = bg % a.G;
+  const int hpg = a.hpg;
+  const int ncols = a.Tq * hpg;
+  const int f0 = (L % ncoltiles) * 64 + wave * kSelWaveCols;
+  if (f0 >= ncols) return;  // whole wave idle (no barriers below)
+  const float scale2 = a.scale * kLog2e;
+
+  SelWave w;
+  int* lst = s_lst[wave];
+  uint32_t* bits = s_bits[wave];
+  sel_wave_setup<T, false>(a, bg, f0, lst, bits, w, lane);
+
+  const int f = f0 + c16;
+  const bool colv = f < ncols;
+  const int colt = colv ? f / hpg : w.t_first;
+  const int colh = colv ? grp * hpg + f % hpg : grp * hpg;
+  const int t_last = w.t_first + w.nt - 1;
+  const int* mylst = lst + (colt - w.t_first) * a.nslots;
+
+  const S* qp = reinterpret_cast<const S*>(a.q) + b * a.sq_b + (int64_t)colh * a.sq_h + (int64_t)colt * a.sq_t;
+  uint4 qf[NKC];
+#pragma unroll
+  for (int kc = 0; kc < NKC; ++kc)
+    qf[kc] = colv ? *reinterpret_cast<const uint4*>(qp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
+
+  const S* kt = reinterpret_cast<const S*>(a.kt) + (int64_t)bg * a.Tp * DK;
+  const S* vt = reinterpret_cast<const S*>(a.vt) + (int64_t)bg * DV * a.Tp;
+  f32x4 oacc[DV / 16];
+#pragma unroll
+  for (int j = 0; j < DV / 16; ++j) oacc[j] = zero4();
+  float m2 = -INFINITY, lsum = 0.f;
+  const int nsub = (a.lprime + 63) / 64;
+  const int nwords = (a.nblk + 31) / 32;
+  const bool one_t = w.nt == 1;
+
+  for (int wd = 0; wd < nwords; ++wd) {
+    uint32_t word = bits[wd];
+    while (word) {
+      const int blk = wd * 32 + __builtin_ctz(word);
+      word &= word - 1;
+      const int blk_lo = blk * a.lprime;
+      const int blk_hi = min(blk_lo + a.lprime, a.Tkv);
+      const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
+      for (int sb = 0; sb < nsub; ++sb) {
+        const int key0 = blk_lo + sb * 64;
+        if (key0 >= blk_hi || (a.causal && key0 > t_last)) break;
+        // S^T[key, col] for the 64 keys of this tile
+        f32x4 st[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const S* krow = kt + (int64_t)(key0 + ks * 16 + c16) * DK;
+          st[ks] = zero4();
+#pragma unroll
+          for (int kc = 0; kc < NKC; ++kc)
+            st[ks] = Mma<T>::run(st[ks], *reinterpret_cast<const uint4*>(krow + kc * KC + g4 * EPF), qf[kc]);
+        }
+        const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 + 63 < blk_hi &&
+                                 f0 + kSelWaveCols <= ncols;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = key0 + ks * 16 + 4 * g4 + i;
+            const bool ok = all_visible || (colsel && (!a.causal || key <= colt) && key < blk_hi);
+            const float v = ok ? st[ks][i] * scale2 : -INFINITY;
+            st[ks][i] = v;
+            mx = fmaxf(mx, v);
+          }
+        mx = wave_max16(mx);
+        const float mnew = fmaxf(m2, mx);
+        const float mref = mnew == -INFINITY ? 0.f : mnew;
+        float rs = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = fast_exp2(st[ks][i] - mref);
+            st[ks][i] = p;
+            rs += p;
+          }
+        rs = wave_sum16(rs);
+        if (__ballot(mnew > m2) != 0ull) {
+          const float alpha = fast_exp2(m2 - mref);
+          lsum *= alpha;
+#pragma unroll
+          for (int j = 0; j < DV / 16; ++j) oacc[j] *= alpha;
+        }
+        lsum += rs;
+        m2 = mnew;
+#pragma unroll
+        for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
+          const uint4 pf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
+#pragma unroll
+          for (int j = 0; j < DV / 16; ++j) {
+            const uint4 vf = frag_cperm<T>(vt + (int64_t)(j * 16 + c16) * a.Tp + key0 + kc2 * CK, g4);
+            oacc[j] = Mma<T>::run(oacc[j], vf, pf);
+          }
+        }
+      }
+    }
+  }
+
+  if (colv) {
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    S* op = reinterpret_cast<S*>(a.o) + b * a.so_b + (int64_t)colh * a.so_h + (int64_t)colt * a.so_t;
+#pragma unroll
+    for (int j = 0; j < DV / 16; ++j) store4<T>(op + j * 16 + 4 * g4, oacc[j] * inv);
+    if (g4 == 0) {
+      if (a.L)
+        a.L[b * a.sl_b + (int64_t)colh * a.sl_h + (int64_t)colt * a.sl_t] = lsum > 0.f ? logf(lsum) : -INFINITY;
+      if (a.M) a.M[b * a.sm_b + (int64_t)colh * a.sm_h + (int64_t)colt * a.sm_t] = m2 * kLn2;
+    }
+  }
+}
+
+template <typename T, int DK, int DV>
+void launch_attn_sel_fwd(const AttnArgs& a, hipStream_t s) {
+  const int ncoltiles = (a.Tq * a.hpg + 63) / 64;
+  hipLaunchKernelGGL((attn_sel_fwd_kernel<T, DK, DV>), dim3(ncoltiles * a.B * a.G), dim3(256), 0, s, a, ncoltiles);
+}
+
+// ============================================================== dQ
+template <typename T, int DK, int DV>
+__global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncoltiles) {
+  using S = typename Store<T>::type;
+  constexpr int EPF = Elem<T>::kPerFrag;
+  constexpr int KC = Elem<T>::kKChunk;
+  constexpr int NKC = DK / KC;
+  constexpr int NVC = DV / KC;
+  constexpr int CK = CFrag<T>::kKeys;
+  constexpr int CT = CK / 16;
+  __shared__ int s_lst[4][kSelMaxT * 64];
+  __shared__ uint32_t s_bits[4][kSelMaxBlocks / 32];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g4 = lane >> 4, c16 = lane & 15;
+  const int L = xcd_contiguous(blockIdx.x, gridDim.x);
+  const int bg = L / ncoltiles;
+  const int b = bg / a.G, grp = bg % a.G;
+  const int hpg = a.hpg;
+  const int ncols = a.Tq * hpg;
+  const int f0 = (L % ncoltiles) * 64 + wave * kSelWaveCols;
+  if (f0 >= ncols) return;
+  const float scale2 = a.scale * kLog2e;
+
+  SelWave w;
+  int* lst = s_lst[wave];
+  uint32_t* bits = s_bits[wave];
+  sel_wave_setup<T, true>(a, bg, f0, lst, bits, w, lane);
+
+  const int f = f0 + c16;
+  const bool colv = f < ncols;
+  const int colt = colv ? f / hpg : w.t_first;
+  const int colh = colv ? grp * hpg + f % hpg : grp * hpg;
+  const int t_last = w.t_first + w.nt - 1;
+  const int* mylst = lst + (colt - w.t_first) * a.nslots;
+
+  uint4 qf[NKC], dof[NVC];
+  {
+    const S* qp = reinterpret_cast<const S*>(a.q) + b * a.sq_b + (int64_t)colh * a.sq_h + (int64_t)colt * a.sq_t;
+    const S* dp = reinterpret_cast<const S*>(a.dout) + b * a.sdo_b + (int64_t)colh * a.sdo_h +
+                  (int64_t)colt * a.sdo_t;
+#pragma unroll
+    for (int kc = 0; kc < NKC; ++kc)
+      qf[kc] = colv ? *reinterpret_cast<const uint4*>(qp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int kc = 0; kc < NVC; ++kc)
+      dof[kc] = colv ? *reinterpret_cast<const uint4*>(dp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
+  }
+  const int64_t srow = ((int64_t)b * a.H + colh) * a.Tq + colt;
+  const float l2 = colv ? a.lse2[srow] : INFINITY;
+  const float dl = colv ? a.delta[srow] : 0.f;
+
+  const S* kt = reinterpret_cast<const S*>(a.kt) + (int64_t)bg * a.Tp * DK;
+  const S* kn = reinterpret_cast<const S*>(a.kn) + (int64_t)bg * DK * a.Tp;
+  const S* vn = reinterpret_cast<const S*>(a.vn) + (int64_t)bg * a.Tp * DV;
+  f32x4 dqa[DK / 16];
+#pragma unroll
+  for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
+  const int nsub = (a.lprime + 63) / 64;
+  const int nwords = (a.nblk + 31) / 32;
+  const bool one_t = w.nt == 1;
+
+  for (int wd = 0; wd < nwords; ++wd) {
+    uint32_t word = bits[wd];
+    while (word) {
+      const int blk = wd * 32 + __builtin_ctz(word);
+      word &= word - 1;
+      const int blk_lo = blk * a.lprime;
+      const int blk_hi = min(blk_lo + a.lprime, a.Tkv);
+      const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
+      for (int sb = 0; sb < nsub; ++sb) {
+        const int key0 = blk_lo + sb * 64;
+        if (key0 >= blk_hi || (a.causal && key0 > t_last)) break;
+        f32x4 st[4], dp[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const S* krow = kt + (int64_t)(key0 + ks * 16 + c16) * DK;
+          const S* vrow = vn + (int64_t)(key0 + ks * 16 + c16) * DV;
+          st[ks] = zero4();
+          dp[ks] = zero4();
+#pragma unroll
+          for (int kc = 0; kc < NKC; ++kc)
+            st[ks] = Mma<T>::run(st[ks], *reinterpret_cast<const uint4*>(krow + kc * KC + g4 * EPF), qf[kc]);
+#pragma unroll
+          for (int kc = 0; kc < NVC; ++kc)
+            dp[ks] = Mma<T>::run(dp[ks], *reinterpret_cast<const uint4*>(vrow + kc * KC + g4 * EPF), dof[kc]);
+        }
+        const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 + 63 < blk_hi &&
+                                 f0 + kSelWaveCols <= ncols;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = key0 + ks * 16 + 4 * g4 + i;
+            const bool ok = all_visible || (colsel && (!a.causal || key <= colt) && key < blk_hi);
+            const float p = ok ? fast_exp2(st[ks][i] * scale2 - l2) : 0.f;
+            st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
+          }
+#pragma unroll
+        for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
+          const uint4 sf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
+#pragma unroll
+          for (int j = 0; j < DK / 16; ++j) {
+            const uint4 kf = frag_cperm<T>(kn + (int64_t)(j * 16 + c16) * a.Tp + key0 + kc2 * CK, g4);
+            dqa[j] = Mma<T>::run(dqa[j], kf, sf);
+          }
+        }
+      }
+    }
+  }
+
+  if (colv) {
+    S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)colt * a.sdq_t;
+#pragma unroll
+    for (int j = 0; j < DK / 16; ++j) store4<T>(dqp + j * 16 + 4 * g4, dqa[j] * a.scale);
+  }
+}
+
+template <typename T, int DK, int DV>
+void launch_attn_sel_dq(const AttnArgs& a, hipStream_t s) {
+  const int ncoltiles = (a.Tq * a.hpg + 63) / 64;
+  hipLaunchKernelGGL((attn_sel_dq_kernel<T, DK, DV>), dim3(ncoltiles * a.B * a.G), dim3(256), 0, s, a, ncoltiles);
+}
+
+}  // namespace nsa

@@ -86,15 +86,19 @@ template <> struct CFrag<float> {
                       __float_as_uint(c0[3]));
   }
 };
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+// two floats -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 template <> struct CFrag<bf16> {
   static constexpr int kKeys = 32;
   // slots 0..3 <- tile c0 rows 4g+i ; slots 4..7 <- tile c1 rows 16+4g+i
   __device__ __forceinline__ static uint4 pack(f32x4 c0, f32x4 c1) {
-    uint32_t w0 = (uint32_t)f32_to_bf16_bits(c0[0]) | ((uint32_t)f32_to_bf16_bits(c0[1]) << 16);
-    uint32_t w1 = (uint32_t)f32_to_bf16_bits(c0[2]) | ((uint32_t)f32_to_bf16_bits(c0[3]) << 16);
-    uint32_t w2 = (uint32_t)f32_to_bf16_bits(c1[0]) | ((uint32_t)f32_to_bf16_bits(c1[1]) << 16);
-    uint32_t w3 = (uint32_t)f32_to_bf16_bits(c1[2]) | ((uint32_t)f32_to_bf16_bits(c1[3]) << 16);
-    return make_uint4(w0, w1, w2, w3);
+    return make_uint4(pack_bf16x2(c0[0], c0[1]), pack_bf16x2(c0[2], c0[3]), pack_bf16x2(c1[0], c1[1]),
+                      pack_bf16x2(c1[2], c1[3]));
   }
 };
 
@@ -135,9 +139,24 @@ template <> __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
   *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
 }
 template <> __device__ __forceinline__ void store4<bf16>(uint16_t* p, f32x4 v) {
-  uint32_t w0 = (uint32_t)f32_to_bf16_bits(v[0]) | ((uint32_t)f32_to_bf16_bits(v[1]) << 16);
-  uint32_t w1 = (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16);
-  *reinterpret_cast<uint2*>(p) = make_uint2(w0, w1);
+  *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
+
+// 2^x on the transcendental unit (v_exp_f32); exp2(-inf) = 0.  Inputs here are <= 0,
+// results below the normal range may flush, which the softmax tolerates.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// n / d and n % d for non-negative 32-bit n, with a shift when d is a power of two
+struct IntDiv {
+  int d, shift;  // shift < 0: d is not a power of two
+  __host__ __device__ static IntDiv make(int d_) {
+    IntDiv r{d_, -1};
+    for (int s = 0; s < 31; ++s)
+      if ((1 << s) == d_) r.shift = s;
+    return r;
+  }
+  __device__ __forceinline__ int div(int n) const { return shift >= 0 ? (n >> shift) : n / d; }
+  __device__ __forceinline__ int mod(int n) const { return shift >= 0 ? (n & (d - 1)) : n % d; }
+};
 
 }  // namespace nsa

@@ -88,17 +88,27 @@ __global__ __launch_bounds__(256) void pool_bwd_c_kernel(const typename Store<T>
                                                          const typename Store<T>::type* __restrict__ dR,
                                                          float* __restrict__ dC, int BG, int T_, int W, int l, int d,
                                                          int n_act) {
+  // 64 channels x 4 interleaved block groups per workgroup; the 4 group sums are
+  // combined in a fixed order
+  __shared__ float part[4][64];
   const int u = blockIdx.y;
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= W) return;
-  const float cu = Elem<T>::to_f32(C[(int64_t)u * W + c]);
+  const int cl = threadIdx.x & 63, ig = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + cl;
   float acc = 0.f;
-  for (int64_t bg = 0; bg < BG; ++bg)
-    for (int i = 0; i < n_act; ++i) {
-      const float y = Elem<T>::to_f32(Y[(bg * T_ + (int64_t)i * d + u) * W + c]);
-      if (y + cu > 0.f) acc += Elem<T>::to_f32(dR[(bg * n_act + i) * W + c]);
+  if (c < W) {
+    const float cu = Elem<T>::to_f32(C[(int64_t)u * W + c]);
+    for (int64_t bg = 0; bg < BG; ++bg) {
+#pragma unroll 4
+      for (int i = ig; i < n_act; i += 4) {
+        const float y = Elem<T>::to_f32(Y[(bg * T_ + (int64_t)i * d + u) * W + c]);
+        const float g = Elem<T>::to_f32(dR[(bg * n_act + i) * W + c]);
+        acc += (y + cu > 0.f) ? g : 0.f;
+      }
     }
-  dC[(int64_t)u * W + c] = acc / (float)l;
+  }
+  part[ig][cl] = acc;
+  __syncthreads();
+  if (ig == 0 && c < W) dC[(int64_t)u * W + c] = (((part[0][cl] + part[1][cl]) + part[2][cl]) + part[3][cl]) / (float)l;
 }
 
 }  // namespace nsa
@@ -139,7 +149,7 @@ extern "C" int nsa_compress_pool_bwd(const void* Y, const void* C, const void* d
   if (n_ctx == 0) return NSA_OK;
   hipStream_t st = (hipStream_t)stream;
   TimingScope ts(kIdPoolBwd, (hipStream_t)stream);
-  dim3 gt(n_ctx, Z * G), gc((width + 255) / 256, l);
+  dim3 gt(n_ctx, Z * G), gc((width + 63) / 64, l);
   if (dtype == NSA_F32) {
     hipLaunchKernelGGL(pool_bwd_tok_kernel<float>, gt, dim3(256), 0, st, (const float*)Y, (const float*)C,
                        (const float*)dR, (const float*)dVc, (float*)dY, (float*)dV, n_ctx, width, head_dim_v, l, d,

@@ -5,10 +5,13 @@
 // sums them in item order (fixed, so the result is reproducible) and accumulates
 // into the caller's dK / dV with their strides.
 #include "nsa_attn.h"
+#include "nsa_attn_bwd_dkdv.h"
 #include "nsa_device.h"
 #include "nsa_kernels.h"
 
 namespace nsa {
+
+constexpr int kReduceSplit = 10;
 
 bool dispatch_attn_fwd_f32(int, int, int, const AttnArgs&, hipStream_t);
 bool dispatch_attn_fwd_bf16(int, int, int, const AttnArgs&, hipStream_t);
@@ -35,8 +38,8 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
   const int b = bg / a.G, grp = bg % a.G;
   const int width = DK + DV;
   int key0, key_hi, first, count, step;
-  if (br == kCompression) {
-    const int nseg = (a.Tq + kSegT - 1) / kSegT;
+  if (br != kSelection) {
+    const int nseg = dkdv_nseg(br, a.Tq, a.window);
     key0 = blockIdx.x * 64;
     key_hi = a.Tkv;
     first = blockIdx.x * nseg;
@@ -54,7 +57,10 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
   }
   if (count == 0 || key0 >= key_hi) return;
   const float* base = a.partial + (int64_t)bg * a.items_per_bg * 64 * width;
-  for (int e = threadIdx.x; e < 64 * width; e += 256) {
+  // blockIdx.z splits the tile's 64 x width elements over kReduceSplit workgroups
+  const int per = (64 * width + kReduceSplit - 1) / kReduceSplit;
+  const int e_end = min(64 * width, (int)(blockIdx.z + 1) * per);
+  for (int e = blockIdx.z * per + threadIdx.x; e < e_end; e += 256) {
     const int kl = e / width, col = e % width;
     const int key = key0 + kl;
     if (key >= key_hi) continue;
@@ -73,10 +79,10 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
 
 void launch_partial_reduce(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st) {
   int tiles;
-  if (br == kCompression) tiles = (a.Tkv + 63) / 64;
+  if (br != kSelection) tiles = (a.Tkv + 63) / 64;
   else tiles = a.nblk * ((a.lprime + 63) / 64);
   if (tiles <= 0) return;
-  dim3 grid(tiles, a.B * a.G);
+  dim3 grid(tiles, a.B * a.G, kReduceSplit);
   if (dtype == kF32)
     hipLaunchKernelGGL(partial_reduce_kernel<float>, grid, dim3(256), 0, st, a, dk, dv, br);
   else

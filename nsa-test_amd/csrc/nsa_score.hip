@@ -110,21 +110,54 @@ __global__ __launch_bounds__(256) void score_topn_kernel(ScoreArgs a) {
   }
   __syncthreads();
 
-  // ---- Eq. 8 logits: one thread per compressed block, all rows ----
-  const S* kc = reinterpret_cast<const S*>(a.kc) + b * a.sk_b + g * a.sk_g;
-  for (int i = tid; i < ncomp; i += 256) {
-    float acc[R];
+  // ---- Eq. 8 logits: a thread owns one compressed block and a group of rows ----
+  // (rows are split over threads when there are fewer than 256 columns, so the
+  // early, short rows of a causal sequence still occupy the whole workgroup).
+  // The key row is read as 16-byte vectors (the feature axis has unit stride); each
+  // logit is still one sequential fma chain over e = 0..dk-1.
+  {
+    constexpr int EV = 16 / sizeof(S);
+    const S* kc = reinterpret_cast<const S*>(a.kc) + b * a.sk_b + g * a.sk_g;
+    int nrg = 1;
+    while (nrg < R && nrg * 2 * ncomp <= 256 && (rows % (nrg * 2)) == 0) nrg *= 2;
+    const int cpt = 256 / nrg;           // columns per pass
+    const int rg = tid / cpt;
+    const int nr = rows / nrg;           // rows per thread
+    const int r0 = rg * nr;
+    for (int i = tid % cpt; i < ncomp; i += cpt) {
+      float acc[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    for (int e = 0; e < dk; ++e) {
-      const float kv = ldf<S>(kc, (int64_t)e * a.sk_d + (int64_t)i * a.sk_i);
+      for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+      const S* krow = kc + (int64_t)i * a.sk_i;
+      for (int e0 = 0; e0 < dk; e0 += EV) {
+        const uint4 raw = *reinterpret_cast<const uint4*>(krow + e0);
+        float kv[EV];
+        if (sizeof(S) == 2) {
+          const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            kv[2 * u] = __uint_as_float(w[u] << 16);
+            kv[2 * u + 1] = __uint_as_float(w[u] & 0xffff0000u);
+          }
+        } else {
+          kv[0] = __uint_as_float(raw.x);
+          kv[1] = __uint_as_float(raw.y);
+          kv[2] = __uint_as_float(raw.z);
+          kv[3] = __uint_as_float(raw.w);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (r < nr) {
+            const float* qr = qs + (r0 + r) * dk + e0;
+#pragma unroll
+            for (int u = 0; u < EV; ++u) acc[r] = fmaf(qr[u], kv[u], acc[r]);
+          }
+        }
+      }
 #pragma unroll
       for (int r = 0; r < R; ++r)
-        if (r < rows) acc[r] = fmaf(qs[r * dk + e], kv, acc[r]);
+        if (r < nr) ev[(r0 + r) * ncomp + i] = acc[r] * a.scale;
     }
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (r < rows) ev[r * ncomp + i] = acc[r] * a.scale;
   }
   __syncthreads();
 
@@ -298,6 +331,17 @@ extern "C" int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* b
   if (d <= 0 || l <= 0 || l_prime <= 0 || l % d || l_prime % d)
     return nsa::set_error(NSA_ERR_INVALID, "need l % d == 0 and l_prime % d == 0");
   if (n < 0 || n > 64) return nsa::set_error(NSA_ERR_INVALID, "n outside [0, 64]");
+  {
+    const int esz = dtype == NSA_F32 ? 4 : 2;
+    // strides of size-1 axes never address memory and are not checked
+    const bool ok = stride_kk == 1 && (head_dim_qk * esz) % 16 == 0 && ((uintptr_t)k_cmp) % 16 == 0 &&
+                    (Z == 1 || (stride_kz * esz) % 16 == 0) && (n_kv_groups == 1 || (stride_kg * esz) % 16 == 0) &&
+                    (n_blocks == 1 || (stride_kn * esz) % 16 == 0);
+    if (!ok)
+      return nsa::set_error(NSA_ERR_LAYOUT,
+                            "k_cmp needs a unit-stride feature axis (the [Z,G,N,dk] storage of the reference's "
+                            "[Z,G,dk,N] view) with 16-byte aligned rows");
+  }
   if (n_ctx == 0) return NSA_OK;
   ScoreArgs a{};
   a.q = q;

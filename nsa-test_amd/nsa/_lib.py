@@ -35,7 +35,7 @@ SIGNATURES = {
     "nsa_last_error": (ctypes.c_char_p, []),
     "nsa_head_dims_supported": (_I, [_I, _I, _I]),
     "nsa_fwd_workspace_size": (_Z, [_I] * 11),
-    "nsa_bwd_workspace_size": (_Z, [_I] * 11),
+    "nsa_bwd_workspace_size": (_Z, [_I] * 12),
     "nsa_sliding_window_fwd": (_I, [_P, _P, _P, _P, _F, _P, _P, *_S22, *[_I] * 7, _I, _P, _Z, _P]),
     "nsa_sliding_window_bwd": (
         _I, [_P, _P, _P, _P, _P, _F, _P, _P, *_S22, _P, _P, _P, *_S12, *[_I] * 7, _I, _P, _Z, _P]),

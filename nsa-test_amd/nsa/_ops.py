@@ -151,7 +151,7 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     dvk = dv if direct_dv else torch.zeros(Z, G, Tkv, DV, device=dev, dtype=cdt)
     n_slots = indices.shape[-1] if branch == SELECTION else 0
     ws_bytes = _lib.size("nsa_bwd_workspace_size", branch, _dtype_code(cdt), Z, H, G, Tq, Tkv, DK, DV, n_slots,
-                         lprime)
+                         lprime, int(window) if branch == SLIDING else 1)
     ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
     dt = _dtype_code(cdt)
     st = _stream(dev)

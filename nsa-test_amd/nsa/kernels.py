@@ -361,7 +361,8 @@ def score_and_select(q: torch.Tensor, k_compressed: torch.Tensor, block_ends: to
     G, N = k_compressed.shape[1], k_compressed.shape[-1]
     cdt = _ops.compute_dtype(q.dtype)
     qc = q.to(cdt)
-    kc = k_compressed.to(cdt)
+    # the kernel reads each compressed key as one row: [B,G,N,dk] storage
+    kc = k_compressed.to(cdt).transpose(-1, -2).contiguous().transpose(-1, -2)
     be = block_ends.to(torch.int32).contiguous()
     s = config.l_prime // config.d
     nsel = (N + s - 1) // s

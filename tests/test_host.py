@@ -107,10 +107,12 @@ def test_ctypes_signatures_match_header():
 
 def test_workspace_sizes():
     f = _lib.size("nsa_fwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64)
-    b = _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64)
+    b = _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 512)
     assert 0 < f < b
-    s = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 16, 64)
-    assert s > b
+    # a wider window spreads each key tile over more query segments
+    assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 8192) > b
+    s = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 16, 64, 1)
+    assert s > f
 
 
 def test_error_codes_without_gpu_work():
