@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int RC = sizeof(S) == 4 ? 16 : kRowChunk;  // fp32 stages half the rows (LDS)
   constexpr int QP = DK + EPF;
   constexpr int OP = DV + EPF;
-  constexpr int RP = RC + 4;
+  constexpr int RP = RC + (sizeof(S) == 2 ? 8 : 4);  // 16-byte aligned transposed rows
   constexpr int CK = CFrag<T>::kKeys;
   constexpr int CT = CK / 16;
   constexpr int RPAIRS = RC / 2;
@@ -233,6 +233,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
       }
     }
   };
+  // position of chunk row r in the transposed (C-permuted for bf16) stage; rows 2k and
+  // 2k+1 stay adjacent
+  auto rowpos = [](int r) -> int { return sizeof(S) == 2 ? cperm_pos32(r) : r; };
   auto store_chunk = [&](int buf) {
 #pragma unroll
     for (int j = 0; j < NQ; ++j) {
@@ -242,7 +245,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
         const int e = (c / RPAIRS) * EPF;
         *reinterpret_cast<uint4*>(&Qs[buf][(2 * rp) * QP + e]) = pq[j][0];
         *reinterpret_cast<uint4*>(&Qs[buf][(2 * rp + 1) * QP + e]) = pq[j][1];
-        PairT<S>::store(&QTs[buf][e * RP + 2 * rp], RP, pq[j][0], pq[j][1]);
+        PairT<S>::store(&QTs[buf][e * RP + rowpos(2 * rp)], RP, pq[j][0], pq[j][1]);
       }
     }
 #pragma unroll
@@ -253,7 +256,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
         const int e = (c / RPAIRS) * EPF;
         *reinterpret_cast<uint4*>(&Os[buf][(2 * rp) * OP + e]) = po[j][0];
         *reinterpret_cast<uint4*>(&Os[buf][(2 * rp + 1) * OP + e]) = po[j][1];
-        PairT<S>::store(&OTs[buf][e * RP + 2 * rp], RP, po[j][0], po[j][1]);
+        PairT<S>::store(&OTs[buf][e * RP + rowpos(2 * rp)], RP, po[j][0], po[j][1]);
       }
     }
     if (tid < RC) {

@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
 
   int ntiles = 0, key_lo = 0, nsubblk = 1;
   if (BR == kSliding) {
-    key_lo = max(0, t_first - a.window + 1) & ~15;
+    key_lo = max(0, t_first - a.window + 1) & ~31;  // 32-key aligned (C-permuted K^T chunks)
     const int hi = min(t_last, a.Tkv - 1);
     ntiles = hi >= key_lo ? (hi - key_lo) / 64 + 1 : 0;
   } else if (BR == kCompression) {

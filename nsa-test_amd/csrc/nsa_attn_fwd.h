@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   int key_lo = 0;
   int nsubblk = 1;
   if (BR == kSliding) {
-    key_lo = max(0, t_first - a.window + 1) & ~15;
+    key_lo = max(0, t_first - a.window + 1) & ~31;  // 32-key aligned (C-permuted V^T chunks)
     const int hi = min(t_last, a.Tkv - 1);
     ntiles = hi >= key_lo ? (hi - key_lo) / 64 + 1 : 0;
   } else if (BR == kCompression) {

@@ -114,7 +114,6 @@ __global__ __launch_bounds__(256) void attn_sel_fwd_kernel(AttnArgs a, int ncolt
 #pragma unroll
   for (int j = 0; j < DV / 16; ++j) oacc[j] = zero4();
   float m2 = -INFINITY, lsum = 0.f;
-  const int nsub = (a.lprime + 63) / 64;
   const int nwords = (a.nblk + 31) / 32;
   const bool one_t = w.nt == 1;
 
@@ -126,9 +125,9 @@ __global__ __launch_bounds__(256) void attn_sel_fwd_kernel(AttnArgs a, int ncolt
       const int blk_lo = blk * a.lprime;
       const int blk_hi = min(blk_lo + a.lprime, a.Tkv);
       const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
-      for (int sb = 0; sb < nsub; ++sb) {
-        const int key0 = blk_lo + sb * 64;
-        if (key0 >= blk_hi || (a.causal && key0 > t_last)) break;
+      // tiles start on a 32-key boundary (the C-permuted chunks of vt / kn)
+      for (int key0 = blk_lo & ~31; key0 < blk_hi; key0 += 64) {
+        if (a.causal && key0 > t_last) break;
         // S^T[key, col] for the 64 keys of this tile
         f32x4 st[4];
 #pragma unroll
@@ -139,15 +138,15 @@ __global__ __launch_bounds__(256) void attn_sel_fwd_kernel(AttnArgs a, int ncolt
           for (int kc = 0; kc < NKC; ++kc)
             st[ks] = Mma<T>::run(st[ks], *reinterpret_cast<const uint4*>(krow + kc * KC + g4 * EPF), qf[kc]);
         }
-        const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 + 63 < blk_hi &&
-                                 f0 + kSelWaveCols <= ncols;
+        const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 >= blk_lo &&
+                                 key0 + 63 < blk_hi && f0 + kSelWaveCols <= ncols;
         float mx = -INFINITY;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = key0 + ks * 16 + 4 * g4 + i;
-            const bool ok = all_visible || (colsel && (!a.causal || key <= colt) && key < blk_hi);
+            const bool ok = all_visible || (colsel && (!a.causal || key <= colt) && key >= blk_lo && key < blk_hi);
             const float v = ok ? st[ks][i] * scale2 : -INFINITY;
             st[ks][i] = v;
             mx = fmaxf(mx, v);
@@ -263,7 +262,6 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
   f32x4 dqa[DK / 16];
 #pragma unroll
   for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
-  const int nsub = (a.lprime + 63) / 64;
   const int nwords = (a.nblk + 31) / 32;
   const bool one_t = w.nt == 1;
 
@@ -275,9 +273,9 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
       const int blk_lo = blk * a.lprime;
       const int blk_hi = min(blk_lo + a.lprime, a.Tkv);
       const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
-      for (int sb = 0; sb < nsub; ++sb) {
-        const int key0 = blk_lo + sb * 64;
-        if (key0 >= blk_hi || (a.causal && key0 > t_last)) break;
+      // tiles start on a 32-key boundary (the C-permuted chunks of vt / kn)
+      for (int key0 = blk_lo & ~31; key0 < blk_hi; key0 += 64) {
+        if (a.causal && key0 > t_last) break;
         f32x4 st[4], dp[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
@@ -292,14 +290,14 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
           for (int kc = 0; kc < NVC; ++kc)
             dp[ks] = Mma<T>::run(dp[ks], *reinterpret_cast<const uint4*>(vrow + kc * KC + g4 * EPF), dof[kc]);
         }
-        const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 + 63 < blk_hi &&
-                                 f0 + kSelWaveCols <= ncols;
+        const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 >= blk_lo &&
+                                 key0 + 63 < blk_hi && f0 + kSelWaveCols <= ncols;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int key = key0 + ks * 16 + 4 * g4 + i;
-            const bool ok = all_visible || (colsel && (!a.causal || key <= colt) && key < blk_hi);
+            const bool ok = all_visible || (colsel && (!a.causal || key <= colt) && key >= blk_lo && key < blk_hi);
             const float p = ok ? fast_exp2(st[ks][i] * scale2 - l2) : 0.f;
             st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
           }

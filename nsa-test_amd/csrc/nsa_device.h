@@ -102,16 +102,21 @@ template <> struct CFrag<bf16> {
   }
 };
 
-// Load the "C-permuted" fragment of a row-major [rows][keys] array whose K axis is
-// the key axis: matches CFrag<T>::pack.  `row` points at the first key of the chunk.
+// "C-permuted" storage of a key-major operand ([rows][keys] arrays whose K axis is the
+// key axis: V^T, K^T, and the transposed Q / dO row chunks).  The fragment a lane
+// needs is the keys {4g..4g+3} and {16+4g..16+4g+3} of a 32-key chunk (CFrag<bf16>);
+// storing each 32-key chunk in the order p = 8g + j  <->  key = j < 4 ? 4g + j : 12 + 4g + j
+// makes that fragment one 16-byte vector.  fp32 chunks (16 keys, keys 4g..4g+3 per lane)
+// need no permutation.
+__host__ __device__ __forceinline__ int cperm_pos32(int key) {  // key within its 32-chunk -> position
+  return 8 * ((key & 15) >> 2) + (key & 3) + ((key & 16) ? 4 : 0);
+}
 template <typename T> __device__ __forceinline__ uint4 frag_cperm(const typename Store<T>::type* row, int g);
 template <> __device__ __forceinline__ uint4 frag_cperm<float>(const float* row, int g) {
   return *reinterpret_cast<const uint4*>(row + 4 * g);
 }
 template <> __device__ __forceinline__ uint4 frag_cperm<bf16>(const uint16_t* row, int g) {
-  uint2 lo = *reinterpret_cast<const uint2*>(row + 4 * g);
-  uint2 hi = *reinterpret_cast<const uint2*>(row + 16 + 4 * g);
-  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+  return *reinterpret_cast<const uint4*>(row + 8 * g);
 }
 
 // Standard fragment: 16 contiguous bytes at row[kchunk_base + g * kPerFrag].

@@ -45,10 +45,12 @@ __global__ __launch_bounds__(256) void repack_kernel(const S* __restrict__ src, 
     }
   }
   if (colm) {
+    // key-major operands are stored C-permuted within each 32-key chunk (bf16)
     for (int i = tid; i < 64 * 64; i += 256) {
       const int cc = i >> 6, rr = i & 63;
       const int r = r0 + rr, c = c0 + cc;
-      if (r < Rp && c < C) colm[obase + (int64_t)c * Rp + r] = tile[rr][cc];
+      const int rpos = sizeof(S) == 2 ? ((r & ~31) | cperm_pos32(r & 31)) : r;
+      if (r < Rp && c < C) colm[obase + (int64_t)c * Rp + rpos] = tile[rr][cc];
     }
   }
 }
