@@ -211,6 +211,17 @@ def cpu_baseline(name, samples, seed=0):
                       f"({t_group:.1f}s), extrapolated x{T / samples:.0f} rows x{G} groups"}
 
 
+def measured_traffic(config, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    passes (already scaled by the calibration copy's counter readings), or None."""
+    f = ROOT / "profiles" / f"nsa_{config}_traffic.json"
+    try:
+        rec = json.loads(f.read_text())["kernels"][kernel]
+    except (OSError, KeyError, ValueError):
+        return None
+    return round(rec["hbm_bytes"])
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -235,6 +246,12 @@ def main():
     cfg, mod, w = make_workload(args.config, dev)
     print(f"[bench] workload {args.config} {c}", file=sys.stderr, flush=True)
 
+    # untimed: one elementwise pass that reads 256 MiB and writes 256 MiB (torch's
+    # neg kernel, a name no other launch here uses), against which rocprofv3's
+    # FETCH_SIZE / WRITE_SIZE counters are calibrated
+    calib = torch.ones(64 << 20, device=dev, dtype=torch.float32)
+    torch.neg(calib)
+    del calib
     # untimed: breakdown, the dominant kernel and the exact valid-pair counts
     breakdown = kernel_breakdown(cfg, mod, w)
     idx, be = nsa_step(cfg, mod, w, backward=False)
@@ -284,7 +301,8 @@ def main():
         "mfma_frac_end_to_end": round(total_alg / step_s / 1e12 / PEAK_BF16_TFLOPS, 4),
         "roofline": {"bound": "mfma", "kernel": KERNELS[dominant], "achieved": round(achieved, 2),
                      "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "launch_ms": round(per_launch_ms, 4), "launches": tm.launches, "traffic": None},
+                     "launch_ms": round(per_launch_ms, 4), "launches": tm.launches,
+                     "traffic": measured_traffic(args.config, KERNELS[dominant])},
         "valid_pairs": {"sliding": pairs[0], "compression": pairs[1], "selection": pairs[2]},
         "breakdown_ms": {k: v["ms"] for k, v in breakdown.items()},
     }
