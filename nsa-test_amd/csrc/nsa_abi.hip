@@ -95,11 +95,13 @@ Layout make_layout(const Shape& s, bool bwd) {
 }
 
 // Unit feature stride and 16-byte aligned rows; the strides of size-1 axes are
-// never used to address memory, so they are not checked.
+// never used to address memory, so they are not checked.  The head and time strides
+// must fit 32 bits (the kernels multiply them as 32-bit operands into 64-bit offsets).
 bool row_ok(const void* p, int64_t inner, int64_t s0, int64_t s1, int64_t s2, int esz, int n0 = 2, int n1 = 2,
             int n2 = 2) {
   if (inner != 1) return false;
   if (((uintptr_t)p) % 16) return false;
+  if ((n1 != 1 && (s1 < 0 || s1 > INT32_MAX)) || (n2 != 1 && (s2 < 0 || s2 > INT32_MAX))) return false;
   return (n0 == 1 || (s0 * esz) % 16 == 0) && (n1 == 1 || (s1 * esz) % 16 == 0) && (n2 == 1 || (s2 * esz) % 16 == 0);
 }
 

@@ -6,7 +6,8 @@
 // RC rows, staged in LDS row-major (operand of S = Q K^T and dP = dO V^T) and
 // transposed (operand of dK^T += Q^T dS and dV^T += dO^T P, whose reduction runs over
 // the rows).  The next chunk is loaded into registers while the current one is
-// computed, and the LDS stage is double-buffered, so each chunk costs one barrier.
+// computed; the single LDS stage keeps the footprint small enough (about 47 KB at
+// dk = 192) for two workgroups per CU.
 // Staging threads own pairs of adjacent rows, so every transposed LDS write stores
 // two rows at once, and the transposed row pitch (RC + 4) keeps those writes free of
 // bank conflicts.
@@ -40,9 +41,9 @@ template <> struct PairT<uint16_t> {
     const uint32_t wa[4] = {a.x, a.y, a.z, a.w};
     const uint32_t wb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      *reinterpret_cast<uint32_t*>(dst + (2 * w) * RP) = (wa[w] & 0xffffu) | (wb[w] << 16);
-      *reinterpret_cast<uint32_t*>(dst + (2 * w + 1) * RP) = (wa[w] >> 16) | (wb[w] & 0xffff0000u);
+    for (int w = 0; w < 4; ++w) {  // v_perm_b32: bytes 0-3 from wa, 4-7 from wb
+      *reinterpret_cast<uint32_t*>(dst + (2 * w) * RP) = __builtin_amdgcn_perm(wb[w], wa[w], 0x05040100u);
+      *reinterpret_cast<uint32_t*>(dst + (2 * w + 1) * RP) = __builtin_amdgcn_perm(wb[w], wa[w], 0x07060302u);
     }
   }
 };
@@ -74,15 +75,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int NQ = (QPC + 255) / 256;
   constexpr int NO = (OPC + 255) / 256;
   static_assert(RC % CK == 0, "row chunk");
+  // One LDS stage (two barriers per chunk): the smaller footprint lets two workgroups
+  // share a CU, which hides far more latency than a second stage would.
+  constexpr int NB = 1;
 
-  __shared__ __attribute__((aligned(16))) S Qs[2][RC * QP];
-  __shared__ __attribute__((aligned(16))) S QTs[2][DK * RP];
-  __shared__ __attribute__((aligned(16))) S Os[2][RC * OP];
-  __shared__ __attribute__((aligned(16))) S OTs[2][DV * RP];
-  __shared__ int s_t[2][RC];
-  __shared__ float s_l2[2][RC];
-  __shared__ float s_dl[2][RC];
+  __shared__ __attribute__((aligned(16))) S Qs[NB][RC * QP];
+  __shared__ __attribute__((aligned(16))) S QTs[NB][DK * RP];
+  __shared__ __attribute__((aligned(16))) S Os[NB][RC * OP];
+  __shared__ __attribute__((aligned(16))) S OTs[NB][DV * RP];
+  __shared__ int s_t[NB][RC];
+  __shared__ float s_l2[NB][RC];
+  __shared__ float s_dl[NB][RC];
   __shared__ int s_be[64];
+  __shared__ int s_tl[kSegT];  // selection: the item's query timesteps
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -100,7 +105,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   // ---- decode the work item: key tile + segment of rows ----
   int key0, blk_hi = a.Tkv;
   int f_lo, f_hi;              // flattened row range (row f -> (t, head))
-  const int* tlist = nullptr;  // selection: row f -> t = tlist[f / hpg]
+  int e_base = 0;              // selection: row f -> t = s_tl[f / hpg - e_base]
   if (BR == kSliding) {
     const int nseg = dkdv_nseg(kSliding, a.Tq, a.window);
     const int tile = item / nseg, seg = item % nseg;
@@ -141,12 +146,15 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
     const int* co = a.csr_off + (int64_t)bg * (a.nblk + 1);
     const int e_lo = co[j] + k * kSegT;
     const int e_hi = min(co[j + 1], e_lo + kSegT);
-    tlist = a.csr_t + (int64_t)bg * a.Tq * a.nslots;
     key0 = j * a.lprime + sub * 64;
     blk_hi = min(j * a.lprime + a.lprime, a.Tkv);
     f_lo = e_lo * hpg;
     f_hi = e_hi * hpg;
     if (key0 >= blk_hi) return;  // sub-tile past the sequence end: no partial is read
+    e_base = e_lo;
+    const int* tlist = a.csr_t + (int64_t)bg * a.Tq * a.nslots;
+    for (int i = tid; i < e_hi - e_lo; i += 256) s_tl[i] = tlist[e_lo + i];
+    __syncthreads();
   }
 
   // ---- this wave's 16 keys: K and V rows as B operands, kept in registers ----
@@ -173,6 +181,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
     }
   }
 
+  // Wait for the K/V fragments here: otherwise the loop's first use of them becomes a
+  // wait inside the loop body, which also stalls on the prefetch of the next chunk.
+  __builtin_amdgcn_s_waitcnt(0);
+
   f32x4 dka[DK / 16], dva[DV / 16];
 #pragma unroll
   for (int j = 0; j < DK / 16; ++j) dka[j] = zero4();
@@ -183,20 +195,22 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   const S* obase = reinterpret_cast<const S*>(a.dout) + b * a.sdo_b;
   auto row_t = [&](int f) -> int {
     const int e = hdiv.div(f);
-    return tlist ? tlist[e] : e;
+    return BR == kSelection ? s_tl[e - e_base] : e;
   };
 
   // ---- register prefetch of one chunk (pairs of adjacent rows) ----
   uint4 pq[NQ][2], po[NO][2];
   int pr_t = -1;
   float pr_l2 = INFINITY, pr_dl = 0.f;
-  auto load_rows = [&](int f, const S* base, int64_t sh, int64_t st, int e, uint4& dst) {
-    dst = make_uint4(0, 0, 0, 0);
-    if (f < f_hi) {
-      const int t = row_t(f);
-      const int h = grp * hpg + hdiv.mod(f);
-      dst = *reinterpret_cast<const uint4*>(base + (int64_t)h * sh + (int64_t)t * st + e);
-    }
+  // Rows past the item's end re-read its last row (finite data); they are masked
+  // (p = 0) through s_t = -1, so every load is unconditional and the loads of a chunk
+  // issue back to back.
+  const int sqh = (int)a.sq_h, sqt = (int)a.sq_t, soh = (int)a.sdo_h, sot = (int)a.sdo_t;
+  auto load_rows = [&](int f, const S* base, int sh, int st, int e, uint4& dst) {
+    const int fe = min(f, f_hi - 1);
+    const int t = row_t(fe);
+    const int h = grp * hpg + hdiv.mod(fe);
+    dst = *reinterpret_cast<const uint4*>(base + e + ((int64_t)h * sh + (int64_t)t * st));
   };
   auto load_chunk = [&](int fc) {
 #pragma unroll
@@ -205,8 +219,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
       if (c < QPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
-        load_rows(fc + 2 * rp, qbase, a.sq_h, a.sq_t, e, pq[j][0]);
-        load_rows(fc + 2 * rp + 1, qbase, a.sq_h, a.sq_t, e, pq[j][1]);
+        load_rows(fc + 2 * rp, qbase, sqh, sqt, e, pq[j][0]);
+        load_rows(fc + 2 * rp + 1, qbase, sqh, sqt, e, pq[j][1]);
       }
     }
 #pragma unroll
@@ -215,22 +229,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
       if (c < OPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
-        load_rows(fc + 2 * rp, obase, a.sdo_h, a.sdo_t, e, po[j][0]);
-        load_rows(fc + 2 * rp + 1, obase, a.sdo_h, a.sdo_t, e, po[j][1]);
+        load_rows(fc + 2 * rp, obase, soh, sot, e, po[j][0]);
+        load_rows(fc + 2 * rp + 1, obase, soh, sot, e, po[j][1]);
       }
     }
     if (tid < RC) {
       const int f = fc + tid;
-      pr_t = -1;
-      pr_l2 = INFINITY;
-      pr_dl = 0.f;
-      if (f < f_hi) {
-        pr_t = row_t(f);
-        const int h = grp * hpg + hdiv.mod(f);
-        const int64_t srow = ((int64_t)b * a.H + h) * a.Tq + pr_t;
-        pr_l2 = a.lse2[srow];
-        pr_dl = a.delta[srow];
-      }
+      const int fe = min(f, f_hi - 1);
+      const int t = row_t(fe);
+      const int h = grp * hpg + hdiv.mod(fe);
+      const int64_t srow = ((int64_t)b * a.H + h) * a.Tq + t;
+      pr_l2 = a.lse2[srow];
+      pr_dl = a.delta[srow];
+      pr_t = f < f_hi ? t : -1;
     }
   };
   // position of chunk row r in the transposed (C-permuted for bf16) stage; rows 2k and
@@ -269,8 +280,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   const int nchunks = (f_hi - f_lo + RC - 1) / RC;
   if (nchunks > 0) load_chunk(f_lo);
   for (int c = 0; c < nchunks; ++c) {
-    const int buf = c & 1;
+    const int buf = c % NB;
     const int fc = f_lo + c * RC;
+    if (NB == 1 && c > 0) __syncthreads();  // the previous chunk's reads are done
     store_chunk(buf);
     if (c + 1 < nchunks) load_chunk(fc + RC);
     __syncthreads();
@@ -291,7 +303,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
       all_visible = full && (!a.causal || kw0 + 15 <= t_min) && kw0 + 15 < blk_hi;
     }
 
-    if (active) {
+    // Waves whose keys no row of the chunk can see still run the (fully masked) products:
+    // a branch around them makes the compiler shuttle the dK/dV accumulators between
+    // register files on every chunk, which costs more than the skipped work.
+    (void)active;
+    {
       f32x4 pt[RC / 16], dst[RC / 16];
 #pragma unroll
       for (int rs = 0; rs < RC / 16; ++rs) {

@@ -151,17 +151,23 @@ template <> __device__ __forceinline__ void store4<bf16>(uint16_t* p, f32x4 v) {
 // results below the normal range may flush, which the softmax tolerates.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// n / d and n % d for non-negative 32-bit n, with a shift when d is a power of two
+// n / d and n % d for 0 <= n < 2^31, branch-free: q = (n * m) >> s with
+// l = ceil(log2 d), s = 31 + l, m = ceil(2^s / d).  m < 2^32 because d > 2^(l-1), and the
+// rounding error n (m - 2^s/d) / 2^s < 2^-l <= 1/d never reaches the next integer.
 struct IntDiv {
-  int d, shift;  // shift < 0: d is not a power of two
+  int d;
+  uint32_t m;
+  int s;
   __host__ __device__ static IntDiv make(int d_) {
-    IntDiv r{d_, -1};
-    for (int s = 0; s < 31; ++s)
-      if ((1 << s) == d_) r.shift = s;
-    return r;
+    int l = 0;
+    while ((1ll << l) < d_) ++l;
+    const uint64_t two_s = 1ull << (31 + l);
+    return IntDiv{d_, (uint32_t)((two_s + (uint64_t)d_ - 1) / (uint64_t)d_), 31 + l};
   }
-  __device__ __forceinline__ int div(int n) const { return shift >= 0 ? (n >> shift) : n / d; }
-  __device__ __forceinline__ int mod(int n) const { return shift >= 0 ? (n & (d - 1)) : n % d; }
+  __device__ __forceinline__ int div(int n) const {
+    return (int)(((uint64_t)(uint32_t)n * m) >> s);
+  }
+  __device__ __forceinline__ int mod(int n) const { return n - div(n) * d; }
 };
 
 }  // namespace nsa
