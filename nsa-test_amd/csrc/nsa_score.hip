@@ -22,6 +22,7 @@
 // fma), flushed to 0 below -64 so no denormal ever enters the pipeline.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdio.h>
 
 #include "nsa_attn.h"
 #include "nsa_device.h"
@@ -64,160 +65,202 @@ struct ScoreArgs {
   int TT;  // timesteps per workgroup
 };
 
-constexpr int kMaxRows = 64;  // R = TT * hpg accumulators per thread
+constexpr int kMaxRows = 64;  // rows (timestep, head) of one workgroup
+constexpr int kMaxCols = 4096;  // compressed blocks a row can score
 
 template <typename S>
-__device__ __forceinline__ float ldf(const S* p, int64_t off);
-template <> __device__ __forceinline__ float ldf<float>(const float* p, int64_t off) { return p[off]; }
-template <> __device__ __forceinline__ float ldf<uint16_t>(const uint16_t* p, int64_t off) {
-  return bf16_bits_to_f32(p[off]);
+__device__ __forceinline__ void unpack16(const uint4& raw, float* v);
+template <> __device__ __forceinline__ void unpack16<float>(const uint4& raw, float* v) {
+  v[0] = __uint_as_float(raw.x);
+  v[1] = __uint_as_float(raw.y);
+  v[2] = __uint_as_float(raw.z);
+  v[3] = __uint_as_float(raw.w);
+}
+template <> __device__ __forceinline__ void unpack16<uint16_t>(const uint4& raw, float* v) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    v[2 * u] = __uint_as_float(w[u] << 16);
+    v[2 * u + 1] = __uint_as_float(w[u] & 0xffff0000u);
+  }
 }
 
-template <typename S, int R>
-__global__ __launch_bounds__(256) void score_topn_kernel(ScoreArgs a) {
+// One workgroup per (batch, group, TT consecutive timesteps); NW = blockDim / 64 waves.
+// Wave w owns the rows r = w + NW * rr (rr < RPW) of the TT * hpg (timestep, head)
+// rows, and lane L of a wave owns the compressed blocks i = L + 64 c (c < C): the
+// logits, the softmax and Eq. 9 of a row all stay inside the wave that owns it, in
+// registers.  The query row of a wave is wave-uniform, so it is read through the scalar
+// unit and broadcast to the FMAs; each 16-byte key load feeds RPW * (16 / sizeof(S))
+// FMAs.
+template <typename S, int RPW, int C>
+__global__ __launch_bounds__(512) void score_topn_kernel(ScoreArgs a, const S* __restrict__ qg) {
   extern __shared__ float lds[];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  constexpr int EV = 16 / sizeof(S);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int NW = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bg = blockIdx.y, b = bg / a.G, g = bg % a.G;
   const int t0 = blockIdx.x * a.TT;
   const int TT = min(a.TT, a.T - t0);
-  const int rows = TT * a.hpg;  // r = tt * hpg + hh
+  const int hpg = a.hpg;
+  const int rows = TT * hpg;  // r = tt * hpg + hh
   const int t_last = t0 + TT - 1;
   const int NB = a.NB, nsel = a.nsel, dk = a.dk;
+  const int segw = 64 * a.s + a.a;  // columns Eq. 9 reads for 64 consecutive blocks
+
+  float* pseg = lds + wave * segw;                          // [NW][segw]
+  float* ps = lds + NW * segw;                              // [rows][nsel]
+  float* agg = ps + rows * nsel;                            // [TT][nsel]
+  int* top = reinterpret_cast<int*>(agg + a.TT * nsel);     // [TT][64]
+  int* chosen = top + a.TT * 64;                            // [TT][64]
+
   // columns with any visible row (plus block 0 for the no-visible-block rule)
   __shared__ int s_ncomp;
   if (tid == 0) s_ncomp = 0;
   __syncthreads();
   {
     int mx = 0;
-    for (int i = tid; i < NB; i += 256)
+    for (int i = tid; i < NB; i += blockDim.x)
       if (a.block_ends[i] <= t_last) mx = i + 1;
     if (mx) atomicMax(&s_ncomp, mx);
   }
   __syncthreads();
   int ncomp = s_ncomp;
   if (ncomp == 0 && NB > 0) ncomp = 1;
+  const int nch = (ncomp + 63) >> 6;  // <= C (checked by the launcher)
 
-  float* qs = lds;                           // [R][dk]
-  float* ev = qs + rows * dk;                // [rows][ncomp]
-  float* agg = ev + (int64_t)rows * ncomp;   // [TT][nsel]
-  int* top = reinterpret_cast<int*>(agg + a.TT * nsel);  // [TT][64]
-
-  const S* q = reinterpret_cast<const S*>(a.q);
-  for (int x = tid; x < rows * dk; x += 256) {
-    const int r = x / dk, e = x % dk;
-    const int t = t0 + r / a.hpg, h = g * a.hpg + r % a.hpg;
-    qs[r * dk + e] = ldf<S>(q, b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)t * a.sq_t + (int64_t)e * a.sq_d);
+  int be[C];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int i = c * 64 + lane;
+    be[c] = (c < nch && i < ncomp) ? a.block_ends[i] : 0x7fffffff;
   }
-  __syncthreads();
 
-  // ---- Eq. 8 logits: a thread owns one compressed block and a group of rows ----
-  // (rows are split over threads when there are fewer than 256 columns, so the
-  // early, short rows of a causal sequence still occupy the whole workgroup).
-  // The key row is read as 16-byte vectors (the feature axis has unit stride); each
-  // logit is still one sequential fma chain over e = 0..dk-1.
-  {
-    constexpr int EV = 16 / sizeof(S);
-    const S* kc = reinterpret_cast<const S*>(a.kc) + b * a.sk_b + g * a.sk_g;
-    int nrg = 1;
-    while (nrg < R && nrg * 2 * ncomp <= 256 && (rows % (nrg * 2)) == 0) nrg *= 2;
-    const int cpt = 256 / nrg;           // columns per pass
-    const int rg = tid / cpt;
-    const int nr = rows / nrg;           // rows per thread
-    const int r0 = rg * nr;
-    for (int i = tid % cpt; i < ncomp; i += cpt) {
-      float acc[R];
+  // ---- Eq. 8 logits: one sequential fma chain over e = 0..dk-1 per (row, block) ----
+  float acc[RPW][C];
 #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-      const S* krow = kc + (int64_t)i * a.sk_i;
-      for (int e0 = 0; e0 < dk; e0 += EV) {
-        const uint4 raw = *reinterpret_cast<const uint4*>(krow + e0);
-        float kv[EV];
-        if (sizeof(S) == 2) {
-          const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  for (int rr = 0; rr < RPW; ++rr)
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            kv[2 * u] = __uint_as_float(w[u] << 16);
-            kv[2 * u + 1] = __uint_as_float(w[u] & 0xffff0000u);
-          }
-        } else {
-          kv[0] = __uint_as_float(raw.x);
-          kv[1] = __uint_as_float(raw.y);
-          kv[2] = __uint_as_float(raw.z);
-          kv[3] = __uint_as_float(raw.w);
+    for (int c = 0; c < C; ++c) acc[rr][c] = 0.0f;
+  const S* kc = reinterpret_cast<const S*>(a.kc) + b * a.sk_b + g * a.sk_g;
+  const S* qb = qg + b * a.sq_b;
+  for (int e0 = 0; e0 < dk; e0 += EV) {
+    float qv[RPW][EV];
+#pragma unroll
+    for (int rr = 0; rr < RPW; ++rr) {
+      const int r = min(wave + NW * rr, rows - 1);
+      const int t = t0 + r / hpg, h = g * hpg + r % hpg;
+      unpack16<S>(*reinterpret_cast<const uint4*>(qb + (int64_t)h * a.sq_h + (int64_t)t * a.sq_t + e0), qv[rr]);
+    }
+    // the key loads of up to 8 chunks are issued (unconditionally: lanes past the last
+    // block re-read it) before the first FMA waits on one
+    constexpr int CB = C < 8 ? C : 8;
+#pragma unroll
+    for (int cb = 0; cb < C; cb += CB) {
+      if (cb < nch) {
+        uint4 kraw[CB];
+#pragma unroll
+        for (int c = 0; c < CB; ++c) {
+          const int i = min((cb + c) * 64 + lane, ncomp - 1);
+          kraw[c] = *reinterpret_cast<const uint4*>(kc + (int64_t)i * a.sk_i + e0);
         }
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
-          if (r < nr) {
-            const float* qr = qs + (r0 + r) * dk + e0;
+        for (int c = 0; c < CB; ++c) {
+          if (cb + c < nch) {
+            float kv[EV];
+            unpack16<S>(kraw[c], kv);
 #pragma unroll
-            for (int u = 0; u < EV; ++u) acc[r] = fmaf(qr[u], kv[u], acc[r]);
+            for (int rr = 0; rr < RPW; ++rr)
+#pragma unroll
+              for (int u = 0; u < EV; ++u) acc[rr][cb + c] = fmaf(qv[rr][u], kv[u], acc[rr][cb + c]);
           }
         }
       }
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (r < nr) ev[(r0 + r) * ncomp + i] = acc[r] * a.scale;
     }
   }
-  __syncthreads();
 
-  // ---- softmax per row (one wave per row) ----
-  for (int r = wave; r < rows; r += 4) {
-    const int t = t0 + r / a.hpg;
-    const int h = g * a.hpg + r % a.hpg;
-    float* row = ev + (int64_t)r * ncomp;
-    bool anyv = false;
+  // ---- per row: softmax (Eq. 8) and Eq. 9, inside the owning wave ----
+#pragma unroll
+  for (int rr = 0; rr < RPW; ++rr) {
+    const int r = wave + NW * rr;
+    if (r >= rows) continue;  // wave-uniform
+    const int t = t0 + r / hpg, h = g * hpg + r % hpg;
     float mx = -INFINITY;
-    for (int i = lane; i < ncomp; i += 64) {
-      const bool v = a.block_ends[i] <= t;
+    bool anyv = false;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      acc[rr][c] = acc[rr][c] * a.scale;
+      const bool v = be[c] <= t;
       anyv |= v;
-      if (v) mx = fmaxf(mx, row[i]);
+      if (v) mx = fmaxf(mx, acc[rr][c]);
     }
     const bool any_row = __ballot(anyv) != 0ull;
-    if (!any_row) mx = row[0];  // block 0 made visible
+    if (!any_row) mx = __shfl(acc[rr][0], 0);  // block 0 made visible
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    // lane partial over its blocks in ascending order, then the xor butterfly
     float part = 0.0f;
-    for (int i = lane; i < ncomp; i += 64) {
-      const bool v = a.block_ends[i] <= t || (!any_row && i == 0);
-      const float e = v ? exp32(row[i] - mx) : 0.0f;
-      row[i] = e;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const bool v = be[c] <= t || (!any_row && c == 0 && lane == 0);
+      const float e = v ? exp32(acc[rr][c] - mx) : 0.0f;
+      acc[rr][c] = e;
       part += e;
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) part = part + __shfl_xor(part, off);
     const float sum = part;
-    for (int i = lane; i < ncomp; i += 64) row[i] = row[i] / sum;
+#pragma unroll
+    for (int c = 0; c < C; ++c) acc[rr][c] = acc[rr][c] / sum;
     if (a.p_cmp) {
       float* pc = a.p_cmp + (((int64_t)b * a.H + h) * a.T + t) * NB;
-      for (int i = lane; i < NB; i += 64) pc[i] = i < ncomp ? row[i] : 0.0f;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int i = c * 64 + lane;
+        if (i < NB) pc[i] = i < ncomp ? acc[rr][c] : 0.0f;
+      }
+    }
+    // Eq. 9 in the reference's (m, n) order, 64 selection blocks at a time from a
+    // per-wave copy of the columns they read
+    float* psr = ps + r * nsel;
+    for (int j0 = 0; j0 < nsel; j0 += 64) {
+      const int lo = j0 * a.s;
+#pragma unroll
+      for (int c = 0; c < C; ++c) {
+        const int i = c * 64 + lane;
+        if (i >= lo && i < lo + segw) pseg[i - lo] = i < ncomp ? acc[rr][c] : 0.0f;
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __builtin_amdgcn_wave_barrier();
+      const int j = j0 + lane;
+      if (j < nsel) {
+        float s9 = 0.0f;
+        for (int m = 0; m < a.s; ++m)
+          for (int nn = 0; nn < a.a; ++nn) {
+            const int ci = a.s * j + m + nn;
+            if (ci < NB) s9 += ci < ncomp ? pseg[ci - lo] : 0.0f;
+          }
+        psr[j] = s9;
+        if (a.p_slc) a.p_slc[(((int64_t)b * a.H + h) * a.T + t) * nsel + j] = s9;
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+      __builtin_amdgcn_wave_barrier();
     }
   }
   __syncthreads();
 
-  // ---- Eq. 9 per head, Eq. 10 over the group's heads ----
-  for (int x = tid; x < TT * nsel; x += 256) {
+  // ---- Eq. 10: heads added in head order ----
+  for (int x = tid; x < TT * nsel; x += blockDim.x) {
     const int tt = x / nsel, j = x % nsel;
-    const int t = t0 + tt;
     float ag = 0.0f;
-    for (int hh = 0; hh < a.hpg; ++hh) {
-      const float* row = ev + (int64_t)(tt * a.hpg + hh) * ncomp;
-      float acc = 0.0f;
-      for (int m = 0; m < a.s; ++m)
-        for (int nn = 0; nn < a.a; ++nn) {
-          const int ci = a.s * j + m + nn;
-          if (ci < NB) acc += ci < ncomp ? row[ci] : 0.0f;
-        }
-      if (a.p_slc) a.p_slc[(((int64_t)b * a.H + g * a.hpg + hh) * a.T + t) * nsel + j] = acc;
-      ag += acc;
-    }
+    for (int hh = 0; hh < hpg; ++hh) ag += ps[(tt * hpg + hh) * nsel + j];
     agg[tt * nsel + j] = ag;
   }
   __syncthreads();
 
   // ---- top-n (one wave per timestep) ----
   const int kk = min(a.n, nsel);
-  for (int tt = wave; tt < TT; tt += 4) {
+  for (int tt = wave; tt < TT; tt += NW) {
     const int t = t0 + tt;
     float* ag = agg + tt * nsel;
     for (int rk = 0; rk < kk; ++rk) {
@@ -248,62 +291,89 @@ __global__ __launch_bounds__(256) void score_topn_kernel(ScoreArgs a) {
     }
     if (lane == 0) {
       int64_t* o = a.out + b * a.so_b + g * a.so_g + (int64_t)t * a.so_t;
-      int64_t sel[64];
+      int* sel = chosen + tt * 64;
       int no = 0;
-      int64_t cand[3];
-      int nc = 0;
-      if (a.include_fixed) {
-        cand[nc++] = 0;
-        cand[nc++] = t >= a.lprime ? (t - a.lprime) / a.lprime : 0;
-        cand[nc++] = t / a.lprime;
-      }
+      // fixed candidates [0, max(0, (t - l') / l'), t / l'] first
+      const int nc = a.include_fixed ? 3 : 0;
+      const int c1 = t >= a.lprime ? (t - a.lprime) / a.lprime : 0;
+      const int c2 = t / a.lprime;
       for (int c = 0; c < nc + kk && no < a.n; ++c) {
-        const int64_t v = c < nc ? cand[c] : (int64_t)top[tt * 64 + c - nc];
+        const int v = c < nc ? (c == 0 ? 0 : c == 1 ? c1 : c2) : top[tt * 64 + c - nc];
         bool dup = false;
         for (int u = 0; u < no; ++u) dup |= sel[u] == v;
         if (!dup) sel[no++] = v;
       }
-      for (int u = 0; u < a.n; ++u) o[(int64_t)u * a.so_n] = u < no ? sel[u] : -1;
+      for (int u = 0; u < a.n; ++u) o[(int64_t)u * a.so_n] = u < no ? (int64_t)sel[u] : -1;
     }
   }
 }
 
-template <typename S, int R>
-static hipError_t launch_score_R(const ScoreArgs& a, size_t lds, hipStream_t st) {
-  auto fn = score_topn_kernel<S, R>;
+template <typename S, int RPW, int C>
+static hipError_t launch_score_k(const ScoreArgs& a, int nw, size_t lds, hipStream_t st) {
+  auto fn = score_topn_kernel<S, RPW, C>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid((a.T + a.TT - 1) / a.TT, a.B * a.G);
-  hipLaunchKernelGGL(fn, grid, dim3(256), lds, st, a);
+  hipLaunchKernelGGL(fn, grid, dim3(64 * nw), lds, st, a, reinterpret_cast<const S*>(a.q));
   return hipGetLastError();
 }
 
-template <typename S>
-static hipError_t launch_score_T(const ScoreArgs& a, int rows, size_t lds, hipStream_t st) {
-  if (rows <= 4) return launch_score_R<S, 4>(a, lds, st);
-  if (rows <= 8) return launch_score_R<S, 8>(a, lds, st);
-  if (rows <= 16) return launch_score_R<S, 16>(a, lds, st);
-  if (rows <= 32) return launch_score_R<S, 32>(a, lds, st);
-  return launch_score_R<S, 64>(a, lds, st);
+template <typename S, int RPW>
+static hipError_t launch_score_c(const ScoreArgs& a, int nw, int C, size_t lds, hipStream_t st) {
+  switch (C) {
+    case 1: return launch_score_k<S, RPW, 1>(a, nw, lds, st);
+    case 2: return launch_score_k<S, RPW, 2>(a, nw, lds, st);
+    case 4: return launch_score_k<S, RPW, 4>(a, nw, lds, st);
+    case 8: return launch_score_k<S, RPW, 8>(a, nw, lds, st);
+    case 16: if constexpr (RPW <= 8) return launch_score_k<S, RPW, 16>(a, nw, lds, st); break;
+    case 32: if constexpr (RPW <= 4) return launch_score_k<S, RPW, 32>(a, nw, lds, st); break;
+    case 64: if constexpr (RPW <= 2) return launch_score_k<S, RPW, 64>(a, nw, lds, st); break;
+  }
+  return hipErrorInvalidValue;
 }
 
-// Returns 0 on success, 1 when the shape needs more LDS than a workgroup has,
-// 2 on a HIP launch error.
+template <typename S>
+static hipError_t launch_score_r(const ScoreArgs& a, int nw, int RPW, int C, size_t lds, hipStream_t st) {
+  switch (RPW) {
+    case 1: return launch_score_c<S, 1>(a, nw, C, lds, st);
+    case 2: return launch_score_c<S, 2>(a, nw, C, lds, st);
+    case 4: return launch_score_c<S, 4>(a, nw, C, lds, st);
+    case 8: return launch_score_c<S, 8>(a, nw, C, lds, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+static int pow2_at_least(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+
+// Picks (waves, timesteps, rows per wave, column chunks) for the shape.  Returns 0 on
+// success, 1 when no configuration fits (too many heads or compressed blocks), 2 on a
+// HIP launch error.
 int launch_score_topn(int dtype, ScoreArgs a, hipStream_t st) {
   constexpr size_t kLdsMax = 160 * 1024;
-  int TT = a.hpg >= 16 ? 1 : 16 / a.hpg;
-  for (;;) {
-    const int rows = TT * a.hpg;
-    const size_t lds = 4 * ((size_t)rows * a.dk + (size_t)rows * a.NB + (size_t)TT * a.nsel + (size_t)TT * 64);
-    if (rows <= kMaxRows && lds <= kLdsMax) {
-      a.TT = TT;
-      hipError_t e = dtype == kF32 ? launch_score_T<float>(a, rows, lds, st) : launch_score_T<uint16_t>(a, rows, lds, st);
-      return e == hipSuccess ? 0 : 2;
-    }
-    if (TT == 1) return 1;
-    TT /= 2;
-  }
+  if (a.NB > kMaxCols) return 1;
+  const int C = pow2_at_least(max(1, (a.NB + 63) / 64));
+  // accumulator budget per lane: RPW * C <= 64 preferred, 128 at most
+  for (int budget : {64, 128})
+    for (int nw : {4, 8})
+      for (int TT : {4, 2, 1}) {
+        if (TT > 1 && TT * a.hpg > kMaxRows) continue;
+        const int rows = TT * a.hpg;
+        const int RPW = pow2_at_least((rows + nw - 1) / nw);
+        if (RPW > 8 || RPW * C > budget) continue;
+        const int segw = 64 * a.s + a.a;
+        const size_t lds = 4 * ((size_t)nw * segw + (size_t)rows * a.nsel + (size_t)TT * a.nsel + (size_t)TT * 128);
+        if (lds > kLdsMax) continue;
+        a.TT = TT;
+        hipError_t e = dtype == kF32 ? launch_score_r<float>(a, nw, RPW, C, lds, st)
+                                     : launch_score_r<uint16_t>(a, nw, RPW, C, lds, st);
+        return e == hipSuccess ? 0 : 2;
+      }
+  return 1;
 }
 
 }  // namespace nsa
@@ -341,6 +411,9 @@ extern "C" int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* b
       return nsa::set_error(NSA_ERR_LAYOUT,
                             "k_cmp needs a unit-stride feature axis (the [Z,G,N,dk] storage of the reference's "
                             "[Z,G,dk,N] view) with 16-byte aligned rows");
+    const bool qok = stride_qk == 1 && ((uintptr_t)q) % 16 == 0 && (Z == 1 || (stride_qz * esz) % 16 == 0) &&
+                     (H == 1 || (stride_qh * esz) % 16 == 0) && (n_ctx == 1 || (stride_qm * esz) % 16 == 0);
+    if (!qok) return nsa::set_error(NSA_ERR_LAYOUT, "q needs a unit-stride feature axis with 16-byte aligned rows");
   }
   if (n_ctx == 0) return NSA_OK;
   ScoreArgs a{};
@@ -382,7 +455,12 @@ extern "C" int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* b
     TimingScope ts(kIdScore, (hipStream_t)stream);
     rc = launch_score_topn(dtype, a, (hipStream_t)stream);
   }
-  if (rc == 1) return nsa::set_error(NSA_ERR_UNSUPPORTED, "scores of one timestep exceed the LDS of a workgroup");
+  if (rc == 1) {
+    char msg[128];
+    snprintf(msg, sizeof(msg), "no scoring configuration for %d heads per group and %d compressed blocks", a.hpg,
+             a.NB);
+    return nsa::set_error(NSA_ERR_UNSUPPORTED, msg);
+  }
   if (rc == 2) return nsa::set_error(NSA_ERR_HIP, hipGetErrorString(hipGetLastError()));
   return NSA_OK;
 }
