@@ -144,36 +144,34 @@ __global__ __launch_bounds__(512) void score_topn_kernel(ScoreArgs a, const S* _
     for (int c = 0; c < C; ++c) acc[rr][c] = 0.0f;
   const S* kc = reinterpret_cast<const S*>(a.kc) + b * a.sk_b + g * a.sk_g;
   const S* qb = qg + b * a.sq_b;
-  for (int e0 = 0; e0 < dk; e0 += EV) {
-    float qv[RPW][EV];
+  const S* kcol[C];  // the lane's compressed-key rows (past the last block: the last one)
 #pragma unroll
-    for (int rr = 0; rr < RPW; ++rr) {
-      const int r = min(wave + NW * rr, rows - 1);
-      const int t = t0 + r / hpg, h = g * hpg + r % hpg;
-      unpack16<S>(*reinterpret_cast<const uint4*>(qb + (int64_t)h * a.sq_h + (int64_t)t * a.sq_t + e0), qv[rr]);
-    }
-    // the key loads of up to 8 chunks are issued (unconditionally: lanes past the last
-    // block re-read it) before the first FMA waits on one
-    constexpr int CB = C < 8 ? C : 8;
+  for (int c = 0; c < C; ++c) kcol[c] = kc + (int64_t)min(c * 64 + lane, ncomp - 1) * a.sk_i;
+  // Chunks are processed CB at a time, each group under a wave-uniform branch around its
+  // own pass over the feature axis, so groups past the last visible block cost nothing.
+  constexpr int CB = C < 2 ? C : 2;
 #pragma unroll
-    for (int cb = 0; cb < C; cb += CB) {
-      if (cb < nch) {
+  for (int cb = 0; cb < C; cb += CB) {
+    if (cb < nch) {
+      for (int e0 = 0; e0 < dk; e0 += EV) {
+        float qv[RPW][EV];
+#pragma unroll
+        for (int rr = 0; rr < RPW; ++rr) {
+          const int r = min(wave + NW * rr, rows - 1);
+          const int t = t0 + r / hpg, h = g * hpg + r % hpg;
+          unpack16<S>(*reinterpret_cast<const uint4*>(qb + (int64_t)h * a.sq_h + (int64_t)t * a.sq_t + e0), qv[rr]);
+        }
         uint4 kraw[CB];
 #pragma unroll
-        for (int c = 0; c < CB; ++c) {
-          const int i = min((cb + c) * 64 + lane, ncomp - 1);
-          kraw[c] = *reinterpret_cast<const uint4*>(kc + (int64_t)i * a.sk_i + e0);
-        }
+        for (int c = 0; c < CB; ++c) kraw[c] = *reinterpret_cast<const uint4*>(kcol[cb + c] + e0);
 #pragma unroll
         for (int c = 0; c < CB; ++c) {
-          if (cb + c < nch) {
-            float kv[EV];
-            unpack16<S>(kraw[c], kv);
+          float kv[EV];
+          unpack16<S>(kraw[c], kv);
 #pragma unroll
-            for (int rr = 0; rr < RPW; ++rr)
+          for (int rr = 0; rr < RPW; ++rr)
 #pragma unroll
-              for (int u = 0; u < EV; ++u) acc[rr][cb + c] = fmaf(qv[rr][u], kv[u], acc[rr][cb + c]);
-          }
+            for (int u = 0; u < EV; ++u) acc[rr][cb + c] = fmaf(qv[rr][u], kv[u], acc[rr][cb + c]);
         }
       }
     }
@@ -189,10 +187,12 @@ __global__ __launch_bounds__(512) void score_topn_kernel(ScoreArgs a, const S* _
     bool anyv = false;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      acc[rr][c] = acc[rr][c] * a.scale;
-      const bool v = be[c] <= t;
-      anyv |= v;
-      if (v) mx = fmaxf(mx, acc[rr][c]);
+      if (c < nch) {
+        acc[rr][c] = acc[rr][c] * a.scale;
+        const bool v = be[c] <= t;
+        anyv |= v;
+        if (v) mx = fmaxf(mx, acc[rr][c]);
+      }
     }
     const bool any_row = __ballot(anyv) != 0ull;
     if (!any_row) mx = __shfl(acc[rr][0], 0);  // block 0 made visible
@@ -202,22 +202,25 @@ __global__ __launch_bounds__(512) void score_topn_kernel(ScoreArgs a, const S* _
     float part = 0.0f;
 #pragma unroll
     for (int c = 0; c < C; ++c) {
-      const bool v = be[c] <= t || (!any_row && c == 0 && lane == 0);
-      const float e = v ? exp32(acc[rr][c] - mx) : 0.0f;
-      acc[rr][c] = e;
-      part += e;
+      if (c < nch) {
+        const bool v = be[c] <= t || (!any_row && c == 0 && lane == 0);
+        const float e = v ? exp32(acc[rr][c] - mx) : 0.0f;
+        acc[rr][c] = e;
+        part += e;
+      }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) part = part + __shfl_xor(part, off);
     const float sum = part;
 #pragma unroll
-    for (int c = 0; c < C; ++c) acc[rr][c] = acc[rr][c] / sum;
+    for (int c = 0; c < C; ++c)
+      if (c < nch) acc[rr][c] = acc[rr][c] / sum;
     if (a.p_cmp) {
       float* pc = a.p_cmp + (((int64_t)b * a.H + h) * a.T + t) * NB;
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const int i = c * 64 + lane;
-        if (i < NB) pc[i] = i < ncomp ? acc[rr][c] : 0.0f;
+        if (i < NB) pc[i] = (c < nch && i < ncomp) ? acc[rr][c] : 0.0f;
       }
     }
     // Eq. 9 in the reference's (m, n) order, 64 selection blocks at a time from a
@@ -228,7 +231,7 @@ __global__ __launch_bounds__(512) void score_topn_kernel(ScoreArgs a, const S* _
 #pragma unroll
       for (int c = 0; c < C; ++c) {
         const int i = c * 64 + lane;
-        if (i >= lo && i < lo + segw) pseg[i - lo] = i < ncomp ? acc[rr][c] : 0.0f;
+        if (i >= lo && i < lo + segw) pseg[i - lo] = (c < nch && i < ncomp) ? acc[rr][c] : 0.0f;
       }
       __builtin_amdgcn_s_waitcnt(0);
       __builtin_amdgcn_wave_barrier();
