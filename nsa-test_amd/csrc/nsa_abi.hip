@@ -55,7 +55,7 @@ struct Shape {
 };
 
 struct Layout {
-  size_t kt = 0, kn = 0, vt = 0, vn = 0, lse2 = 0, delta = 0, clean = 0, chunk = 0, csr_off = 0, csr_t = 0,
+  size_t kt = 0, kn = 0, vt = 0, vn = 0, krf = 0, kcf = 0, vrf = 0, vcf = 0, lse2 = 0, delta = 0, clean = 0, chunk = 0, csr_off = 0, csr_t = 0,
          seg_off = 0, partial = 0, total = 0;
 };
 
@@ -71,14 +71,26 @@ Layout make_layout(const Shape& s, bool bwd) {
   const size_t BG = (size_t)s.Z * s.G;
   const size_t kbytes = BG * s.Tp() * s.dk * s.esz();
   const size_t vbytes = BG * s.Tp() * s.dv * s.esz();
-  L.kt = take(kbytes);
+  if (s.br == kSelection) {  // fragment-native operands only
+    L.krf = take(kbytes);
+    if (bwd) {
+      L.kcf = take(kbytes);
+      L.vrf = take(vbytes);
+    } else {
+      L.vcf = take(vbytes);
+    }
+  } else {
+    L.kt = take(kbytes);
+    if (bwd) {
+      L.kn = take(kbytes);
+      L.vn = take(vbytes);
+    } else {
+      L.vt = take(vbytes);
+    }
+  }
   if (bwd) {
-    L.kn = take(kbytes);
-    L.vn = take(vbytes);
     L.lse2 = take((size_t)s.Z * s.H * s.Tq * 4);
     L.delta = take((size_t)s.Z * s.H * s.Tq * 4);
-  } else {
-    L.vt = take(vbytes);
   }
   if (s.br == kSelection) {
     L.clean = take(BG * s.Tq * s.nslots * 4);
@@ -183,13 +195,17 @@ int run_fwd(const Shape& s, const FwdIO& io, float scale, int window, const int3
   a.window = window;
   a.block_ends = block_ends;
   a.causal = causal;
-  a.kt = at<char>(ws, L.kt);
-  a.vt = at<char>(ws, L.vt);
+  const bool sel = s.br == kSelection;
+  auto opt = [&](size_t off, bool use) -> void* { return use ? at<char>(ws, off) : nullptr; };
+  a.kt = opt(L.kt, !sel);
+  a.vt = opt(L.vt, !sel);
+  a.krf = opt(L.krf, sel);
+  a.vcf = opt(L.vcf, sel);
 
   launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp,
-                at<char>(ws, L.kt), nullptr, st);
+                const_cast<void*>(a.kt), nullptr, const_cast<void*>(a.krf), nullptr, st);
   launch_repack(s.dtype, io.V, io.sv[0], io.sv[1], io.sv[2], io.sv[3], s.Z, s.G, s.Tkv, s.dv, a.Tp, nullptr,
-                at<char>(ws, L.vt), st);
+                const_cast<void*>(a.vt), nullptr, const_cast<void*>(a.vcf), st);
   if (s.br == kSelection) {
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
                      s.Tkv, fallback, causal, at<int>(ws, L.clean), nullptr, s.nblk(), st);
@@ -264,18 +280,24 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.window = window;
   a.block_ends = block_ends;
   a.causal = causal;
-  a.kt = at<char>(ws, L.kt);
-  a.kn = at<char>(ws, L.kn);
-  a.vn = at<char>(ws, L.vn);
+  const bool sel = s.br == kSelection;
+  auto opt = [&](size_t off, bool use) -> void* { return use ? at<char>(ws, off) : nullptr; };
+  a.kt = opt(L.kt, !sel);
+  a.kn = opt(L.kn, !sel);
+  a.vn = opt(L.vn, !sel);
+  a.krf = opt(L.krf, sel);
+  a.kcf = opt(L.kcf, sel);
+  a.vrf = opt(L.vrf, sel);
   a.lse2 = at<float>(ws, L.lse2);
   a.delta = at<float>(ws, L.delta);
   a.items_per_bg = s.items_per_bg();
   a.partial = at<float>(ws, L.partial);
 
   launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp,
-                at<char>(ws, L.kt), at<char>(ws, L.kn), st);
+                const_cast<void*>(a.kt), const_cast<void*>(a.kn), const_cast<void*>(a.krf),
+                const_cast<void*>(a.kcf), st);
   launch_repack(s.dtype, io.V, io.sv[0], io.sv[1], io.sv[2], io.sv[3], s.Z, s.G, s.Tkv, s.dv, a.Tp,
-                at<char>(ws, L.vn), nullptr, st);
+                const_cast<void*>(a.vn), nullptr, const_cast<void*>(a.vrf), nullptr, st);
   launch_bwd_rowstats(s.dtype, a, s.dv, st);
   if (s.br == kSelection) {
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,

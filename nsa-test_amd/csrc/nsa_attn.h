@@ -31,6 +31,11 @@ struct AttnArgs {
   const void* kn;
   const void* vt;
   const void* vn;
+  // fragment-native copies (selection kernels): K rowfrag / colfrag, V rowfrag / colfrag
+  const void* krf;
+  const void* kcf;
+  const void* vrf;
+  const void* vcf;
   int Tp;
   // forward outputs / backward inputs
   void* o;

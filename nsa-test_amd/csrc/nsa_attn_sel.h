@@ -79,7 +79,8 @@ __global__ __launch_bounds__(256) void attn_sel_fwd_kernel(AttnArgs a, int ncolt
   __shared__ int s_lst[4][kSelMaxT * 64];
   __shared__ uint32_t s_bits[4][kSelMaxBlocks / 32];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform control below
   const int g4 = lane >> 4, c16 = lane & 15;
   const int L = xcd_contiguous(blockIdx.x, gridDim.x);
   const int bg = L / ncoltiles;
@@ -108,8 +109,8 @@ __global__ __launch_bounds__(256) void attn_sel_fwd_kernel(AttnArgs a, int ncolt
   for (int kc = 0; kc < NKC; ++kc)
     qf[kc] = colv ? *reinterpret_cast<const uint4*>(qp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
 
-  const S* kt = reinterpret_cast<const S*>(a.kt) + (int64_t)bg * a.Tp * DK;
-  const S* vt = reinterpret_cast<const S*>(a.vt) + (int64_t)bg * DV * a.Tp;
+  const S* krf = reinterpret_cast<const S*>(a.krf) + (int64_t)bg * a.Tp * DK;
+  const S* vcf = reinterpret_cast<const S*>(a.vcf) + (int64_t)bg * DV * a.Tp;
   f32x4 oacc[DV / 16];
 #pragma unroll
   for (int j = 0; j < DV / 16; ++j) oacc[j] = zero4();
@@ -117,72 +118,112 @@ __global__ __launch_bounds__(256) void attn_sel_fwd_kernel(AttnArgs a, int ncolt
   const int nwords = (a.nblk + 31) / 32;
   const bool one_t = w.nt == 1;
 
-  for (int wd = 0; wd < nwords; ++wd) {
-    uint32_t word = bits[wd];
-    while (word) {
-      const int blk = wd * 32 + __builtin_ctz(word);
-      word &= word - 1;
-      const int blk_lo = blk * a.lprime;
-      const int blk_hi = min(blk_lo + a.lprime, a.Tkv);
-      const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
-      // tiles start on a 32-key boundary (the C-permuted chunks of vt / kn)
-      for (int key0 = blk_lo & ~31; key0 < blk_hi; key0 += 64) {
-        if (a.causal && key0 > t_last) break;
-        // S^T[key, col] for the 64 keys of this tile
-        f32x4 st[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const S* krow = kt + (int64_t)(key0 + ks * 16 + c16) * DK;
-          st[ks] = zero4();
-#pragma unroll
-          for (int kc = 0; kc < NKC; ++kc)
-            st[ks] = Mma<T>::run(st[ks], *reinterpret_cast<const uint4*>(krow + kc * KC + g4 * EPF), qf[kc]);
-        }
-        const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 >= blk_lo &&
-                                 key0 + 63 < blk_hi && f0 + kSelWaveCols <= ncols;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = key0 + ks * 16 + 4 * g4 + i;
-            const bool ok = all_visible || (colsel && (!a.causal || key <= colt) && key >= blk_lo && key < blk_hi);
-            const float v = ok ? st[ks][i] * scale2 : -INFINITY;
-            st[ks][i] = v;
-            mx = fmaxf(mx, v);
-          }
-        mx = wave_max16(mx);
-        const float mnew = fmaxf(m2, mx);
-        const float mref = mnew == -INFINITY ? 0.f : mnew;
-        float rs = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = fast_exp2(st[ks][i] - mref);
-            st[ks][i] = p;
-            rs += p;
-          }
-        rs = wave_sum16(rs);
-        if (__ballot(mnew > m2) != 0ull) {
-          const float alpha = fast_exp2(m2 - mref);
-          lsum *= alpha;
-#pragma unroll
-          for (int j = 0; j < DV / 16; ++j) oacc[j] *= alpha;
-        }
-        lsum += rs;
-        m2 = mnew;
-#pragma unroll
-        for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
-          const uint4 pf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
-#pragma unroll
-          for (int j = 0; j < DV / 16; ++j) {
-            const uint4 vf = frag_cperm<T>(vt + (int64_t)(j * 16 + c16) * a.Tp + key0 + kc2 * CK, g4);
-            oacc[j] = Mma<T>::run(oacc[j], vf, pf);
-          }
-        }
-      }
+  // Tile cursor over the union bitmap (wave-uniform scalar state).  Tiles start on a
+  // 32-key boundary (the C-permuted chunks of vt / kn) and cover 64 keys.
+  int c_wd = -1, c_blk = -1, c_key0 = 0, c_hi = 0;
+  uint32_t c_word = 0;
+  auto advance = [&]() -> bool {
+    if (c_blk >= 0) {
+      c_key0 += 64;
+      if (c_key0 < c_hi && !(a.causal && c_key0 > t_last)) return true;
     }
+    while (c_word == 0) {
+      if (++c_wd >= nwords) return false;
+      c_word = __builtin_amdgcn_readfirstlane(bits[c_wd]);
+    }
+    c_blk = c_wd * 32 + __builtin_ctz(c_word);
+    c_word &= c_word - 1;
+    const int lo = c_blk * a.lprime;
+    c_hi = min(lo + a.lprime, a.Tkv);
+    c_key0 = lo & ~31;
+    return true;
+  };
+  // K fragments of a tile (S^T = K Q^T) and V^T fragments (O^T += V^T P^T): the next
+  // tile's K is requested as soon as the current S^T is issued, its V as soon as the
+  // current P V is, so the loads overlap the softmax and the products.
+  uint4 kf[4][NKC], vf[64 / CK][DV / 16];
+  auto load_k = [&](int key0) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc)
+        kf[ks][kc] = ld_rowfrag<T>(krf, (key0 >> 4) + ks, kc, DK, lane);
+  };
+  auto load_v = [&](int key0) {
+#pragma unroll
+    for (int kc2 = 0; kc2 < 64 / CK; ++kc2)
+#pragma unroll
+      for (int j = 0; j < DV / 16; ++j)
+        vf[kc2][j] = ld_colfrag<T>(vcf, key0 / CK + kc2, j, DV, lane);
+  };
+
+  bool have = advance();
+  if (have) {
+    load_k(c_key0);
+    load_v(c_key0);
+  }
+  while (have) {
+    const int key0 = c_key0, blk = c_blk;
+    const int blk_lo = blk * a.lprime;
+    const int blk_hi = c_hi;
+    // S^T[key, col] for the 64 keys of this tile
+    f32x4 st[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      st[ks] = zero4();
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) st[ks] = Mma<T>::run(st[ks], kf[ks][kc], qf[kc]);
+    }
+    const bool have_next = advance();
+    if (have_next) load_k(c_key0);
+
+    const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
+    // end of the keys of this block the lane's column sees (blk_lo when none)
+    const int kend = colsel ? max(blk_lo, a.causal ? min(blk_hi, colt + 1) : blk_hi) : blk_lo;
+    const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 >= blk_lo &&
+                             key0 + 63 < blk_hi && f0 + kSelWaveCols <= ncols;
+    float mx = -INFINITY;
+    // lane-visible keys of this block: [blk_lo, kend); branch-free test per element
+    const uint32_t span = all_visible ? 0xffffffffu : (uint32_t)(kend - blk_lo);
+    const int kb = key0 + 4 * g4 - blk_lo;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = (uint32_t)(kb + ks * 16 + i) < span;
+        const float v = ok ? st[ks][i] * scale2 : -INFINITY;
+        st[ks][i] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = wave_max16(mx);
+    const float mnew = fmaxf(m2, mx);
+    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    float rs = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = fast_exp2(st[ks][i] - mref);
+        st[ks][i] = p;
+        rs += p;
+      }
+    rs = wave_sum16(rs);
+    if (__ballot(mnew > m2) != 0ull) {
+      const float alpha = fast_exp2(m2 - mref);
+      lsum *= alpha;
+#pragma unroll
+      for (int j = 0; j < DV / 16; ++j) oacc[j] *= alpha;
+    }
+    lsum += rs;
+    m2 = mnew;
+#pragma unroll
+    for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
+      const uint4 pf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
+#pragma unroll
+      for (int j = 0; j < DV / 16; ++j) oacc[j] = Mma<T>::run(oacc[j], vf[kc2][j], pf);
+    }
+    if (have_next) load_v(c_key0);
+    have = have_next;
   }
 
   if (colv) {
@@ -217,7 +258,8 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
   __shared__ int s_lst[4][kSelMaxT * 64];
   __shared__ uint32_t s_bits[4][kSelMaxBlocks / 32];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform control below
   const int g4 = lane >> 4, c16 = lane & 15;
   const int L = xcd_contiguous(blockIdx.x, gridDim.x);
   const int bg = L / ncoltiles;
@@ -256,9 +298,9 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
   const float l2 = colv ? a.lse2[srow] : INFINITY;
   const float dl = colv ? a.delta[srow] : 0.f;
 
-  const S* kt = reinterpret_cast<const S*>(a.kt) + (int64_t)bg * a.Tp * DK;
-  const S* kn = reinterpret_cast<const S*>(a.kn) + (int64_t)bg * DK * a.Tp;
-  const S* vn = reinterpret_cast<const S*>(a.vn) + (int64_t)bg * a.Tp * DV;
+  const S* krf = reinterpret_cast<const S*>(a.krf) + (int64_t)bg * a.Tp * DK;
+  const S* kcf = reinterpret_cast<const S*>(a.kcf) + (int64_t)bg * DK * a.Tp;
+  const S* vrf = reinterpret_cast<const S*>(a.vrf) + (int64_t)bg * a.Tp * DV;
   f32x4 dqa[DK / 16];
 #pragma unroll
   for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
@@ -266,38 +308,39 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
   const bool one_t = w.nt == 1;
 
   for (int wd = 0; wd < nwords; ++wd) {
-    uint32_t word = bits[wd];
+    uint32_t word = __builtin_amdgcn_readfirstlane(bits[wd]);  // wave-uniform
     while (word) {
       const int blk = wd * 32 + __builtin_ctz(word);
       word &= word - 1;
       const int blk_lo = blk * a.lprime;
       const int blk_hi = min(blk_lo + a.lprime, a.Tkv);
       const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
+      // end of the keys of this block the lane's column sees (blk_lo when none)
+      const int kend = colsel ? max(blk_lo, a.causal ? min(blk_hi, colt + 1) : blk_hi) : blk_lo;
       // tiles start on a 32-key boundary (the C-permuted chunks of vt / kn)
       for (int key0 = blk_lo & ~31; key0 < blk_hi; key0 += 64) {
         if (a.causal && key0 > t_last) break;
         f32x4 st[4], dp[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
-          const S* krow = kt + (int64_t)(key0 + ks * 16 + c16) * DK;
-          const S* vrow = vn + (int64_t)(key0 + ks * 16 + c16) * DV;
           st[ks] = zero4();
           dp[ks] = zero4();
 #pragma unroll
           for (int kc = 0; kc < NKC; ++kc)
-            st[ks] = Mma<T>::run(st[ks], *reinterpret_cast<const uint4*>(krow + kc * KC + g4 * EPF), qf[kc]);
+            st[ks] = Mma<T>::run(st[ks], ld_rowfrag<T>(krf, (key0 >> 4) + ks, kc, DK, lane), qf[kc]);
 #pragma unroll
           for (int kc = 0; kc < NVC; ++kc)
-            dp[ks] = Mma<T>::run(dp[ks], *reinterpret_cast<const uint4*>(vrow + kc * KC + g4 * EPF), dof[kc]);
+            dp[ks] = Mma<T>::run(dp[ks], ld_rowfrag<T>(vrf, (key0 >> 4) + ks, kc, DV, lane), dof[kc]);
         }
         const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 >= blk_lo &&
                                  key0 + 63 < blk_hi && f0 + kSelWaveCols <= ncols;
+        const uint32_t span = all_visible ? 0xffffffffu : (uint32_t)(kend - blk_lo);
+        const int kb = key0 + 4 * g4 - blk_lo;
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int key = key0 + ks * 16 + 4 * g4 + i;
-            const bool ok = all_visible || (colsel && (!a.causal || key <= colt) && key >= blk_lo && key < blk_hi);
+            const bool ok = (uint32_t)(kb + ks * 16 + i) < span;
             const float p = ok ? fast_exp2(st[ks][i] * scale2 - l2) : 0.f;
             st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
           }
@@ -306,7 +349,7 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
           const uint4 sf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
 #pragma unroll
           for (int j = 0; j < DK / 16; ++j) {
-            const uint4 kf = frag_cperm<T>(kn + (int64_t)(j * 16 + c16) * a.Tp + key0 + kc2 * CK, g4);
+            const uint4 kf = ld_colfrag<T>(kcf, key0 / CK + kc2, j, DK, lane);
             dqa[j] = Mma<T>::run(dqa[j], kf, sf);
           }
         }

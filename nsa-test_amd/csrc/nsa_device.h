@@ -119,6 +119,38 @@ template <> __device__ __forceinline__ uint4 frag_cperm<bf16>(const uint16_t* ro
   return *reinterpret_cast<const uint4*>(row + 8 * g);
 }
 
+// Fragment-native operand layouts of a [R][C] matrix (R on the time axis, C features;
+// R a multiple of 64, C of 32): every 16-byte MFMA fragment of a 64-lane wave sits at
+// lane * 16 bytes of one contiguous 1 KB tile, so a fragment load is one coalesced
+// 1 KB request instead of 16 row pieces.
+//  rowfrag: A/B operand whose rows are time (16 per tile) and whose K slots run along
+//           the features (kKChunk per tile; lane g*16 + r holds features g*kPerFrag..).
+//  colfrag: operand whose rows are features (16 per tile) and whose K slots run along
+//           time in the C-permuted order of a CFrag chunk (lane g*16 + f holds the
+//           kPerFrag times of group g).
+template <typename T>
+__host__ __device__ __forceinline__ int64_t rowfrag_off(int r, int c, int C) {
+  constexpr int EPF = Elem<T>::kPerFrag, KC = Elem<T>::kKChunk;
+  return ((((int64_t)(r >> 4) * (C / KC) + c / KC) * 64 + ((c % KC) / EPF) * 16 + (r & 15)) * EPF) + (c % EPF);
+}
+template <typename T>
+__host__ __device__ __forceinline__ int64_t colfrag_off(int r, int c, int C) {
+  constexpr int EPF = Elem<T>::kPerFrag, CK = CFrag<T>::kKeys;
+  const int p = CK == 32 ? cperm_pos32(r & 31) : (r & 15);
+  return ((((int64_t)(r / CK) * (C / 16) + (c >> 4)) * 64 + (p / EPF) * 16 + (c & 15)) * EPF) + (p % EPF);
+}
+// the lane's fragment of rowfrag tile (row16, kc) / colfrag tile (chunk, fgroup)
+template <typename T>
+__device__ __forceinline__ uint4 ld_rowfrag(const typename Store<T>::type* m, int row16, int kc, int C, int lane) {
+  constexpr int EPF = Elem<T>::kPerFrag, KC = Elem<T>::kKChunk;
+  return *reinterpret_cast<const uint4*>(m + (((int64_t)row16 * (C / KC) + kc) * 64 + lane) * EPF);
+}
+template <typename T>
+__device__ __forceinline__ uint4 ld_colfrag(const typename Store<T>::type* m, int chunk, int fg, int C, int lane) {
+  constexpr int EPF = Elem<T>::kPerFrag;
+  return *reinterpret_cast<const uint4*>(m + (((int64_t)chunk * (C / 16) + fg) * 64 + lane) * EPF);
+}
+
 // Standard fragment: 16 contiguous bytes at row[kchunk_base + g * kPerFrag].
 template <typename T>
 __device__ __forceinline__ uint4 frag_std(const typename Store<T>::type* row, int g) {

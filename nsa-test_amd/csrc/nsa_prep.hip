@@ -2,6 +2,8 @@
 // zero-padded layouts the attention kernels stage from, and the per-row backward
 // statistics.  All of these are HBM streams over group-sized (not head-sized)
 // tensors, except bwd_rowstats which reads O and dO once.
+#include <type_traits>
+
 #include "nsa_attn.h"
 #include "nsa_device.h"
 #include "nsa_kernels.h"
@@ -11,10 +13,13 @@ namespace nsa {
 // Source matrix per (b,g): element (r, c) at src + b*s_b + g*s_g + r*s_r + c*s_c,
 // r < R (time), c < C (feature).  Writes, for r < Rp (rows >= R zero-filled):
 //   rowm[bg][r][c]  (if non-null)     colm[bg][c][r]  (if non-null)
+//   rowf (if non-null): the rowfrag layout, colf (if non-null): the colfrag layout.
 template <typename S>
 __global__ __launch_bounds__(256) void repack_kernel(const S* __restrict__ src, int64_t s_b, int64_t s_g,
                                                      int64_t s_r, int64_t s_c, int G, int R, int C, int Rp,
-                                                     S* __restrict__ rowm, S* __restrict__ colm) {
+                                                     S* __restrict__ rowm, S* __restrict__ colm,
+                                                     S* __restrict__ rowf, S* __restrict__ colf) {
+  using T = typename std::conditional<sizeof(S) == 2, bf16, float>::type;
   __shared__ S tile[64][65];
   const int bg = blockIdx.z;
   const int b = bg / G, g = bg % G;
@@ -53,17 +58,33 @@ __global__ __launch_bounds__(256) void repack_kernel(const S* __restrict__ src, 
       if (r < Rp && c < C) colm[obase + (int64_t)c * Rp + rpos] = tile[rr][cc];
     }
   }
+  // fragment-native layouts: consecutive threads write consecutive elements
+  if (rowf) {
+    for (int i = tid; i < 64 * 64; i += 256) {
+      const int rr = i >> 6, cc = i & 63;
+      const int r = r0 + rr, c = c0 + cc;
+      if (r < Rp && c < C) rowf[obase + rowfrag_off<T>(r, c, C)] = tile[rr][cc];
+    }
+  }
+  if (colf) {
+    for (int i = tid; i < 64 * 64; i += 256) {
+      const int cc = i >> 6, rr = i & 63;
+      const int r = r0 + rr, c = c0 + cc;
+      if (r < Rp && c < C) colf[obase + colfrag_off<T>(r, c, C)] = tile[rr][cc];
+    }
+  }
 }
 
 void launch_repack(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t s_r, int64_t s_c, int B, int G,
-                   int R, int C, int Rp, void* rowm, void* colm, hipStream_t st) {
+                   int R, int C, int Rp, void* rowm, void* colm, void* rowf, void* colf, hipStream_t st) {
+  if (!rowm && !colm && !rowf && !colf) return;
   dim3 grid((Rp + 63) / 64, (C + 63) / 64, B * G);
   if (dtype == kF32) {
     hipLaunchKernelGGL(repack_kernel<float>, grid, dim3(256), 0, st, (const float*)src, s_b, s_g, s_r, s_c, G, R, C,
-                       Rp, (float*)rowm, (float*)colm);
+                       Rp, (float*)rowm, (float*)colm, (float*)rowf, (float*)colf);
   } else {
     hipLaunchKernelGGL(repack_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, s_b, s_g, s_r, s_c, G,
-                       R, C, Rp, (uint16_t*)rowm, (uint16_t*)colm);
+                       R, C, Rp, (uint16_t*)rowm, (uint16_t*)colm, (uint16_t*)rowf, (uint16_t*)colf);
   }
 }
 
