@@ -307,54 +307,83 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
   const int nwords = (a.nblk + 31) / 32;
   const bool one_t = w.nt == 1;
 
-  for (int wd = 0; wd < nwords; ++wd) {
-    uint32_t word = __builtin_amdgcn_readfirstlane(bits[wd]);  // wave-uniform
-    while (word) {
-      const int blk = wd * 32 + __builtin_ctz(word);
-      word &= word - 1;
-      const int blk_lo = blk * a.lprime;
-      const int blk_hi = min(blk_lo + a.lprime, a.Tkv);
-      const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
-      // end of the keys of this block the lane's column sees (blk_lo when none)
-      const int kend = colsel ? max(blk_lo, a.causal ? min(blk_hi, colt + 1) : blk_hi) : blk_lo;
-      // tiles start on a 32-key boundary (the C-permuted chunks of vt / kn)
-      for (int key0 = blk_lo & ~31; key0 < blk_hi; key0 += 64) {
-        if (a.causal && key0 > t_last) break;
-        f32x4 st[4], dp[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          st[ks] = zero4();
-          dp[ks] = zero4();
-#pragma unroll
-          for (int kc = 0; kc < NKC; ++kc)
-            st[ks] = Mma<T>::run(st[ks], ld_rowfrag<T>(krf, (key0 >> 4) + ks, kc, DK, lane), qf[kc]);
-#pragma unroll
-          for (int kc = 0; kc < NVC; ++kc)
-            dp[ks] = Mma<T>::run(dp[ks], ld_rowfrag<T>(vrf, (key0 >> 4) + ks, kc, DV, lane), dof[kc]);
-        }
-        const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 >= blk_lo &&
-                                 key0 + 63 < blk_hi && f0 + kSelWaveCols <= ncols;
-        const uint32_t span = all_visible ? 0xffffffffu : (uint32_t)(kend - blk_lo);
-        const int kb = key0 + 4 * g4 - blk_lo;
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool ok = (uint32_t)(kb + ks * 16 + i) < span;
-            const float p = ok ? fast_exp2(st[ks][i] * scale2 - l2) : 0.f;
-            st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
-          }
-#pragma unroll
-        for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
-          const uint4 sf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
-#pragma unroll
-          for (int j = 0; j < DK / 16; ++j) {
-            const uint4 kf = ld_colfrag<T>(kcf, key0 / CK + kc2, j, DK, lane);
-            dqa[j] = Mma<T>::run(dqa[j], kf, sf);
-          }
-        }
-      }
+  // wave-uniform tile cursor over the union bitmap (as in the forward)
+  int c_wd = -1, c_blk = -1, c_key0 = 0, c_hi = 0;
+  uint32_t c_word = 0;
+  auto advance = [&]() -> bool {
+    if (c_blk >= 0) {
+      c_key0 += 64;
+      if (c_key0 < c_hi && !(a.causal && c_key0 > t_last)) return true;
     }
+    while (c_word == 0) {
+      if (++c_wd >= nwords) return false;
+      c_word = __builtin_amdgcn_readfirstlane(bits[c_wd]);
+    }
+    c_blk = c_wd * 32 + __builtin_ctz(c_word);
+    c_word &= c_word - 1;
+    const int lo = c_blk * a.lprime;
+    c_hi = min(lo + a.lprime, a.Tkv);
+    c_key0 = lo & ~31;
+    return true;
+  };
+  // K and V rowfrags of a tile feed S^T = K Q^T and dP^T = V dO^T; the K colfrags feed
+  // dQ^T += K^T dS^T.  The colfrags are requested once S^T / dP^T are issued and the
+  // next tile's rowfrags once this tile's are consumed, so loads overlap the softmax.
+  uint4 kf[4][NKC], vf[4][NVC], knf[64 / CK][DK / 16];
+  auto load_rows = [&](int key0) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) kf[ks][kc] = ld_rowfrag<T>(krf, (key0 >> 4) + ks, kc, DK, lane);
+#pragma unroll
+      for (int kc = 0; kc < NVC; ++kc) vf[ks][kc] = ld_rowfrag<T>(vrf, (key0 >> 4) + ks, kc, DV, lane);
+    }
+  };
+  bool have = advance();
+  if (have) load_rows(c_key0);
+  while (have) {
+    const int key0 = c_key0, blk = c_blk;
+    const int blk_lo = blk * a.lprime;
+    const int blk_hi = c_hi;
+    f32x4 st[4], dp[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      st[ks] = zero4();
+      dp[ks] = zero4();
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) st[ks] = Mma<T>::run(st[ks], kf[ks][kc], qf[kc]);
+#pragma unroll
+      for (int kc = 0; kc < NVC; ++kc) dp[ks] = Mma<T>::run(dp[ks], vf[ks][kc], dof[kc]);
+    }
+#pragma unroll
+    for (int kc2 = 0; kc2 < 64 / CK; ++kc2)
+#pragma unroll
+      for (int j = 0; j < DK / 16; ++j) knf[kc2][j] = ld_colfrag<T>(kcf, key0 / CK + kc2, j, DK, lane);
+    const bool have_next = advance();
+    if (have_next) load_rows(c_key0);
+
+    const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
+    // end of the keys of this block the lane's column sees (blk_lo when none)
+    const int kend = colsel ? max(blk_lo, a.causal ? min(blk_hi, colt + 1) : blk_hi) : blk_lo;
+    const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 >= blk_lo &&
+                             key0 + 63 < blk_hi && f0 + kSelWaveCols <= ncols;
+    const uint32_t span = all_visible ? 0xffffffffu : (uint32_t)(kend - blk_lo);
+    const int kb = key0 + 4 * g4 - blk_lo;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = (uint32_t)(kb + ks * 16 + i) < span;
+        const float p = ok ? fast_exp2(st[ks][i] * scale2 - l2) : 0.f;
+        st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
+      }
+#pragma unroll
+    for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
+      const uint4 sf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
+#pragma unroll
+      for (int j = 0; j < DK / 16; ++j) dqa[j] = Mma<T>::run(dqa[j], knf[kc2][j], sf);
+    }
+    have = have_next;
   }
 
   if (colv) {
