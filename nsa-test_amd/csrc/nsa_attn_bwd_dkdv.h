@@ -6,9 +6,9 @@
 // RC rows, staged in LDS row-major (operand of S = Q K^T and dP = dO V^T) and
 // transposed (operand of dK^T += Q^T dS and dV^T += dO^T P, whose reduction runs over
 // the rows).  The next chunk is loaded into registers while the current one is
-// computed; the single LDS stage keeps the footprint small enough (about 47 KB at
-// dk = 192) for two workgroups per CU.
-// Staging threads own pairs of adjacent rows, so every transposed LDS write stores
+// computed.  bf16 stages only the row-major rows and reads the transposed operands with
+// the LDS transpose load; fp32 stages a transposed copy as well.
+// fp32 staging threads own pairs of adjacent rows, so every transposed LDS write stores
 // two rows at once, and the transposed row pitch (RC + 4) keeps those writes free of
 // bank conflicts.
 //
@@ -72,17 +72,25 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int RPAIRS = RC / 2;
   constexpr int QPC = RPAIRS * (DK / EPF);  // two-row pieces of one Q chunk
   constexpr int OPC = RPAIRS * (DV / EPF);
-  constexpr int NQ = (QPC + 255) / 256;
-  constexpr int NO = (OPC + 255) / 256;
+  // bf16: the transposed operands (Q^T, dO^T) are read from the row-major stage with
+  // the LDS transpose load (ds_read_b64_tr_b16), so only the row-major stage exists and
+  // every staged piece is one 16-byte run of one row (coalesced global reads).
+  // fp32: pairs of rows are staged row-major and transposed.
+  constexpr bool kTr = sizeof(S) == 2;
+  constexpr int QPCS = kTr ? RC * (DK / EPF) : QPC;  // staged pieces per chunk
+  constexpr int OPCS = kTr ? RC * (DV / EPF) : OPC;
+  constexpr int NQ = (QPCS + 255) / 256;
+  constexpr int NO = (OPCS + 255) / 256;
   static_assert(RC % CK == 0, "row chunk");
-  // One LDS stage (two barriers per chunk): the smaller footprint lets two workgroups
-  // share a CU, which hides far more latency than a second stage would.
-  constexpr int NB = 1;
+  // bf16: two LDS stages (one barrier per chunk; about 44 KB at dk = 192, so two
+  // workgroups still share a CU).  fp32 keeps one stage (its transposed copy doubles
+  // the footprint).
+  constexpr int NB = kTr ? 2 : 1;
 
   __shared__ __attribute__((aligned(16))) S Qs[NB][RC * QP];
-  __shared__ __attribute__((aligned(16))) S QTs[NB][DK * RP];
+  __shared__ __attribute__((aligned(16))) S QTs[NB][kTr ? 8 : DK * RP];
   __shared__ __attribute__((aligned(16))) S Os[NB][RC * OP];
-  __shared__ __attribute__((aligned(16))) S OTs[NB][DV * RP];
+  __shared__ __attribute__((aligned(16))) S OTs[NB][kTr ? 8 : DV * RP];
   __shared__ int s_t[NB][RC];
   __shared__ float s_l2[NB][RC];
   __shared__ float s_dl[NB][RC];
@@ -215,21 +223,37 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   // (p = 0) through s_t = -1, so every load is unconditional and the loads of a chunk
   // issue back to back.
   const int sqh = (int)a.sq_h, sqt = (int)a.sq_t, soh = (int)a.sdo_h, sot = (int)a.sdo_t;
-  auto load_rows = [&](int f, const S* base, int sh, int st, int e, uint4& dst) {
+  auto load_row = [&](int f, const S* base, int sh, int st, int e) -> uint4 {
     const int fe = min(f, f_hi - 1);
     const int t = row_t(fe);
     const int h = grp * hpg + hdiv.mod(fe);
-    dst = *reinterpret_cast<const uint4*>(base + e + ((int64_t)h * sh + (int64_t)t * st));
+    return *reinterpret_cast<const uint4*>(base + e + ((int64_t)h * sh + (int64_t)t * st));
   };
+  // the piece index c = tid + 256 j is in range for every thread when the piece count
+  // is a multiple of 256 (known at compile time: no branch)
+  auto in_q = [&](int c) { return QPCS % 256 == 0 || c < QPCS; };
+  auto in_o = [&](int c) { return OPCS % 256 == 0 || c < OPCS; };
   auto load_chunk = [&](int fc) {
+    if constexpr (kTr) {
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const int c = tid + 256 * j;
+        if (in_q(c)) pq[j][0] = load_row(fc + c / (DK / EPF), qbase, sqh, sqt, (c % (DK / EPF)) * EPF);
+      }
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        const int c = tid + 256 * j;
+        if (in_o(c)) po[j][0] = load_row(fc + c / (DV / EPF), obase, soh, sot, (c % (DV / EPF)) * EPF);
+      }
+    } else {
 #pragma unroll
     for (int j = 0; j < NQ; ++j) {
       const int c = tid + 256 * j;
       if (c < QPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
-        load_rows(fc + 2 * rp, qbase, sqh, sqt, e, pq[j][0]);
-        load_rows(fc + 2 * rp + 1, qbase, sqh, sqt, e, pq[j][1]);
+        pq[j][0] = load_row(fc + 2 * rp, qbase, sqh, sqt, e);
+        pq[j][1] = load_row(fc + 2 * rp + 1, qbase, sqh, sqt, e);
       }
     }
 #pragma unroll
@@ -238,9 +262,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
       if (c < OPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
-        load_rows(fc + 2 * rp, obase, soh, sot, e, po[j][0]);
-        load_rows(fc + 2 * rp + 1, obase, soh, sot, e, po[j][1]);
+        po[j][0] = load_row(fc + 2 * rp, obase, soh, sot, e);
+        po[j][1] = load_row(fc + 2 * rp + 1, obase, soh, sot, e);
       }
+    }
     }
     if (tid < RC) {
       const int f = fc + tid;
@@ -257,6 +282,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   // 2k+1 stay adjacent
   auto rowpos = [](int r) -> int { return sizeof(S) == 2 ? cperm_pos32(r) : r; };
   auto store_chunk = [&](int buf) {
+    if constexpr (kTr) {
+#pragma unroll
+      for (int j = 0; j < NQ; ++j) {
+        const int c = tid + 256 * j;
+        if (in_q(c))
+          *reinterpret_cast<uint4*>(&Qs[buf][(c / (DK / EPF)) * QP + (c % (DK / EPF)) * EPF]) = pq[j][0];
+      }
+#pragma unroll
+      for (int j = 0; j < NO; ++j) {
+        const int c = tid + 256 * j;
+        if (in_o(c))
+          *reinterpret_cast<uint4*>(&Os[buf][(c / (DV / EPF)) * OP + (c % (DV / EPF)) * EPF]) = po[j][0];
+      }
+    } else {
 #pragma unroll
     for (int j = 0; j < NQ; ++j) {
       const int c = tid + 256 * j;
@@ -278,6 +317,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
         *reinterpret_cast<uint4*>(&Os[buf][(2 * rp + 1) * OP + e]) = po[j][1];
         PairT<S>::store(&OTs[buf][e * RP + rowpos(2 * rp)], RP, po[j][0], po[j][1]);
       }
+    }
     }
     if (tid < RC) {
       s_t[buf][tid] = pr_t;
@@ -349,12 +389,26 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
       for (int kc2 = 0; kc2 < RC / CK; ++kc2) {
         const uint4 pf = CFrag<T>::pack(pt[kc2 * CT], pt[kc2 * CT + CT - 1]);
         const uint4 sf = CFrag<T>::pack(dst[kc2 * CT], dst[kc2 * CT + CT - 1]);
+        if constexpr (kTr) {
+          // A = dO^T / Q^T (16 features x the 32 rows of the C-permuted CFrag order):
+          // lanes 4*rho+q of group g4 address row kc2*32 + 4*g4 + rho (then +16),
+          // features 4q..4q+3 of the 16-feature tile
+          const int r0 = kc2 * CK + 4 * g4 + (c16 >> 2);
+          const int f4 = 4 * (c16 & 3);
+#pragma unroll
+          for (int j = 0; j < DV / 16; ++j)
+            dva[j] = Mma<T>::run(dva[j], ld_tr_pair(&Os[buf][r0 * OP + j * 16 + f4], 16 * OP), pf);
+#pragma unroll
+          for (int j = 0; j < DK / 16; ++j)
+            dka[j] = Mma<T>::run(dka[j], ld_tr_pair(&Qs[buf][r0 * QP + j * 16 + f4], 16 * QP), sf);
+        } else {
 #pragma unroll
         for (int j = 0; j < DV / 16; ++j)
           dva[j] = Mma<T>::run(dva[j], frag_cperm<T>(&OTs[buf][(j * 16 + c16) * RP + kc2 * CK], g4), pf);
 #pragma unroll
         for (int j = 0; j < DK / 16; ++j)
           dka[j] = Mma<T>::run(dka[j], frag_cperm<T>(&QTs[buf][(j * 16 + c16) * RP + kc2 * CK], g4), sf);
+        }
       }
     }
   }

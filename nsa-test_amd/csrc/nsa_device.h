@@ -119,6 +119,20 @@ template <> __device__ __forceinline__ uint4 frag_cperm<bf16>(const uint16_t* ro
   return *reinterpret_cast<const uint4*>(row + 8 * g);
 }
 
+// LDS transpose load (ds_read_b64_tr_b16): within each 16-lane group, lanes 4*rho..4*rho+3
+// together address row rho (16 consecutive 16-bit elements, 4 per lane) of a 4 x 16
+// block and lane j receives column j: {row0[j], row1[j], row2[j], row3[j]}.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint2 ld_tr16x4(const uint16_t* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+// Two transpose loads, the second `delta` elements further on: one 8-slot bf16 fragment.
+__device__ __forceinline__ uint4 ld_tr_pair(const uint16_t* p, int delta) {
+  const uint2 lo = ld_tr16x4(p), hi = ld_tr16x4(p + delta);
+  return make_uint4(lo.x, lo.y, hi.x, hi.y);
+}
+
 // Fragment-native operand layouts of a [R][C] matrix (R on the time axis, C features;
 // R a multiple of 64, C of 32): every 16-byte MFMA fragment of a 64-lane wave sits at
 // lane * 16 bytes of one contiguous 1 KB tile, so a fragment load is one coalesced
