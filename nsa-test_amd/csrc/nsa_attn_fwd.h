@@ -146,12 +146,35 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     ntiles = s_misc[0] * nsubblk;
   }
 
+  // ---- K rows / V^T columns of a 64-key tile: loaded into registers one tile ahead,
+  // stored to LDS once the previous tile's products are done ----
+  constexpr int NKP = (64 * (DK / EPF) + 255) / 256;
+  constexpr int NVP = (DV * (64 / EPF) + 255) / 256;
+  u32x4 pk[NKP], pv[NVP];
+  int pbe = 0x7fffffff;
+  auto tile_key0 = [&](int it) -> int { return BR == kSliding ? key_lo + it * 64 : it * 64; };
+  auto load_tile = [&](int key0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NKP; ++j) {
+      const int c = min(tid + 256 * j, 64 * (DK / EPF) - 1);
+      pk[j] = *reinterpret_cast<const u32x4*>(kt + (int64_t)(key0 + c / (DK / EPF)) * DK + (c % (DK / EPF)) * EPF);
+    }
+#pragma unroll
+    for (int j = 0; j < NVP; ++j) {
+      const int c = min(tid + 256 * j, DV * (64 / EPF) - 1);
+      pv[j] = *reinterpret_cast<const u32x4*>(vt + (int64_t)(c / (64 / EPF)) * a.Tp + key0 + (c % (64 / EPF)) * EPF);
+    }
+    if (BR == kCompression && tid < 64) {
+      const int key = key0 + tid;
+      pbe = key < a.Tkv ? a.block_ends[key] : 0x7fffffff;
+    }
+  };
+  if (BR != kSelection && ntiles > 0) load_tile(tile_key0(0));
+
   for (int it = 0; it < ntiles; ++it) {
     int key0, blk_lo = 0, blk_hi = 0;
-    if (BR == kSliding) {
-      key0 = key_lo + it * 64;
-    } else if (BR == kCompression) {
-      key0 = it * 64;
+    if (BR == kSliding || BR == kCompression) {
+      key0 = tile_key0(it);
     } else {
       const int blk = s_union[it / nsubblk];
       blk_lo = blk * a.lprime;
@@ -161,23 +184,22 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     }
 
     // ---- stage K rows and V^T columns of keys [key0, key0+64) ----
-    for (int c = tid; c < 64 * (DK / EPF); c += 256) {
-      const int r = c / (DK / EPF);
-      const int e = (c % (DK / EPF)) * EPF;
-      *reinterpret_cast<uint4*>(&Ks[r * KP + e]) =
-          *reinterpret_cast<const uint4*>(kt + (int64_t)(key0 + r) * DK + e);
+    if (BR == kSelection) load_tile(key0);
+#pragma unroll
+    for (int j = 0; j < NKP; ++j) {
+      const int c = tid + 256 * j;
+      if ((64 * (DK / EPF)) % 256 == 0 || c < 64 * (DK / EPF))
+        *reinterpret_cast<u32x4*>(&Ks[(c / (DK / EPF)) * KP + (c % (DK / EPF)) * EPF]) = pk[j];
     }
-    for (int c = tid; c < DV * (64 / EPF); c += 256) {
-      const int r = c / (64 / EPF);
-      const int e = (c % (64 / EPF)) * EPF;
-      *reinterpret_cast<uint4*>(&Vs[r * VP + e]) =
-          *reinterpret_cast<const uint4*>(vt + (int64_t)r * a.Tp + key0 + e);
+#pragma unroll
+    for (int j = 0; j < NVP; ++j) {
+      const int c = tid + 256 * j;
+      if ((DV * (64 / EPF)) % 256 == 0 || c < DV * (64 / EPF))
+        *reinterpret_cast<u32x4*>(&Vs[(c / (64 / EPF)) * VP + (c % (64 / EPF)) * EPF]) = pv[j];
     }
-    if (BR == kCompression && tid < 64) {
-      const int key = key0 + tid;
-      s_be[tid] = key < a.Tkv ? a.block_ends[key] : 0x7fffffff;
-    }
+    if (BR == kCompression && tid < 64) s_be[tid] = pbe;
     __syncthreads();
+    if (BR != kSelection && it + 1 < ntiles) load_tile(tile_key0(it + 1));
 
     int be_min = 0, be_max = 0;
     if (BR == kCompression) {
@@ -211,7 +233,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
         }
         active = __ballot(colsel) != 0ull;
       }
-      if (!active) continue;
+      // Inactive pairs still run fully masked on the sliding / compression paths: a
+      // branch around the products makes the compiler move the accumulators between
+      // register files on every tile.
+      if (BR == kSelection && !active) continue;
 
       f32x4 st[4];
 #pragma unroll
@@ -223,6 +248,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       }
 
       const int t = colt[s];
+      // sliding: the column sees keys [kmin_s, kmin_s + kspan_s) (branch-free test)
+      const int kmin_s = max(t - a.window + 1, 0);
+      const uint32_t kspan_s = colv[s] ? (uint32_t)max(0, min(t, a.Tkv - 1) + 1 - kmin_s) : 0u;
       // interior tiles (every key visible to every column of the subtile) skip masking
       bool all_visible = false;
       if (BR == kSliding)
@@ -246,9 +274,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
             const int key = key0 + ks * 16 + 4 * g4 + i;
             bool ok;
             if (BR == kSliding) {
-              ok = colv[s] && key <= t && key > t - a.window && key < a.Tkv;
+              ok = (uint32_t)(key - kmin_s) < kspan_s;
             } else if (BR == kCompression) {
-              ok = colv[s] && s_be[ks * 16 + 4 * g4 + i] <= t;
+              ok = colv[s] & (s_be[ks * 16 + 4 * g4 + i] <= t);
             } else {
               ok = colsel && (!a.causal || key <= t) && key < blk_hi;
             }
