@@ -19,6 +19,7 @@ namespace nsa {
 // ============================== dQ (query-major) ===============================
 template <typename T, int DK, int DV, int BR>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
+  static_assert(BR == kSliding || BR == kCompression, "selection uses attn_sel_dq_kernel");
   using S = typename Store<T>::type;
   constexpr int EPF = Elem<T>::kPerFrag;
   constexpr int KC = Elem<T>::kKChunk;
@@ -29,16 +30,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   constexpr int VP = DV + EPF;
   constexpr int CK = CFrag<T>::kKeys;
   constexpr int CT = CK / 16;
+  // bf16 reads the K^T operand from the K rows with the LDS transpose load; fp32 stages
+  // a K^T copy from the kn layout
+  constexpr bool kTr = sizeof(S) == 2;
   static_assert(DK % KC == 0 && DV % KC == 0, "head dims");
 
-  __shared__ __attribute__((aligned(16))) S Ks[64 * KP];   // K rows   [key][d]
-  __shared__ __attribute__((aligned(16))) S KnS[DK * NP];  // K^T      [d][key]
-  __shared__ __attribute__((aligned(16))) S Vns[64 * VP];  // V rows   [key][dv]
+  __shared__ __attribute__((aligned(16))) S Ks[64 * KP];                 // K rows   [key][d]
+  __shared__ __attribute__((aligned(16))) S KnS[kTr ? 8 : DK * NP];      // K^T      [d][key]
+  __shared__ __attribute__((aligned(16))) S Vns[64 * VP];                // V rows   [key][dv]
   __shared__ int s_be[64];
   __shared__ int s_misc[4];
-  __shared__ int s_list[BR == kSelection ? kSelListMax : 1];
-  __shared__ int s_union[BR == kSelection ? kSelMaxBlocks : 1];
-  __shared__ uint32_t s_bits[BR == kSelection ? kSelMaxBlocks / 32 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -82,17 +83,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   const int64_t srow = ((int64_t)b * a.H + colh) * a.Tq + colt;
   const float l2 = colv ? a.lse2[srow] : INFINITY;
   const float dl = colv ? a.delta[srow] : 0.f;
+  // sliding: the column sees keys [kmin_s, kmin_s + kspan_s) (branch-free test)
+  const int kmin_s = max(colt - a.window + 1, 0);
+  const uint32_t kspan_s = colv ? (uint32_t)max(0, min(colt, a.Tkv - 1) + 1 - kmin_s) : 0u;
 
   f32x4 dqa[DK / 16];
 #pragma unroll
   for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
 
-  int ntiles = 0, key_lo = 0, nsubblk = 1;
+  int ntiles = 0, key_lo = 0;
   if (BR == kSliding) {
     key_lo = max(0, t_first - a.window + 1) & ~31;  // 32-key aligned (C-permuted K^T chunks)
     const int hi = min(t_last, a.Tkv - 1);
     ntiles = hi >= key_lo ? (hi - key_lo) / 64 + 1 : 0;
-  } else if (BR == kCompression) {
+  } else {
     if (tid == 0) s_misc[0] = 0;
     __syncthreads();
     int mx = 0;
@@ -101,141 +105,123 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     if (mx) atomicMax(&s_misc[0], mx);
     __syncthreads();
     ntiles = (s_misc[0] + 63) / 64;
-  } else {
-    const int nt = t_last - t_first + 1;
-    const int total = nt * a.nslots;
-    const int nwords = (a.nblk + 31) / 32;
-    for (int i = tid; i < nwords; i += 256) s_bits[i] = 0;
-    __syncthreads();
-    const int* selrow = a.sel + ((int64_t)bg * a.Tq + t_first) * a.nslots;
-    for (int i = tid; i < total; i += 256) {
-      const int v = selrow[i];
-      s_list[i] = v;
-      if (v >= 0) atomicOr(&s_bits[v >> 5], 1u << (v & 31));
-    }
-    __syncthreads();
-    if (tid == 0) {
-      int n = 0;
-      for (int w = 0; w < nwords; ++w) {
-        uint32_t bits = s_bits[w];
-        while (bits) {
-          const int bit = __builtin_ctz(bits);
-          bits &= bits - 1;
-          s_union[n++] = w * 32 + bit;
-        }
-      }
-      s_misc[0] = n;
-    }
-    __syncthreads();
-    nsubblk = (a.lprime + 63) / 64;
-    ntiles = s_misc[0] * nsubblk;
   }
 
-  for (int it = 0; it < ntiles; ++it) {
-    int key0, blk_lo = 0, blk_hi = 0;
-    if (BR == kSliding) {
-      key0 = key_lo + it * 64;
-    } else if (BR == kCompression) {
-      key0 = it * 64;
-    } else {
-      const int blk = s_union[it / nsubblk];
-      blk_lo = blk * a.lprime;
-      blk_hi = min(blk_lo + a.lprime, a.Tkv);
-      key0 = blk_lo + (it % nsubblk) * 64;
-      if ((a.causal && key0 > t_last) || key0 >= blk_hi) continue;
+  // ---- tile operands, loaded into registers one tile ahead ----
+  constexpr int NKP = (64 * (DK / EPF) + 255) / 256;
+  constexpr int NNP = kTr ? 1 : (DK * (64 / EPF) + 255) / 256;
+  constexpr int NVP = (64 * (DV / EPF) + 255) / 256;
+  u32x4 pk[NKP], pn[NNP], pv[NVP];
+  int pbe = 0x7fffffff;
+  auto tile_key0 = [&](int it) -> int { return BR == kSliding ? key_lo + it * 64 : it * 64; };
+  auto load_tile = [&](int key0) {
+#pragma unroll
+    for (int j = 0; j < NKP; ++j) {
+      const int c = min(tid + 256 * j, 64 * (DK / EPF) - 1);
+      pk[j] = *reinterpret_cast<const u32x4*>(kt + (int64_t)(key0 + c / (DK / EPF)) * DK + (c % (DK / EPF)) * EPF);
     }
-    for (int c = tid; c < 64 * (DK / EPF); c += 256) {
-      const int r = c / (DK / EPF);
-      const int e = (c % (DK / EPF)) * EPF;
-      *reinterpret_cast<uint4*>(&Ks[r * KP + e]) = *reinterpret_cast<const uint4*>(kt + (int64_t)(key0 + r) * DK + e);
+    if constexpr (!kTr) {
+#pragma unroll
+      for (int j = 0; j < NNP; ++j) {
+        const int c = min(tid + 256 * j, DK * (64 / EPF) - 1);
+        pn[j] = *reinterpret_cast<const u32x4*>(kn + (int64_t)(c / (64 / EPF)) * a.Tp + key0 + (c % (64 / EPF)) * EPF);
+      }
     }
-    for (int c = tid; c < DK * (64 / EPF); c += 256) {
-      const int r = c / (64 / EPF);
-      const int e = (c % (64 / EPF)) * EPF;
-      *reinterpret_cast<uint4*>(&KnS[r * NP + e]) = *reinterpret_cast<const uint4*>(kn + (int64_t)r * a.Tp + key0 + e);
-    }
-    for (int c = tid; c < 64 * (DV / EPF); c += 256) {
-      const int r = c / (DV / EPF);
-      const int e = (c % (DV / EPF)) * EPF;
-      *reinterpret_cast<uint4*>(&Vns[r * VP + e]) = *reinterpret_cast<const uint4*>(vn + (int64_t)(key0 + r) * DV + e);
+#pragma unroll
+    for (int j = 0; j < NVP; ++j) {
+      const int c = min(tid + 256 * j, 64 * (DV / EPF) - 1);
+      pv[j] = *reinterpret_cast<const u32x4*>(vn + (int64_t)(key0 + c / (DV / EPF)) * DV + (c % (DV / EPF)) * EPF);
     }
     if (BR == kCompression && tid < 64) {
       const int key = key0 + tid;
-      s_be[tid] = key < a.Tkv ? a.block_ends[key] : 0x7fffffff;
+      pbe = key < a.Tkv ? a.block_ends[key] : 0x7fffffff;
     }
+  };
+  if (ntiles > 0) load_tile(tile_key0(0));
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int key0 = tile_key0(it);
+#pragma unroll
+    for (int j = 0; j < NKP; ++j) {
+      const int c = tid + 256 * j;
+      if ((64 * (DK / EPF)) % 256 == 0 || c < 64 * (DK / EPF))
+        *reinterpret_cast<u32x4*>(&Ks[(c / (DK / EPF)) * KP + (c % (DK / EPF)) * EPF]) = pk[j];
+    }
+    if constexpr (!kTr) {
+#pragma unroll
+      for (int j = 0; j < NNP; ++j) {
+        const int c = tid + 256 * j;
+        if ((DK * (64 / EPF)) % 256 == 0 || c < DK * (64 / EPF))
+          *reinterpret_cast<u32x4*>(&KnS[(c / (64 / EPF)) * NP + (c % (64 / EPF)) * EPF]) = pn[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NVP; ++j) {
+      const int c = tid + 256 * j;
+      if ((64 * (DV / EPF)) % 256 == 0 || c < 64 * (DV / EPF))
+        *reinterpret_cast<u32x4*>(&Vns[(c / (DV / EPF)) * VP + (c % (DV / EPF)) * EPF]) = pv[j];
+    }
+    if (BR == kCompression && tid < 64) s_be[tid] = pbe;
     __syncthreads();
+    if (it + 1 < ntiles) load_tile(tile_key0(it + 1));
 
-    bool active;
-    bool colsel = false;
     int be_max = 0;
-    if (BR == kSliding) {
-      active = sub_t1 >= 0 && key0 <= sub_t1 && key0 + 63 > sub_t0 - a.window;
-    } else if (BR == kCompression) {
-      int be_min = s_be[lane];
-      be_max = be_min;
+    if (BR == kCompression) {
+      be_max = s_be[lane];
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        be_min = min(be_min, __shfl_xor(be_min, o));
-        be_max = max(be_max, __shfl_xor(be_max, o));
-      }
-      active = sub_t1 >= 0 && be_min <= sub_t1;
-    } else {
-      if (colv && (!a.causal || key0 <= colt)) {
-        const int* lst = &s_list[(colt - t_first) * a.nslots];
-        const int blk = blk_lo / a.lprime;
-        for (int j = 0; j < a.nslots; ++j) {
-          const int v = lst[j];
-          if (v == blk) colsel = true;
-          if (v < 0 || v >= blk) break;
-        }
-      }
-      active = __ballot(colsel) != 0ull;
+      for (int o = 1; o < 64; o <<= 1) be_max = max(be_max, __shfl_xor(be_max, o));
     }
 
-    if (active) {
-      f32x4 st[4], dp[4];
+    // Every (subtile, tile) pair runs the products, fully masked when no key is
+    // visible: a branch around them would make the compiler move the accumulators
+    // between register files on every tile.
+    f32x4 st[4], dp[4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        st[ks] = zero4();
-        dp[ks] = zero4();
-        const S* krow = &Ks[(ks * 16 + c16) * KP];
-        const S* vrow = &Vns[(ks * 16 + c16) * VP];
+    for (int ks = 0; ks < 4; ++ks) {
+      st[ks] = zero4();
+      dp[ks] = zero4();
+      const S* krow = &Ks[(ks * 16 + c16) * KP];
+      const S* vrow = &Vns[(ks * 16 + c16) * VP];
 #pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) st[ks] = Mma<T>::run(st[ks], frag_std<T>(krow + kc * KC, g4), qf[kc]);
+      for (int kc = 0; kc < NKC; ++kc) st[ks] = Mma<T>::run(st[ks], frag_std<T>(krow + kc * KC, g4), qf[kc]);
 #pragma unroll
-        for (int kc = 0; kc < NVC; ++kc) dp[ks] = Mma<T>::run(dp[ks], frag_std<T>(vrow + kc * KC, g4), dof[kc]);
-      }
-      bool all_visible = false;
-      const bool full = f0 + 16 <= ncols;
-      if (BR == kSliding)
-        all_visible = full && key0 + 63 <= sub_t0 && key0 > sub_t1 - a.window && key0 + 63 < a.Tkv;
-      else if (BR == kCompression)
-        all_visible = full && be_max <= sub_t0;
+      for (int kc = 0; kc < NVC; ++kc) dp[ks] = Mma<T>::run(dp[ks], frag_std<T>(vrow + kc * KC, g4), dof[kc]);
+    }
+    bool all_visible = false;
+    const bool full = f0 + 16 <= ncols;
+    if (BR == kSliding)
+      all_visible = full && key0 + 63 <= sub_t0 && key0 > sub_t1 - a.window && key0 + 63 < a.Tkv;
+    else
+      all_visible = full && be_max <= sub_t0;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float p;
-          if (all_visible) {
-            p = fast_exp2(st[ks][i] * scale2 - l2);
-          } else {
-            const int key = key0 + ks * 16 + 4 * g4 + i;
-            bool ok;
-            if (BR == kSliding) {
-              ok = colv && key <= colt && key > colt - a.window && key < a.Tkv;
-            } else if (BR == kCompression) {
-              ok = colv && s_be[ks * 16 + 4 * g4 + i] <= colt;
-            } else {
-              ok = colsel && (!a.causal || key <= colt) && key < blk_hi;
-            }
-            p = ok ? fast_exp2(st[ks][i] * scale2 - l2) : 0.f;
-          }
-          st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
+      for (int i = 0; i < 4; ++i) {
+        float p;
+        if (all_visible) {
+          p = fast_exp2(st[ks][i] * scale2 - l2);
+        } else {
+          const int key = key0 + ks * 16 + 4 * g4 + i;
+          bool ok;
+          if (BR == kSliding) ok = (uint32_t)(key - kmin_s) < kspan_s;
+          else ok = colv & (s_be[ks * 16 + 4 * g4 + i] <= colt);
+          p = ok ? fast_exp2(st[ks][i] * scale2 - l2) : 0.f;
         }
+        st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
       }
+    }
 #pragma unroll
-      for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
-        const uint4 sf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
+    for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
+      const uint4 sf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
+      if constexpr (kTr) {
+        // A = K^T (16 features x the 32 keys of the C-permuted CFrag order) from the
+        // K rows: lanes 4*rho+q of group g4 address key kc2*32 + 4*g4 + rho (then +16)
+        const int r0 = kc2 * CK + 4 * g4 + (c16 >> 2);
+        const int f4 = 4 * (c16 & 3);
+#pragma unroll
+        for (int j = 0; j < DK / 16; ++j)
+          dqa[j] = Mma<T>::run(dqa[j], ld_tr_pair(&Ks[r0 * KP + j * 16 + f4], 16 * KP), sf);
+      } else {
 #pragma unroll
         for (int j = 0; j < DK / 16; ++j) {
           const uint4 kf = frag_cperm<T>(&KnS[(j * 16 + c16) * NP + kc2 * CK], g4);
