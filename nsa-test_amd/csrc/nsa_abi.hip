@@ -127,9 +127,6 @@ int validate(const Shape& s) {
   if (s.br == kSelection) {
     if (s.lprime <= 0 || s.lprime % 16) return fail(NSA_ERR_INVALID, "block_size_selection=%d must be a positive multiple of 16", s.lprime);
     if (s.nslots < 0 || s.nslots > 64) return fail(NSA_ERR_INVALID, "n_slots=%d outside [0, 64]", s.nslots);
-    const int nt = kFwdCols / s.hpg() + 2;
-    if ((int64_t)nt * s.nslots > kSelListMax)
-      return fail(NSA_ERR_UNSUPPORTED, "n_slots=%d too large for %d heads per group", s.nslots, s.hpg());
     if (s.nblk() > kSelMaxBlocks) return fail(NSA_ERR_UNSUPPORTED, "%d selection blocks exceed %d", s.nblk(), kSelMaxBlocks);
   }
   return NSA_OK;

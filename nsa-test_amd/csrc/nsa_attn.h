@@ -13,8 +13,7 @@ constexpr int kFwdNSub = 2;
 constexpr int kFwdCols = 4 * kFwdNSub * 16;
 constexpr int kDqNSub = 1;
 constexpr int kDqCols = 4 * kDqNSub * 16;
-// Per-workgroup selection bookkeeping limits (timesteps x slots, distinct blocks).
-constexpr int kSelListMax = 2048;
+// Distinct selection blocks a row's union bitmap can hold.
 constexpr int kSelMaxBlocks = 4096;
 // Query rows staged per step of the dK/dV kernels.
 constexpr int kRowChunk = 32;

@@ -27,6 +27,7 @@ namespace nsa {
 
 template <typename T, int DK, int DV, int BR>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
+  static_assert(BR == kSliding || BR == kCompression, "selection uses attn_sel_fwd_kernel");
   using S = typename Store<T>::type;
   constexpr int EPF = Elem<T>::kPerFrag;
   constexpr int KC = Elem<T>::kKChunk;
@@ -42,9 +43,6 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) S Vs[DV * VP];
   __shared__ int s_be[64];
   __shared__ int s_misc[4];
-  __shared__ int s_list[BR == kSelection ? kSelListMax : 1];
-  __shared__ int s_union[BR == kSelection ? kSelMaxBlocks : 1];
-  __shared__ uint32_t s_bits[BR == kSelection ? kSelMaxBlocks / 32 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -101,12 +99,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
   // ---- tile list ---------------------------------------------------------------
   int ntiles = 0;
   int key_lo = 0;
-  int nsubblk = 1;
   if (BR == kSliding) {
     key_lo = max(0, t_first - a.window + 1) & ~31;  // 32-key aligned (C-permuted V^T chunks)
     const int hi = min(t_last, a.Tkv - 1);
     ntiles = hi >= key_lo ? (hi - key_lo) / 64 + 1 : 0;
-  } else if (BR == kCompression) {
+  } else {
     if (tid == 0) s_misc[0] = 0;
     __syncthreads();
     int mx = 0;
@@ -115,35 +112,6 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     if (mx) atomicMax(&s_misc[0], mx);
     __syncthreads();
     ntiles = (s_misc[0] + 63) / 64;
-  } else {
-    // union of the selected blocks of this workgroup's timesteps (ascending)
-    const int nt = t_last - t_first + 1;
-    const int total = nt * a.nslots;
-    const int nwords = (a.nblk + 31) / 32;
-    for (int i = tid; i < nwords; i += 256) s_bits[i] = 0;
-    __syncthreads();
-    const int* selrow = a.sel + ((int64_t)bg * a.Tq + t_first) * a.nslots;
-    for (int i = tid; i < total; i += 256) {
-      const int v = selrow[i];
-      s_list[i] = v;
-      if (v >= 0) atomicOr(&s_bits[v >> 5], 1u << (v & 31));
-    }
-    __syncthreads();
-    if (tid == 0) {
-      int n = 0;
-      for (int w = 0; w < nwords; ++w) {
-        uint32_t bits = s_bits[w];
-        while (bits) {
-          const int bit = __builtin_ctz(bits);
-          bits &= bits - 1;
-          s_union[n++] = w * 32 + bit;
-        }
-      }
-      s_misc[0] = n;
-    }
-    __syncthreads();
-    nsubblk = (a.lprime + 63) / 64;
-    ntiles = s_misc[0] * nsubblk;
   }
 
   // ---- K rows / V^T columns of a 64-key tile: loaded into registers one tile ahead,
@@ -169,22 +137,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       pbe = key < a.Tkv ? a.block_ends[key] : 0x7fffffff;
     }
   };
-  if (BR != kSelection && ntiles > 0) load_tile(tile_key0(0));
+  if (ntiles > 0) load_tile(tile_key0(0));
 
   for (int it = 0; it < ntiles; ++it) {
-    int key0, blk_lo = 0, blk_hi = 0;
-    if (BR == kSliding || BR == kCompression) {
-      key0 = tile_key0(it);
-    } else {
-      const int blk = s_union[it / nsubblk];
-      blk_lo = blk * a.lprime;
-      blk_hi = min(blk_lo + a.lprime, a.Tkv);
-      key0 = blk_lo + (it % nsubblk) * 64;
-      if ((a.causal && key0 > t_last) || key0 >= blk_hi) continue;  // uniform across the workgroup
-    }
-
+    const int key0 = tile_key0(it);
     // ---- stage K rows and V^T columns of keys [key0, key0+64) ----
-    if (BR == kSelection) load_tile(key0);
 #pragma unroll
     for (int j = 0; j < NKP; ++j) {
       const int c = tid + 256 * j;
@@ -199,45 +156,17 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     }
     if (BR == kCompression && tid < 64) s_be[tid] = pbe;
     __syncthreads();
-    if (BR != kSelection && it + 1 < ntiles) load_tile(tile_key0(it + 1));
+    if (it + 1 < ntiles) load_tile(tile_key0(it + 1));
 
-    int be_min = 0, be_max = 0;
+    int be_max = 0;
     if (BR == kCompression) {
-      be_min = s_be[lane];
-      be_max = be_min;
+      be_max = s_be[lane];
 #pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        be_min = min(be_min, __shfl_xor(be_min, o));
-        be_max = max(be_max, __shfl_xor(be_max, o));
-      }
+      for (int o = 1; o < 64; o <<= 1) be_max = max(be_max, __shfl_xor(be_max, o));
     }
 
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
-      // wave-uniform skip of (subtile x tile) pairs with no visible key
-      bool active;
-      bool colsel = false;
-      if (BR == kSliding) {
-        active = sub_t1[s] >= 0 && key0 <= sub_t1[s] && key0 + 63 > sub_t0[s] - a.window;
-      } else if (BR == kCompression) {
-        active = sub_t1[s] >= 0 && be_min <= sub_t1[s];
-      } else {
-        if (colv[s] && (!a.causal || key0 <= colt[s])) {
-          const int* lst = &s_list[(colt[s] - t_first) * a.nslots];
-          const int blk = blk_lo / a.lprime;
-          for (int j = 0; j < a.nslots; ++j) {
-            const int v = lst[j];
-            if (v == blk) colsel = true;
-            if (v < 0 || v >= blk) break;
-          }
-        }
-        active = __ballot(colsel) != 0ull;
-      }
-      // Inactive pairs still run fully masked on the sliding / compression paths: a
-      // branch around the products makes the compiler move the accumulators between
-      // register files on every tile.
-      if (BR == kSelection && !active) continue;
-
       f32x4 st[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
@@ -273,13 +202,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
           for (int i = 0; i < 4; ++i) {
             const int key = key0 + ks * 16 + 4 * g4 + i;
             bool ok;
-            if (BR == kSliding) {
-              ok = (uint32_t)(key - kmin_s) < kspan_s;
-            } else if (BR == kCompression) {
-              ok = colv[s] & (s_be[ks * 16 + 4 * g4 + i] <= t);
-            } else {
-              ok = colsel && (!a.causal || key <= t) && key < blk_hi;
-            }
+            if (BR == kSliding) ok = (uint32_t)(key - kmin_s) < kspan_s;
+            else ok = colv[s] & (s_be[ks * 16 + 4 * g4 + i] <= t);
             const float v = ok ? st[ks][i] * scale2 : -INFINITY;
             st[ks][i] = v;
             mx = fmaxf(mx, v);

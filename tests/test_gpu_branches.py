@@ -65,6 +65,7 @@ SLIDING_CASES = [
     (1, 4, 2, 77, 128, 128, 1, torch.float32),    # window 1: out = v_t
     (1, 8, 2, 700, 128, 128, 512, torch.bfloat16),
     (1, 6, 3, 96, 48, 48, 40, torch.float32),     # head dims zero-padded to a compiled pair
+    (1, 6, 2, 333, 64, 64, 70, torch.bfloat16),   # 3 heads per group (not a power of two)
 ]
 
 
@@ -92,6 +93,7 @@ COMPRESSION_CASES = [
     (1, 16, 1, 1100, 192, 128, 32, 16, torch.bfloat16),
     (1, 4, 2, 20, 64, 64, 32, 16, torch.float32),  # no row sees a block: all zero, L = -inf
     (1, 4, 1, 5000, 128, 128, 32, 16, torch.bfloat16),
+    (1, 6, 2, 400, 64, 64, 32, 16, torch.bfloat16),  # 3 heads per group
 ]
 
 
@@ -124,6 +126,8 @@ SELECTION_CASES = [
     (1, 4, 1, 300, 64, 64, 128, 3, torch.float32),  # selection blocks larger than a tile
     (4, 16, 4, 256, 64, 64, 64, 16, torch.float32),  # n larger than the number of blocks
     (1, 32, 2, 1024, 128, 128, 64, 16, torch.bfloat16),
+    (1, 2, 2, 400, 64, 64, 32, 16, torch.bfloat16),  # one head per group, 16 slots
+    (1, 6, 2, 333, 64, 64, 48, 5, torch.float32),    # 3 heads per group, blocks straddling 32-key chunks
 ]
 
 
