@@ -89,7 +89,7 @@ def make_workload(name, dev, seed=0):
 def nsa_step(cfg, mod, w, backward=True):
     """One NSA forward (+ backward): every kernel of the hot path runs once."""
     import torch
-    from nsa import CompressionAttention, SelectionAttention, SlidingWindowAttention, score_and_select
+    from nsa import CompressionAttention, GatedMix, SelectionAttention, SlidingWindowAttention, score_and_select
 
     scale = 1.0 / math.sqrt(cfg.head_dim_qk)
     q = w["q"]
@@ -100,7 +100,7 @@ def nsa_step(cfg, mod, w, backward=True):
     o_s = SelectionAttention.apply(q, w["k_sel"].transpose(-1, -2), w["v_sel"], idx, scale, cfg)
     o_w = SlidingWindowAttention.apply(q, w["k_win"].transpose(-1, -2), w["v_win"], scale, cfg.w, cfg)
     gt = torch.sigmoid(w["gate_logits"])
-    o = o_c * gt[..., 0:1] + o_s * gt[..., 1:2] + o_w * gt[..., 2:3]
+    o = GatedMix.apply(o_c, o_s, o_w, gt)
     if backward:
         o.backward(w["dO"])
         for t in list(w.values()) + list(mod.parameters()):

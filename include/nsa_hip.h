@@ -184,6 +184,23 @@ int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* Block_ends, 
                    int head_dim_qk, int n_blocks, int l, int d, int l_prime, int n, int include_fixed, int n_fixed,
                    int dtype, float scale, void* workspace, size_t workspace_bytes, nsa_stream_t stream);
 
+/* ---- gated mix of the three branches (NSAAttention.forward, nsa/kernels.py:2446-2463) --
+ * No entry point of its own in the reference (torch elementwise ops there); fused here.
+ * Forward: out[b,h,t,:] = g0 o_cmp + g1 o_sel + g2 o_win, summed in fp32 and rounded once
+ * (the reference's eval path sums in float64 and rounds once).  o_* share the strides
+ * so_*, gates [B,H,T,3] any strides, out any strides; every row unit-stride and 16-byte
+ * aligned.  Backward: do_k = g_k dout (contiguous [B,H,T,dv]) and dgates[b,h,t,k] =
+ * sum_d dout . o_k (contiguous fp32 [B,H,T,3]). */
+int nsa_gate_mix_fwd(const void* o_cmp, const void* o_sel, const void* o_win, int64_t so_b, int64_t so_h,
+                     int64_t so_t, const void* gates, int64_t sg_b, int64_t sg_h, int64_t sg_t, int64_t sg_k,
+                     void* out, int64_t sout_b, int64_t sout_h, int64_t sout_t, int B, int H, int T, int dv,
+                     int dtype, nsa_stream_t stream);
+int nsa_gate_mix_bwd(const void* dout, int64_t sd_b, int64_t sd_h, int64_t sd_t, const void* o_cmp,
+                     const void* o_sel, const void* o_win, int64_t so_b, int64_t so_h, int64_t so_t,
+                     const void* gates, int64_t sg_b, int64_t sg_h, int64_t sg_t, int64_t sg_k, void* do_cmp,
+                     void* do_sel, void* do_win, float* dgates, int B, int H, int T, int dv, int dtype,
+                     nsa_stream_t stream);
+
 /* ---- compression pooling (compress_tokens, nsa/kernels.py:2119-2208) --------
  * With the first MLP layer split as W1 = [W1k | W1p]:  Y = k W1k^T  [Z,G,T,width],
  * C = E W1p^T + b1  [l,width].  Forward writes R[i] = mean_{u<l} relu(Y[d*i+u] + C[u])

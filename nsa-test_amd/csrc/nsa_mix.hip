@@ -1,0 +1,219 @@
+// Gated mix of the three branch outputs (reference nsa/kernels.py NSAAttention.forward:
+// o = o_cmp * g[...,0] + o_sel * g[...,1] + o_win * g[...,2]) and its backward, fused:
+// one pass over the outputs instead of a chain of broadcast elementwise kernels.
+//   forward : out = sum_k g_k o_k                         (fp32 sum, rounded once)
+//   backward: dO_k = g_k dout,  dg_k = sum_d dout . o_k   (fp32)
+// Rows are (b, h, t); LPR lanes share a row and read 16-byte pieces of it.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/nsa_hip.h"
+#include "nsa_device.h"
+#include "nsa_kernels.h"
+
+namespace nsa {
+
+struct MixArgs {
+  const void* o[3];
+  int64_t so_b, so_h, so_t;
+  const void* g;
+  int64_t sg_b, sg_h, sg_t, sg_k;
+  void* out;  // forward output, or backward dout (read)
+  int64_t sx_b, sx_h, sx_t;
+  void* dO[3];  // backward: contiguous [B,H,T,dv]
+  float* dg;    // backward: contiguous [B,H,T,3]
+  int B, H, T, dv;
+};
+
+template <typename S>
+__device__ __forceinline__ float ld1(const S* p);
+template <> __device__ __forceinline__ float ld1<float>(const float* p) { return *p; }
+template <> __device__ __forceinline__ float ld1<uint16_t>(const uint16_t* p) { return bf16_bits_to_f32(*p); }
+
+template <typename S>
+__device__ __forceinline__ void unpack_piece(const uint4& v, float* f) {
+  if constexpr (sizeof(S) == 4) {
+    f[0] = __uint_as_float(v.x);
+    f[1] = __uint_as_float(v.y);
+    f[2] = __uint_as_float(v.z);
+    f[3] = __uint_as_float(v.w);
+  } else {
+    const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      f[2 * u] = __uint_as_float(w[u] << 16);
+      f[2 * u + 1] = __uint_as_float(w[u] & 0xffff0000u);
+    }
+  }
+}
+template <typename S>
+__device__ __forceinline__ uint4 pack_piece(const float* f) {
+  if constexpr (sizeof(S) == 4) {
+    return make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
+  } else {
+    return make_uint4(pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                      pack_bf16x2(f[6], f[7]));
+  }
+}
+
+template <typename S, bool BWD>
+__global__ __launch_bounds__(256) void gate_mix_kernel(MixArgs a, int lpr_log2) {
+  constexpr int EPF = 16 / sizeof(S);
+  const int lpr = 1 << lpr_log2;
+  const int sub = threadIdx.x & (lpr - 1);
+  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> lpr_log2;
+  const int64_t nrows = (int64_t)a.B * a.H * a.T;
+  const bool valid = row < nrows;
+  const int64_t rr = valid ? row : nrows - 1;
+  const int t = rr % a.T;
+  const int h = (rr / a.T) % a.H;
+  const int b = rr / ((int64_t)a.T * a.H);
+  const int64_t ooff = b * a.so_b + h * a.so_h + (int64_t)t * a.so_t;
+  const int64_t xoff = b * a.sx_b + h * a.sx_h + (int64_t)t * a.sx_t;
+  const S* gp = reinterpret_cast<const S*>(a.g) + b * a.sg_b + h * a.sg_h + (int64_t)t * a.sg_t;
+  const float g0 = ld1<S>(gp), g1 = ld1<S>(gp + a.sg_k), g2 = ld1<S>(gp + 2 * a.sg_k);
+  float dg0 = 0.f, dg1 = 0.f, dg2 = 0.f;
+  for (int e = sub * EPF; e < a.dv; e += lpr * EPF) {
+    float o0[EPF], o1[EPF], o2[EPF];
+    unpack_piece<S>(*reinterpret_cast<const uint4*>(reinterpret_cast<const S*>(a.o[0]) + ooff + e), o0);
+    unpack_piece<S>(*reinterpret_cast<const uint4*>(reinterpret_cast<const S*>(a.o[1]) + ooff + e), o1);
+    unpack_piece<S>(*reinterpret_cast<const uint4*>(reinterpret_cast<const S*>(a.o[2]) + ooff + e), o2);
+    if constexpr (!BWD) {
+      float r[EPF];
+#pragma unroll
+      for (int u = 0; u < EPF; ++u) r[u] = g0 * o0[u] + g1 * o1[u] + g2 * o2[u];
+      if (valid) *reinterpret_cast<uint4*>(reinterpret_cast<S*>(a.out) + xoff + e) = pack_piece<S>(r);
+    } else {
+      float x[EPF], d0[EPF], d1[EPF], d2[EPF];
+      unpack_piece<S>(*reinterpret_cast<const uint4*>(reinterpret_cast<const S*>(a.out) + xoff + e), x);
+#pragma unroll
+      for (int u = 0; u < EPF; ++u) {
+        d0[u] = g0 * x[u];
+        d1[u] = g1 * x[u];
+        d2[u] = g2 * x[u];
+        dg0 += x[u] * o0[u];
+        dg1 += x[u] * o1[u];
+        dg2 += x[u] * o2[u];
+      }
+      if (valid) {
+        const int64_t coff = rr * a.dv + e;
+        *reinterpret_cast<uint4*>(reinterpret_cast<S*>(a.dO[0]) + coff) = pack_piece<S>(d0);
+        *reinterpret_cast<uint4*>(reinterpret_cast<S*>(a.dO[1]) + coff) = pack_piece<S>(d1);
+        *reinterpret_cast<uint4*>(reinterpret_cast<S*>(a.dO[2]) + coff) = pack_piece<S>(d2);
+      }
+    }
+  }
+  if constexpr (BWD) {
+    for (int off = lpr >> 1; off > 0; off >>= 1) {
+      dg0 += __shfl_xor(dg0, off);
+      dg1 += __shfl_xor(dg1, off);
+      dg2 += __shfl_xor(dg2, off);
+    }
+    if (valid && sub == 0) {
+      a.dg[rr * 3 + 0] = dg0;
+      a.dg[rr * 3 + 1] = dg1;
+      a.dg[rr * 3 + 2] = dg2;
+    }
+  }
+}
+
+template <bool BWD>
+static int launch_mix(int dtype, const MixArgs& a, hipStream_t st) {
+  const int64_t nrows = (int64_t)a.B * a.H * a.T;
+  if (nrows == 0) return NSA_OK;
+  const int pieces = a.dv / (dtype == NSA_F32 ? 4 : 8);
+  int lg = 0;
+  while ((1 << lg) < pieces && lg < 6) ++lg;
+  const int64_t rows_per_wg = 256 >> lg;
+  dim3 grid((unsigned)((nrows + rows_per_wg - 1) / rows_per_wg));
+  if (dtype == NSA_F32)
+    hipLaunchKernelGGL((gate_mix_kernel<float, BWD>), grid, dim3(256), 0, st, a, lg);
+  else
+    hipLaunchKernelGGL((gate_mix_kernel<uint16_t, BWD>), grid, dim3(256), 0, st, a, lg);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NSA_OK : set_error(NSA_ERR_HIP, hipGetErrorString(e));
+}
+
+static int check_mix(int dtype, int B, int H, int T, int dv, const void* const* ptrs, int n) {
+  if (dtype != NSA_F32 && dtype != NSA_BF16) return set_error(NSA_ERR_INVALID, "dtype not supported");
+  if (B < 0 || H < 0 || T < 0 || dv <= 0) return set_error(NSA_ERR_INVALID, "bad shape");
+  const int epf = dtype == NSA_F32 ? 4 : 8;
+  if (dv % epf) return set_error(NSA_ERR_LAYOUT, "head_dim_v must fill 16-byte pieces");
+  for (int i = 0; i < n; ++i)
+    if (((uintptr_t)ptrs[i]) % 16) return set_error(NSA_ERR_LAYOUT, "branch outputs need 16-byte aligned rows");
+  return NSA_OK;
+}
+
+}  // namespace nsa
+
+extern "C" int nsa_gate_mix_fwd(const void* o_cmp, const void* o_sel, const void* o_win, int64_t so_b, int64_t so_h,
+                                int64_t so_t, const void* gates, int64_t sg_b, int64_t sg_h, int64_t sg_t,
+                                int64_t sg_k, void* out, int64_t sout_b, int64_t sout_h, int64_t sout_t, int B, int H,
+                                int T, int dv, int dtype, nsa_stream_t stream) {
+  using namespace nsa;
+  const void* ptrs[4] = {o_cmp, o_sel, o_win, out};
+  if (int rc = check_mix(dtype, B, H, T, dv, ptrs, 4)) return rc;
+  const int esz = dtype == NSA_F32 ? 4 : 2;
+  if ((so_t * esz) % 16 || (so_h * esz) % 16 || (sout_t * esz) % 16 || (sout_h * esz) % 16)
+    return set_error(NSA_ERR_LAYOUT, "rows must be 16-byte aligned");
+  MixArgs a{};
+  a.o[0] = o_cmp;
+  a.o[1] = o_sel;
+  a.o[2] = o_win;
+  a.so_b = so_b;
+  a.so_h = so_h;
+  a.so_t = so_t;
+  a.g = gates;
+  a.sg_b = sg_b;
+  a.sg_h = sg_h;
+  a.sg_t = sg_t;
+  a.sg_k = sg_k;
+  a.out = out;
+  a.sx_b = sout_b;
+  a.sx_h = sout_h;
+  a.sx_t = sout_t;
+  a.B = B;
+  a.H = H;
+  a.T = T;
+  a.dv = dv;
+  return launch_mix<false>(dtype, a, (hipStream_t)stream);
+}
+
+extern "C" int nsa_gate_mix_bwd(const void* dout, int64_t sd_b, int64_t sd_h, int64_t sd_t, const void* o_cmp,
+                                const void* o_sel, const void* o_win, int64_t so_b, int64_t so_h, int64_t so_t,
+                                const void* gates, int64_t sg_b, int64_t sg_h, int64_t sg_t, int64_t sg_k,
+                                void* do_cmp, void* do_sel, void* do_win, float* dgates, int B, int H, int T, int dv,
+                                int dtype, nsa_stream_t stream) {
+  using namespace nsa;
+  const void* ptrs[7] = {dout, o_cmp, o_sel, o_win, do_cmp, do_sel, do_win};
+  if (int rc = check_mix(dtype, B, H, T, dv, ptrs, 7)) return rc;
+  const int esz = dtype == NSA_F32 ? 4 : 2;
+  if ((so_t * esz) % 16 || (so_h * esz) % 16 || (sd_t * esz) % 16 || (sd_h * esz) % 16)
+    return set_error(NSA_ERR_LAYOUT, "rows must be 16-byte aligned");
+  MixArgs a{};
+  a.o[0] = o_cmp;
+  a.o[1] = o_sel;
+  a.o[2] = o_win;
+  a.so_b = so_b;
+  a.so_h = so_h;
+  a.so_t = so_t;
+  a.g = gates;
+  a.sg_b = sg_b;
+  a.sg_h = sg_h;
+  a.sg_t = sg_t;
+  a.sg_k = sg_k;
+  a.out = const_cast<void*>(dout);
+  a.sx_b = sd_b;
+  a.sx_h = sd_h;
+  a.sx_t = sd_t;
+  a.dO[0] = do_cmp;
+  a.dO[1] = do_sel;
+  a.dO[2] = do_win;
+  a.dg = dgates;
+  a.B = B;
+  a.H = H;
+  a.T = T;
+  a.dv = dv;
+  return launch_mix<true>(dtype, a, (hipStream_t)stream);
+}

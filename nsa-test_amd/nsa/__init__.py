@@ -9,6 +9,7 @@ Attention" (arXiv:2502.11089).
 """
 from .kernels import (
     CompressionAttention,
+    GatedMix,
     NSAAttention,
     NSAConfig,
     SelectionAttention,

@@ -299,6 +299,45 @@ class _CompressPool(torch.autograd.Function):
 
 
 # ============================================================== selection (Eq. 9 / 10)
+class GatedMix(torch.autograd.Function):
+    """o = o_cmp * g[..., 0] + o_sel * g[..., 1] + o_win * g[..., 2] (NSAAttention.forward,
+    reference nsa/kernels.py:2446-2463) as one fused HIP pass each way.  Branch outputs
+    [B,H,T,dv], gates [B,H,T,3]; the result is a [B,H,T,dv] view of [B,T,H,dv] storage,
+    so the module's transpose + reshape to [B,T,H*dv] copies nothing."""
+
+    @staticmethod
+    def forward(ctx, o_cmp, o_sel, o_win, gates):
+        _ops._check_device(o_cmp, o_sel, o_win, gates)
+        cdt = _ops.compute_dtype(o_cmp.dtype)
+        os_ = [t.to(cdt).contiguous() for t in (o_cmp, o_sel, o_win)]
+        g = gates.to(cdt)
+        B, H, T, dv = os_[0].shape
+        out = torch.empty(B, T, H, dv, device=o_cmp.device, dtype=cdt).permute(0, 2, 1, 3)
+        so, sg, sx = os_[0].stride(), g.stride(), out.stride()
+        _lib.call("nsa_gate_mix_fwd", *[_ops._ptr(t) for t in os_], so[0], so[1], so[2], _ops._ptr(g), *sg,
+                  _ops._ptr(out), sx[0], sx[1], sx[2], B, H, T, dv, _ops._dtype_code(cdt), _ops._stream(o_cmp.device))
+        ctx.save_for_backward(*os_, g)
+        ctx.dtypes = (o_cmp.dtype, o_sel.dtype, o_win.dtype, gates.dtype)
+        return out.to(o_cmp.dtype)
+
+    @staticmethod
+    def backward(ctx, dout):
+        o_c, o_s, o_w, g = ctx.saved_tensors
+        cdt = o_c.dtype
+        B, H, T, dv = o_c.shape
+        d = dout.to(cdt)
+        if d.stride(-1) != 1 or (d.stride(2) * d.element_size()) % 16 or (d.stride(1) * d.element_size()) % 16:
+            d = d.contiguous()
+        dos = [torch.empty(B, H, T, dv, device=d.device, dtype=cdt) for _ in range(3)]
+        dg = torch.empty(B, H, T, 3, device=d.device, dtype=torch.float32)
+        sd, so, sg = d.stride(), o_c.stride(), g.stride()
+        _lib.call("nsa_gate_mix_bwd", _ops._ptr(d), sd[0], sd[1], sd[2], _ops._ptr(o_c), _ops._ptr(o_s),
+                  _ops._ptr(o_w), so[0], so[1], so[2], _ops._ptr(g), *sg, *[_ops._ptr(t) for t in dos],
+                  _ops._ptr(dg), B, H, T, dv, _ops._dtype_code(cdt), _ops._stream(d.device))
+        dts = ctx.dtypes
+        return dos[0].to(dts[0]), dos[1].to(dts[1]), dos[2].to(dts[2]), dg.to(dts[3])
+
+
 def derive_selection_from_compression_per_timestep(compression_scores: torch.Tensor,
                                                    config: NSAConfig) -> torch.Tensor:
     """Eq. 9 (reference nsa/kernels.py:1920-1962): p_slc[j] = sum_{m<l'/d} sum_{n<l/d}
@@ -464,7 +503,7 @@ class NSAAttention(torch.nn.Module):
 
         gates = self.gate_mlp(x).view(B, T, H, 3).permute(0, 2, 1, 3)
         gates = torch.softmax(gates, dim=-1) if c.gate_mode == "softmax" else torch.sigmoid(gates)
-        o = o_cmp * gates[..., 0:1] + o_sel * gates[..., 1:2] + o_win * gates[..., 2:3]
+        o = GatedMix.apply(o_cmp, o_sel, o_win, gates)
         o = o.transpose(1, 2).reshape(B, T, H * dv)
         out = self.dropout(self.o_proj(o))
         info = None
