@@ -93,7 +93,9 @@ template <> __device__ __forceinline__ void unpack16<uint16_t>(const uint4& raw,
 // unit and broadcast to the FMAs; each 16-byte key load feeds RPW * (16 / sizeof(S))
 // FMAs.
 template <typename S, int RPW, int C>
-__global__ __launch_bounds__(512) void score_topn_kernel(ScoreArgs a, const S* __restrict__ qg) {
+// Up to 8 column chunks the accumulators fit 80 VGPRs and six waves per SIMD hide the
+// scalar-load latency of the query rows; wider rows keep the compiler's default.
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(C * RPW <= 64 && C <= 8 ? 6 : 1))) void score_topn_kernel(ScoreArgs a, const S* __restrict__ qg) {
   extern __shared__ float lds[];
   constexpr int EV = 16 / sizeof(S);
   const int tid = threadIdx.x, lane = tid & 63;
