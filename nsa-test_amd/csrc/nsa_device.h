@@ -185,6 +185,14 @@ __device__ __forceinline__ float wave_sum16(float v) {
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// Orders a wave's LDS stores before its later LDS loads of other lanes' data: waits
+// for the wave's LDS operations only (lgkmcnt(0), vmcnt / expcnt left at their
+// maximum), so global loads and stores stay in flight.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_wave_barrier();
+}
+
 // Store 4 consecutive values (one C-tile column slice) as T.
 template <typename T> __device__ __forceinline__ void store4(typename Store<T>::type* p, f32x4 v);
 template <> __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {

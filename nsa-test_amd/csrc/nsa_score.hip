@@ -1,16 +1,21 @@
 // Fused selection scoring on gfx950: Eq. 8 (compressed-attention probabilities),
 // Eq. 9 (triangular remap to selection blocks), Eq. 10 (GQA head sum) and the top-n
-// with fixed blocks, one workgroup per (batch, group, TT consecutive timesteps).
-//
-// Nothing is materialised in HBM except the n indices per (b, g, t) (and, when the
+// with fixed blocks, in two kernels:
+//   score_logits_kernel  the Eq. 8 logits of every (row, visible compressed block) as a
+//                        register-tiled fp32 GEMM into the caller's workspace;
+//   score_rows_kernel    softmax, Eq. 9, Eq. 10 and the top-n, one workgroup per
+//                        (batch, group, TT consecutive timesteps).
+// Besides the workspace only the n indices per (b, g, t) are written (and, when the
 // caller asks for them, the p_cmp / p_slc score tensors the reference module returns
 // in attn_info).
 //
 // The fp32 arithmetic follows a fixed order so that the indices are reproducible
 // bit for bit (this unit is compiled with -ffp-contract=off):
 //   logit   acc = fma(q[e], k[e][i], acc) for e = 0..dk-1, then acc * scale
-//   softmax e_i = exp32(s_i - max); sum = 64 lane partials (lane L adds i = L mod 64 in
-//           ascending order) combined by xor-butterfly over 32,16,8,4,2,1; p = e / sum
+//   softmax e_i = exp32(s_i - max); sum = 64 lane partials (lane L adds the blocks
+//           256 s + 4 L + u, s ascending then u = 0..3) combined by xor-butterfly
+//           over 32,16,8,4,2,1;
+//           p = e * (1 / sum), the reciprocal correctly rounded
 //   Eq. 9   p_slc[j] = sum over (m, n) in the reference's loop order
 //           (nsa/kernels.py:1953-1960), starting from 0
 //   Eq. 10  heads added in head order (nsa/kernels.py:1990-1993)
@@ -33,8 +38,11 @@ __device__ __forceinline__ float exp32(float x) {
   const float kL2e = 1.44269504088896341f;
   const float kLn2Hi = 0.693145751953125f;
   const float kLn2Lo = 1.42860682030941723212e-6f;
-  if (!(x >= -64.0f)) return 0.0f;
-  if (x > 0.0f) x = 0.0f;
+  // branch-free: out-of-range inputs (below -64, -inf, NaN) run the polynomial on 0
+  // and are replaced by 0 at the end; inputs above 0 are clamped to 0
+  const bool ok = x >= -64.0f;
+  x = x > 0.0f ? 0.0f : x;
+  x = ok ? x : 0.0f;
   const float k = rintf(x * kL2e);
   float r = fmaf(-k, kLn2Hi, x);
   r = fmaf(-k, kLn2Lo, r);
@@ -46,7 +54,8 @@ __device__ __forceinline__ float exp32(float x) {
   p = fmaf(p, r, 0.5f);
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
-  return p * __uint_as_float((uint32_t)((int)k + 127) << 23);
+  const float v = p * __uint_as_float((uint32_t)((int)k + 127) << 23);
+  return ok ? v : 0.0f;
 }
 
 struct ScoreArgs {
@@ -59,13 +68,15 @@ struct ScoreArgs {
   int64_t so_b, so_g, so_t, so_n;
   float* p_cmp;  // optional [B,H,T,NB]
   float* p_slc;  // optional [B,H,T,nsel]
+  float* lg;     // workspace: scaled logits [B*G][T*hpg][ncs], row r = t * hpg + head in group
   int B, H, G, hpg, T, dk, NB;
   float scale;
   int a, s, nsel, lprime, n, include_fixed;
-  int TT;  // timesteps per workgroup
+  int ncs;  // logit row stride: NB rounded up to 64
+  int TT;   // rows kernel: timesteps per workgroup
 };
 
-constexpr int kMaxRows = 64;  // rows (timestep, head) of one workgroup
+constexpr int kMaxRows = 64;    // heads per group
 constexpr int kMaxCols = 4096;  // compressed blocks a row can score
 
 template <typename S>
@@ -85,189 +96,282 @@ template <> __device__ __forceinline__ void unpack16<uint16_t>(const uint4& raw,
   }
 }
 
-// One workgroup per (batch, group, TT consecutive timesteps); NW = blockDim / 64 waves.
-// Wave w owns the rows r = w + NW * rr (rr < RPW) of the TT * hpg (timestep, head)
-// rows, and lane L of a wave owns the compressed blocks i = L + 64 c (c < C): the
-// logits, the softmax and Eq. 9 of a row all stay inside the wave that owns it, in
-// registers.  The query row of a wave is wave-uniform, so it is read through the scalar
-// unit and broadcast to the FMAs; each 16-byte key load feeds RPW * (16 / sizeof(S))
-// FMAs.
-template <typename S, int RPW, int C>
-// Up to 8 column chunks the accumulators fit 80 VGPRs and six waves per SIMD hide the
-// scalar-load latency of the query rows; wider rows keep the compiler's default.
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(C * RPW <= 64 && C <= 8 ? 6 : 1))) void score_topn_kernel(ScoreArgs a, const S* __restrict__ qg) {
+// number of compressed blocks [0, ncomp) that hold every block visible at t_last
+// (at least block 0, which the no-visible-block rule scores); s_out is LDS
+__device__ __forceinline__ int score_ncomp(const ScoreArgs& a, int t_last, int* s_out) {
+  if (threadIdx.x == 0) *s_out = 0;
+  __syncthreads();
+  int mx = 0;
+  for (int i = threadIdx.x; i < a.NB; i += blockDim.x)
+    if (a.block_ends[i] <= t_last) mx = i + 1;
+  if (mx) atomicMax(s_out, mx);
+  __syncthreads();
+  const int nc = *s_out;
+  return nc == 0 && a.NB > 0 ? 1 : nc;
+}
+
+// ---------------------------------------------------------------- logits ----
+// Eq. 8 logits of one group as a register-tiled fp32 GEMM on the vector ALU:
+// lg[r][i] = scale * (sum over e = 0..dk-1 of q[r][e] k[i][e]), each element one
+// sequential fma chain in e order (the accumulation order the indices are defined by).
+// Workgroup = 256 query rows x 64 compressed blocks; the operands are staged through
+// LDS as fp32 in EK-feature chunks (the next chunk is loaded into registers while the
+// current one is used) and each lane owns an 8 x 8 tile, so one feature step costs a
+// lane four 16-byte LDS reads for 64 FMAs.  Column tiles past the last block visible
+// to the tile's last timestep exit at once (the causal triangle is never computed).
+constexpr int kLgTM = 256, kLgTN = 64, kLgEK = 32;
+
+template <typename S>
+__global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
+  constexpr int EPL = 16 / sizeof(S);           // elements per 16-byte piece
+  constexpr int APT = kLgEK / EPL;              // A pieces per thread (its row's chunk)
+  constexpr int BPT = kLgTN * (kLgEK / EPL) / 256;  // B pieces per thread
+  constexpr int AP = kLgTM + 4, BP = kLgTN + 4;  // padded LDS rows (16-byte aligned)
+  __shared__ __attribute__((aligned(16))) float As[kLgEK * AP];  // [e][row]
+  __shared__ __attribute__((aligned(16))) float Bs[kLgEK * BP];  // [e][col]
+  __shared__ int s_nc;
+
+  const int tid = threadIdx.x;
+  const int bg = blockIdx.z, b = bg / a.G, g = bg % a.G;
+  const int hpg = a.hpg;
+  const int Rall = a.T * hpg;
+  const int row0 = blockIdx.x * kLgTM, col0 = blockIdx.y * kLgTN;
+  const int t_last = min(a.T - 1, (row0 + kLgTM - 1) / hpg);
+  const int ncomp = score_ncomp(a, t_last, &s_nc);
+  if (col0 >= ncomp) return;  // workgroup-uniform
+
+  // the thread's staging row (A) and column (B)
+  const int arow = min(row0 + tid, Rall - 1);
+  const S* qrow = reinterpret_cast<const S*>(a.q) + b * a.sq_b + (int64_t)(g * hpg + arow % hpg) * a.sq_h +
+                  (int64_t)(arow / hpg) * a.sq_t;
+  const int bcol = tid % kLgTN, bpart0 = tid / kLgTN;
+  const S* kcol = reinterpret_cast<const S*>(a.kc) + b * a.sk_b + g * a.sk_g +
+                  (int64_t)min(col0 + bcol, a.NB - 1) * a.sk_i;
+  const int dk = a.dk;
+  uint4 pa[APT], pb[BPT];
+  auto load = [&](int e0) {
+#pragma unroll
+    for (int j = 0; j < APT; ++j)
+      pa[j] = e0 + j * EPL < dk ? *reinterpret_cast<const uint4*>(qrow + e0 + j * EPL) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      const int e = e0 + (bpart0 + j * (256 / kLgTN)) * EPL;
+      pb[j] = e < dk ? *reinterpret_cast<const uint4*>(kcol + e) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int j = 0; j < APT; ++j) {
+      float v[EPL];
+      unpack16<S>(pa[j], v);
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) As[(j * EPL + u) * AP + tid] = v[u];
+    }
+#pragma unroll
+    for (int j = 0; j < BPT; ++j) {
+      float v[EPL];
+      unpack16<S>(pb[j], v);
+#pragma unroll
+      for (int u = 0; u < EPL; ++u) Bs[((bpart0 + j * (256 / kLgTN)) * EPL + u) * BP + bcol] = v[u];
+    }
+  };
+
+  const int tr = tid >> 3, tc = tid & 7;  // lane tile: rows tr*8.., columns tc*8..
+  float acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+
+  // a chunk past dk holds zeros: fma(0, 0, acc) == acc (acc is never -0), so the
+  // padded steps leave every chain exactly as the dk-step one
+  load(0);
+  for (int e0 = 0; e0 < dk; e0 += kLgEK) {
+    __syncthreads();  // the previous chunk's products are done
+    store();
+    __syncthreads();
+    if (e0 + kLgEK < dk) load(e0 + kLgEK);
+#pragma unroll 8
+    for (int e = 0; e < kLgEK; ++e) {
+      const float4 q0 = *reinterpret_cast<const float4*>(&As[e * AP + tr * 8]);
+      const float4 q1 = *reinterpret_cast<const float4*>(&As[e * AP + tr * 8 + 4]);
+      const float4 k0 = *reinterpret_cast<const float4*>(&Bs[e * BP + tc * 8]);
+      const float4 k1 = *reinterpret_cast<const float4*>(&Bs[e * BP + tc * 8 + 4]);
+      const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+      const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[i][j] = fmaf(qv[i], kv[j], acc[i][j]);
+    }
+  }
+
+  float* out = a.lg + ((int64_t)bg * Rall + row0 + tr * 8) * a.ncs + col0 + tc * 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    if (row0 + tr * 8 + i < Rall) {
+      float* o = out + (int64_t)i * a.ncs;
+      *reinterpret_cast<float4*>(o) = make_float4(acc[i][0] * a.scale, acc[i][1] * a.scale, acc[i][2] * a.scale,
+                                                  acc[i][3] * a.scale);
+      *reinterpret_cast<float4*>(o + 4) = make_float4(acc[i][4] * a.scale, acc[i][5] * a.scale,
+                                                      acc[i][6] * a.scale, acc[i][7] * a.scale);
+    }
+  }
+}
+
+// ------------------------------------------------------------------ rows ----
+// One workgroup of kRowsWaves waves per (batch, group, TT consecutive timesteps); wave
+// w takes the rows r = w, w + kRowsWaves, ... of its R = TT * hpg rows.  A row lives
+// in registers: lane L holds the blocks 256 s + 4 L + u (s < NQ, u < 4), one 16-byte
+// piece per s (a coalesced 1 KB load per wave).  Per row:
+//   1. invisible blocks set to -inf (logits are finite; exp32 maps -inf to 0), max;
+//   2. e = exp32(s - max), lane partials over s then u, xor butterfly;
+//   3. p = e * (1 / sum);
+//   4. Eq. 9 into the row's own workspace slot (its logits are consumed).  For the
+//      (a, s) = (2, 4) remap output j = 64 s + L reads blocks 4j..4j+4: the lane's own
+//      piece s plus the first block of the next lane's piece; other remaps go through
+//      a wave-private LDS copy of the row.
+// After a barrier, Eq. 10 adds each timestep's rows in head order from the workspace
+// (the waves of a workgroup share one CU, so its stores are visible after the
+// barrier), and one wave per timestep runs the top-n.
+// Only blocks below ncomp(t_last) are read; the logits kernel computed every block
+// visible to these rows (its tile's last timestep is not earlier than each row's own).
+constexpr int kRowsWaves = 8;
+
+template <int NQ, bool FAST9>
+__global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a) {
   extern __shared__ float lds[];
-  constexpr int EV = 16 / sizeof(S);
+  constexpr int NW = kRowsWaves;
+  constexpr int NBUF = FAST9 ? 0 : NQ * 256;  // floats of a wave's row copy
   const int tid = threadIdx.x, lane = tid & 63;
-  const int NW = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bg = blockIdx.y, b = bg / a.G, g = bg % a.G;
   const int t0 = blockIdx.x * a.TT;
   const int TT = min(a.TT, a.T - t0);
   const int hpg = a.hpg;
-  const int rows = TT * hpg;  // r = tt * hpg + hh
-  const int t_last = t0 + TT - 1;
-  const int NB = a.NB, nsel = a.nsel, dk = a.dk;
-  const int segw = 64 * a.s + a.a;  // columns Eq. 9 reads for 64 consecutive blocks
+  const int R = TT * hpg;  // r = tt * hpg + hh
+  const int NB = a.NB, nsel = a.nsel, ncs = a.ncs;
 
-  float* pseg = lds + wave * segw;                          // [NW][segw]
-  float* ps = lds + NW * segw;                              // [rows][nsel]
-  float* agg = ps + rows * nsel;                            // [TT][nsel]
-  int* top = reinterpret_cast<int*>(agg + a.TT * nsel);     // [TT][64]
-  int* chosen = top + a.TT * 64;                            // [TT][64]
+  float* wb = lds + wave * NBUF;                           // [NW][NBUF] (generic Eq. 9 only)
+  float* agg = lds + NW * NBUF;                            // [TT][nsel]
+  int* sbe = reinterpret_cast<int*>(agg + a.TT * nsel);    // [NQ*256] block ends (INT_MAX past ncomp)
+  int* topl = sbe + NQ * 256;                              // [TT][64] top-k per timestep
+  __shared__ int s_nc;
 
-  // columns with any visible row (plus block 0 for the no-visible-block rule)
-  __shared__ int s_ncomp;
-  if (tid == 0) s_ncomp = 0;
+  const int ncomp = score_ncomp(a, t0 + TT - 1, &s_nc);
+  const int ncol = ((ncomp + 63) >> 6) * 64;  // blocks the logits kernel computed
+  for (int i = tid; i < NQ * 256; i += blockDim.x) sbe[i] = i < ncomp ? a.block_ends[i] : 0x7fffffff;
   __syncthreads();
-  {
-    int mx = 0;
-    for (int i = tid; i < NB; i += blockDim.x)
-      if (a.block_ends[i] <= t_last) mx = i + 1;
-    if (mx) atomicMax(&s_ncomp, mx);
-  }
-  __syncthreads();
-  int ncomp = s_ncomp;
-  if (ncomp == 0 && NB > 0) ncomp = 1;
-  const int nch = (ncomp + 63) >> 6;  // <= C (checked by the launcher)
+  float* lgb = a.lg + ((int64_t)bg * a.T * hpg + (int64_t)t0 * hpg) * ncs;
+  const float4 ninf4 = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
 
-  int be[C];
-#pragma unroll
-  for (int c = 0; c < C; ++c) {
-    const int i = c * 64 + lane;
-    be[c] = (c < nch && i < ncomp) ? a.block_ends[i] : 0x7fffffff;
-  }
-
-  // ---- Eq. 8 logits: one sequential fma chain over e = 0..dk-1 per (row, block) ----
-  float acc[RPW][C];
-#pragma unroll
-  for (int rr = 0; rr < RPW; ++rr)
-#pragma unroll
-    for (int c = 0; c < C; ++c) acc[rr][c] = 0.0f;
-  const S* kc = reinterpret_cast<const S*>(a.kc) + b * a.sk_b + g * a.sk_g;
-  const S* qb = qg + b * a.sq_b;
-  const S* kcol[C];  // the lane's compressed-key rows (past the last block: the last one)
-#pragma unroll
-  for (int c = 0; c < C; ++c) kcol[c] = kc + (int64_t)min(c * 64 + lane, ncomp - 1) * a.sk_i;
-  // Chunks are processed CB at a time, each group under a wave-uniform branch around its
-  // own pass over the feature axis, so groups past the last visible block cost nothing.
-  constexpr int CB = C < 2 ? C : 2;
-#pragma unroll
-  for (int cb = 0; cb < C; cb += CB) {
-    if (cb < nch) {
-      for (int e0 = 0; e0 < dk; e0 += EV) {
-        float qv[RPW][EV];
-#pragma unroll
-        for (int rr = 0; rr < RPW; ++rr) {
-          const int r = min(wave + NW * rr, rows - 1);
-          const int t = t0 + r / hpg, h = g * hpg + r % hpg;
-          unpack16<S>(*reinterpret_cast<const uint4*>(qb + (int64_t)h * a.sq_h + (int64_t)t * a.sq_t + e0), qv[rr]);
-        }
-        uint4 kraw[CB];
-#pragma unroll
-        for (int c = 0; c < CB; ++c) kraw[c] = *reinterpret_cast<const uint4*>(kcol[cb + c] + e0);
-#pragma unroll
-        for (int c = 0; c < CB; ++c) {
-          float kv[EV];
-          unpack16<S>(kraw[c], kv);
-#pragma unroll
-          for (int rr = 0; rr < RPW; ++rr)
-#pragma unroll
-            for (int u = 0; u < EV; ++u) acc[rr][cb + c] = fmaf(qv[rr][u], kv[u], acc[rr][cb + c]);
-        }
-      }
-    }
-  }
-
-  // ---- per row: softmax (Eq. 8) and Eq. 9, inside the owning wave ----
-#pragma unroll
-  for (int rr = 0; rr < RPW; ++rr) {
-    const int r = wave + NW * rr;
-    if (r >= rows) continue;  // wave-uniform
+  for (int r = wave; r < R; r += NW) {
     const int t = t0 + r / hpg, h = g * hpg + r % hpg;
-    float mx = -INFINITY;
-    bool anyv = false;
+    float* row = lgb + (int64_t)r * ncs;
+    float v[NQ][4];
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      if (c < nch) {
-        acc[rr][c] = acc[rr][c] * a.scale;
-        const bool v = be[c] <= t;
-        anyv |= v;
-        if (v) mx = fmaxf(mx, acc[rr][c]);
-      }
+    for (int s = 0; s < NQ; ++s) {
+      const int col = 256 * s + 4 * lane;
+      const float4 x = col < ncol ? *reinterpret_cast<const float4*>(row + col) : ninf4;
+      v[s][0] = x.x;
+      v[s][1] = x.y;
+      v[s][2] = x.z;
+      v[s][3] = x.w;
     }
-    const bool any_row = __ballot(anyv) != 0ull;
-    if (!any_row) mx = __shfl(acc[rr][0], 0);  // block 0 made visible
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < NQ; ++s) {
+      const int4 be = *reinterpret_cast<const int4*>(sbe + 256 * s + 4 * lane);
+      v[s][0] = be.x <= t ? v[s][0] : -INFINITY;
+      v[s][1] = be.y <= t ? v[s][1] : -INFINITY;
+      v[s][2] = be.z <= t ? v[s][2] : -INFINITY;
+      v[s][3] = be.w <= t ? v[s][3] : -INFINITY;
+      mx = fmaxf(mx, fmaxf(fmaxf(v[s][0], v[s][1]), fmaxf(v[s][2], v[s][3])));
+    }
+    if (__ballot(mx != -INFINITY) == 0ull) {  // no visible block: block 0 is scored
+      mx = row[0];
+      if (lane == 0) v[0][0] = mx;
+    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
-    // lane partial over its blocks in ascending order, then the xor butterfly
     float part = 0.0f;
 #pragma unroll
-    for (int c = 0; c < C; ++c) {
-      if (c < nch) {
-        const bool v = be[c] <= t || (!any_row && c == 0 && lane == 0);
-        const float e = v ? exp32(acc[rr][c] - mx) : 0.0f;
-        acc[rr][c] = e;
-        part += e;
+    for (int s = 0; s < NQ; ++s)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v[s][u] = exp32(v[s][u] - mx);
+        part += v[s][u];
       }
-    }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) part = part + __shfl_xor(part, off);
-    const float sum = part;
+    const float rs = 1.0f / part;
 #pragma unroll
-    for (int c = 0; c < C; ++c)
-      if (c < nch) acc[rr][c] = acc[rr][c] / sum;
+    for (int s = 0; s < NQ; ++s)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[s][u] *= rs;  // blocks past ncomp: p = 0 exactly
     if (a.p_cmp) {
       float* pc = a.p_cmp + (((int64_t)b * a.H + h) * a.T + t) * NB;
 #pragma unroll
-      for (int c = 0; c < C; ++c) {
-        const int i = c * 64 + lane;
-        if (i < NB) pc[i] = (c < nch && i < ncomp) ? acc[rr][c] : 0.0f;
-      }
-    }
-    // Eq. 9 in the reference's (m, n) order, 64 selection blocks at a time from a
-    // per-wave copy of the columns they read
-    float* psr = ps + r * nsel;
-    for (int j0 = 0; j0 < nsel; j0 += 64) {
-      const int lo = j0 * a.s;
+      for (int s = 0; s < NQ; ++s)
 #pragma unroll
-      for (int c = 0; c < C; ++c) {
-        const int i = c * 64 + lane;
-        if (i >= lo && i < lo + segw) pseg[i - lo] = (c < nch && i < ncomp) ? acc[rr][c] : 0.0f;
+        for (int u = 0; u < 4; ++u) {
+          const int i = 256 * s + 4 * lane + u;
+          if (i < NB) pc[i] = v[s][u];
+        }
+    }
+    // Eq. 9 in the reference's (m, n) order, starting from 0; blocks past ncomp (or
+    // NB) add an exact +0
+    float* psl = a.p_slc ? a.p_slc + (((int64_t)b * a.H + h) * a.T + t) * nsel : nullptr;
+    if constexpr (FAST9) {  // (m, n) -> 4j + {0, 1, 1, 2, 2, 3, 3, 4}
+#pragma unroll
+      for (int s = 0; s < NQ; ++s) {
+        float nb = __shfl_down(v[s][0], 1);
+        const float nb63 = s + 1 < NQ ? __shfl(v[s + 1 < NQ ? s + 1 : s][0], 0) : 0.0f;
+        if (lane == 63) nb = nb63;
+        const float s9 = (((((((0.0f + v[s][0]) + v[s][1]) + v[s][1]) + v[s][2]) + v[s][2]) + v[s][3]) + v[s][3]) + nb;
+        const int j = 64 * s + lane;
+        if (j < nsel) {
+          row[j] = s9;
+          if (psl) psl[j] = s9;
+        }
       }
-      __builtin_amdgcn_s_waitcnt(0);
-      __builtin_amdgcn_wave_barrier();
-      const int j = j0 + lane;
-      if (j < nsel) {
+    } else {
+#pragma unroll
+      for (int s = 0; s < NQ; ++s)
+        *reinterpret_cast<float4*>(wb + 256 * s + 4 * lane) = make_float4(v[s][0], v[s][1], v[s][2], v[s][3]);
+      wave_lds_sync();
+      for (int j = lane; j < nsel; j += 64) {
         float s9 = 0.0f;
         for (int m = 0; m < a.s; ++m)
           for (int nn = 0; nn < a.a; ++nn) {
             const int ci = a.s * j + m + nn;
-            if (ci < NB) s9 += ci < ncomp ? pseg[ci - lo] : 0.0f;
+            if (ci < ncomp) s9 += wb[ci];
           }
-        psr[j] = s9;
-        if (a.p_slc) a.p_slc[(((int64_t)b * a.H + h) * a.T + t) * nsel + j] = s9;
+        row[j] = s9;
+        if (psl) psl[j] = s9;
       }
-      __builtin_amdgcn_s_waitcnt(0);
-      __builtin_amdgcn_wave_barrier();
+      wave_lds_sync();  // the copy is rewritten for the wave's next row
     }
   }
   __syncthreads();
 
-  // ---- Eq. 10: heads added in head order ----
+  // Eq. 10: heads added in head order
   for (int x = tid; x < TT * nsel; x += blockDim.x) {
     const int tt = x / nsel, j = x % nsel;
+    const float* src = lgb + (int64_t)tt * hpg * ncs + j;
     float ag = 0.0f;
-    for (int hh = 0; hh < hpg; ++hh) ag += ps[(tt * hpg + hh) * nsel + j];
+    for (int hh = 0; hh < hpg; ++hh) ag += src[(int64_t)hh * ncs];
     agg[tt * nsel + j] = ag;
   }
   __syncthreads();
 
   // ---- top-n (one wave per timestep) ----
   const int kk = min(a.n, nsel);
+  const int nc = a.include_fixed ? 3 : 0;
   for (int tt = wave; tt < TT; tt += NW) {
     const int t = t0 + tt;
     float* ag = agg + tt * nsel;
+    int* tl = topl + tt * 64;
     for (int rk = 0; rk < kk; ++rk) {
       float bv = -INFINITY;
       int bi = 0x7fffffff;
@@ -288,97 +392,93 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(C * RPW <= 
         }
       }
       if (lane == 0) {
-        top[tt * 64 + rk] = bi;
+        tl[rk] = bi;
         ag[bi] = -INFINITY;  // taken
       }
-      __builtin_amdgcn_s_waitcnt(0);
-      __builtin_amdgcn_wave_barrier();
+      wave_lds_sync();
     }
-    if (lane == 0) {
-      int64_t* o = a.out + b * a.so_b + g * a.so_g + (int64_t)t * a.so_t;
-      int* sel = chosen + tt * 64;
-      int no = 0;
-      // fixed candidates [0, max(0, (t - l') / l'), t / l'] first
-      const int nc = a.include_fixed ? 3 : 0;
-      const int c1 = t >= a.lprime ? (t - a.lprime) / a.lprime : 0;
-      const int c2 = t / a.lprime;
-      for (int c = 0; c < nc + kk && no < a.n; ++c) {
-        const int v = c < nc ? (c == 0 ? 0 : c == 1 ? c1 : c2) : top[tt * 64 + c - nc];
-        bool dup = false;
-        for (int u = 0; u < no; ++u) dup |= sel[u] == v;
-        if (!dup) sel[no++] = v;
+    // candidates: fixed [0, max(0,(t-l')/l'), t/l'] then the top-k.  The top-k are
+    // distinct, so a candidate can only repeat one of the fixed ones before it.
+    const int f1 = t >= a.lprime ? (t - a.lprime) / a.lprime : 0;
+    const int f2 = t / a.lprime;
+    const int ncand = nc + kk;
+    int64_t* o = a.out + b * a.so_b + g * a.so_g + (int64_t)t * a.so_t;
+    int kept = 0;  // candidates kept so far (wave-uniform)
+    for (int c0 = 0; c0 < ncand && kept < a.n; c0 += 64) {
+      const int c = c0 + lane;
+      int v = -1;
+      bool keep = false;
+      if (c < ncand) {
+        v = c < nc ? (c == 0 ? 0 : c == 1 ? f1 : f2) : tl[c - nc];
+        const bool dup = nc > 0 && ((c > 0 && v == 0) || (c > 1 && v == f1) || (c > 2 && v == f2));
+        keep = !dup;
       }
-      for (int u = 0; u < a.n; ++u) o[(int64_t)u * a.so_n] = u < no ? (int64_t)sel[u] : -1;
+      const uint64_t km = __ballot(keep);
+      const int rank = kept + __builtin_popcountll(km & ((1ull << lane) - 1ull));
+      if (keep && rank < a.n) o[(int64_t)rank * a.so_n] = v;
+      kept += __builtin_popcountll(km);
     }
+    for (int u = min(kept, a.n) + lane; u < a.n; u += 64) o[(int64_t)u * a.so_n] = -1;
   }
 }
 
-template <typename S, int RPW, int C>
-static hipError_t launch_score_k(const ScoreArgs& a, int nw, size_t lds, hipStream_t st) {
-  auto fn = score_topn_kernel<S, RPW, C>;
+static int score_ncs(int NB) { return NB > 0 ? ((NB + 63) / 64) * 64 : 64; }
+
+static int score_rows_nq(int ncs) {  // 16-byte pieces per lane: a power of two >= ncs / 256
+  int nq = 1;
+  while (nq * 256 < ncs) nq *= 2;
+  return nq;
+}
+
+static size_t score_rows_lds(int nq, bool fast9, int TT, int nsel) {
+  return 4 * ((size_t)(fast9 ? 0 : kRowsWaves * nq * 256) + (size_t)TT * nsel + (size_t)nq * 256 + (size_t)TT * 64);
+}
+
+template <int NQ, bool FAST9>
+static hipError_t launch_rows_k(const ScoreArgs& a, size_t lds, hipStream_t st) {
+  auto fn = score_rows_kernel<NQ, FAST9>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
   if (e != hipSuccess) return e;
   dim3 grid((a.T + a.TT - 1) / a.TT, a.B * a.G);
-  hipLaunchKernelGGL(fn, grid, dim3(64 * nw), lds, st, a, reinterpret_cast<const S*>(a.q));
+  hipLaunchKernelGGL(fn, grid, dim3(64 * kRowsWaves), lds, st, a);
   return hipGetLastError();
 }
 
-template <typename S, int RPW>
-static hipError_t launch_score_c(const ScoreArgs& a, int nw, int C, size_t lds, hipStream_t st) {
-  switch (C) {
-    case 1: return launch_score_k<S, RPW, 1>(a, nw, lds, st);
-    case 2: return launch_score_k<S, RPW, 2>(a, nw, lds, st);
-    case 4: return launch_score_k<S, RPW, 4>(a, nw, lds, st);
-    case 8: return launch_score_k<S, RPW, 8>(a, nw, lds, st);
-    case 16: if constexpr (RPW <= 8) return launch_score_k<S, RPW, 16>(a, nw, lds, st); break;
-    case 32: if constexpr (RPW <= 4) return launch_score_k<S, RPW, 32>(a, nw, lds, st); break;
-    case 64: if constexpr (RPW <= 2) return launch_score_k<S, RPW, 64>(a, nw, lds, st); break;
+template <bool FAST9>
+static hipError_t launch_rows_q(const ScoreArgs& a, int nq, size_t lds, hipStream_t st) {
+  switch (nq) {
+    case 1: return launch_rows_k<1, FAST9>(a, lds, st);
+    case 2: return launch_rows_k<2, FAST9>(a, lds, st);
+    case 4: return launch_rows_k<4, FAST9>(a, lds, st);
+    case 8: return launch_rows_k<8, FAST9>(a, lds, st);
+    case 16: return launch_rows_k<16, FAST9>(a, lds, st);
   }
   return hipErrorInvalidValue;
 }
 
-template <typename S>
-static hipError_t launch_score_r(const ScoreArgs& a, int nw, int RPW, int C, size_t lds, hipStream_t st) {
-  switch (RPW) {
-    case 1: return launch_score_c<S, 1>(a, nw, C, lds, st);
-    case 2: return launch_score_c<S, 2>(a, nw, C, lds, st);
-    case 4: return launch_score_c<S, 4>(a, nw, C, lds, st);
-    case 8: return launch_score_c<S, 8>(a, nw, C, lds, st);
-  }
-  return hipErrorInvalidValue;
-}
-
-static int pow2_at_least(int x) {
-  int p = 1;
-  while (p < x) p <<= 1;
-  return p;
-}
-
-// Picks (waves, timesteps, rows per wave, column chunks) for the shape.  Returns 0 on
-// success, 1 when no configuration fits (too many heads or compressed blocks), 2 on a
-// HIP launch error.
+// Launches the logits GEMM and the rows kernel.  The rows kernel takes as many
+// timesteps as fit 64 rows and the LDS budget (two workgroups per CU preferred).
+// Returns 0 on success, 1 when no configuration fits, 2 on a HIP launch error.
 int launch_score_topn(int dtype, ScoreArgs a, hipStream_t st) {
-  constexpr size_t kLdsMax = 160 * 1024;
-  if (a.NB > kMaxCols) return 1;
-  const int C = pow2_at_least(max(1, (a.NB + 63) / 64));
-  // accumulator budget per lane: RPW * C <= 64 preferred, 128 at most
-  for (int budget : {64, 128})
-    for (int nw : {4, 8})
-      for (int TT : {4, 2, 1}) {
-        if (TT > 1 && TT * a.hpg > kMaxRows) continue;
-        const int rows = TT * a.hpg;
-        const int RPW = pow2_at_least((rows + nw - 1) / nw);
-        if (RPW > 8 || RPW * C > budget) continue;
-        const int segw = 64 * a.s + a.a;
-        const size_t lds = 4 * ((size_t)nw * segw + (size_t)rows * a.nsel + (size_t)TT * a.nsel + (size_t)TT * 128);
-        if (lds > kLdsMax) continue;
-        a.TT = TT;
-        hipError_t e = dtype == kF32 ? launch_score_r<float>(a, nw, RPW, C, lds, st)
-                                     : launch_score_r<uint16_t>(a, nw, RPW, C, lds, st);
-        return e == hipSuccess ? 0 : 2;
-      }
-  return 1;
+  if (a.NB > kMaxCols || a.hpg > kMaxRows) return 1;
+  a.ncs = score_ncs(a.NB);
+  {
+    const int Rall = a.T * a.hpg;
+    const dim3 grid((Rall + kLgTM - 1) / kLgTM, a.ncs / kLgTN, a.B * a.G);
+    if (dtype == kF32) hipLaunchKernelGGL(score_logits_kernel<float>, grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(score_logits_kernel<uint16_t>, grid, dim3(256), 0, st, a);
+    if (hipGetLastError() != hipSuccess) return 2;
+  }
+  int TT = 1;
+  while (TT * 2 * a.hpg <= kMaxRows && TT * 2 <= a.T) TT *= 2;
+  const int nq = score_rows_nq(a.ncs);
+  const bool fast9 = a.a == 2 && a.s == 4;
+  const size_t lds = score_rows_lds(nq, fast9, TT, a.nsel);
+  if (lds > 156 * 1024) return 1;
+  a.TT = TT;
+  const hipError_t e = fast9 ? launch_rows_q<true>(a, nq, lds, st) : launch_rows_q<false>(a, nq, lds, st);
+  return e == hipSuccess ? 0 : 2;
 }
 
 }  // namespace nsa
@@ -388,7 +488,15 @@ int launch_score_topn(int dtype, ScoreArgs a, hipStream_t st) {
 
 #include "nsa_kernels.h"
 
-extern "C" size_t nsa_score_topn_workspace_size(int, int, int, int, int, int, int) { return 0; }
+// the fp32 logits of every (row, compressed block): Z*H*T rows of NB rounded up to 64
+extern "C" size_t nsa_score_topn_workspace_size(int Z, int H, int n_kv_groups, int n_ctx, int head_dim_qk,
+                                                int n_blocks, int n) {
+  (void)n_kv_groups;
+  (void)head_dim_qk;
+  (void)n;
+  if (Z <= 0 || H <= 0 || n_ctx <= 0 || n_blocks < 0) return 0;
+  return (size_t)Z * H * n_ctx * nsa::score_ncs(n_blocks) * 4;
+}
 
 extern "C" int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* block_ends, int64_t* out_idx,
                               float* p_cmp, float* p_slc, int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
@@ -398,8 +506,6 @@ extern "C" int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* b
                               int n_blocks, int l, int d, int l_prime, int n, int include_fixed, int n_fixed,
                               int dtype, float scale, void* workspace, size_t workspace_bytes, nsa_stream_t stream) {
   using namespace nsa;
-  (void)workspace;
-  (void)workspace_bytes;
   if (dtype != NSA_F32 && dtype != NSA_BF16) return nsa::set_error(NSA_ERR_INVALID, "dtype not supported");
   if (Z <= 0 || H <= 0 || n_kv_groups <= 0 || H % n_kv_groups || n_ctx < 0 || head_dim_qk <= 0 || n_blocks < 0)
     return nsa::set_error(NSA_ERR_INVALID, "bad shape");
@@ -421,7 +527,17 @@ extern "C" int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* b
     if (!qok) return nsa::set_error(NSA_ERR_LAYOUT, "q needs a unit-stride feature axis with 16-byte aligned rows");
   }
   if (n_ctx == 0) return NSA_OK;
+  {
+    const size_t need = (size_t)Z * H * n_ctx * score_ncs(n_blocks) * 4;
+    if (workspace_bytes < need || (need && (!workspace || ((uintptr_t)workspace) % 16))) {
+      char msg[128];
+      snprintf(msg, sizeof(msg), "workspace of %zu bytes (16-byte aligned) required, %zu given", need,
+               workspace_bytes);
+      return nsa::set_error(NSA_ERR_WORKSPACE, msg);
+    }
+  }
   ScoreArgs a{};
+  a.lg = static_cast<float*>(workspace);
   a.q = q;
   a.sq_b = stride_qz;
   a.sq_h = stride_qh;

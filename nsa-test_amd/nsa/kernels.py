@@ -408,10 +408,12 @@ def score_and_select(q: torch.Tensor, k_compressed: torch.Tensor, block_ends: to
     out = torch.empty(B, G, T, config.n, device=q.device, dtype=torch.long)
     pc = torch.empty(B, H, T, N, device=q.device, dtype=torch.float32) if return_scores else None
     ps = torch.empty(B, H, T, nsel, device=q.device, dtype=torch.float32) if return_scores else None
+    ws_bytes = _lib.load().nsa_score_topn_workspace_size(B, H, G, T, dk, N, config.n)
+    ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
     _lib.call("nsa_score_topn", _ops._ptr(qc), _ops._ptr(kc), _ops._ptr(be), _ops._ptr(out), _ops._ptr(pc),
               _ops._ptr(ps), *qc.stride(), *kc.stride(), *out.stride(), B, H, G, T, dk, N, config.l, config.d,
               config.l_prime, config.n, int(bool(config.include_fixed_in_selection)), int(config.n_fixed),
-              _ops._dtype_code(cdt), float(scale), _ops._ptr(None), 0, _ops._stream(q.device))
+              _ops._dtype_code(cdt), float(scale), _ops._ptr(ws), ws_bytes, _ops._stream(q.device))
     if return_scores:
         return out, pc, ps
     return out

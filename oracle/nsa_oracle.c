@@ -214,14 +214,19 @@ int oracle_attn_bwd(int kind, int B, int H, int G, int Tq, int Tkv, int dk, int 
 }
 
 /* ------------------------------------------------------ Eq. 8 -> top-n --- */
-/* Sum of e[0..n) in the order the GPU kernel uses: 64 lane partials (lane L sums
- * the elements with index = L mod 64, ascending), then a butterfly over lane
- * distance 32, 16, 8, 4, 2, 1. */
+/* Sum of e[0..n) in the order the GPU kernel uses: 64 lane partials, lane L summing
+ * the elements 256 s + 4 L + u (s ascending, then u = 0..3) -- the four consecutive
+ * elements of each 1 KB row piece it holds -- then a butterfly over lane distance
+ * 32, 16, 8, 4, 2, 1. */
 static float lane_order_sum(const float* e, int n) {
   float part[64];
   for (int L = 0; L < 64; ++L) {
     float acc = 0.0f;
-    for (int i = L; i < n; i += 64) acc += e[i];
+    for (int s = 0; 256 * s < n; ++s)
+      for (int u = 0; u < 4; ++u) {
+        const int i = 256 * s + 4 * L + u;
+        if (i < n) acc += e[i];
+      }
     part[L] = acc;
   }
   for (int off = 32; off >= 1; off >>= 1) {
@@ -276,7 +281,10 @@ int oracle_score_topn(int B, int H, int G, int T, int dk, int NB, const float* q
           }
           for (int i = 0; i < NB; ++i) sv[i] = vis[i] ? oracle_exp32(sv[i] - mx) : 0.0f;
           const float sum = lane_order_sum(sv, NB);
-          for (int i = 0; i < NB; ++i) sv[i] = sv[i] / sum;
+          /* normalised with the correctly rounded reciprocal of the sum (one multiply
+           * per block) */
+          const float rs = 1.0f / sum;
+          for (int i = 0; i < NB; ++i) sv[i] = sv[i] * rs;
           if (p_cmp) memcpy(p_cmp + (((int64_t)b * H + h) * T + tr) * NB, sv, sizeof(float) * (size_t)NB);
           /* Eq. 9, accumulated in the reference's (m, n) order */
           for (int j = 0; j < nsel; ++j) {

@@ -135,3 +135,29 @@ def test_score_topn_full_size_sampled(dev, cfgname):
     assert (idx == (t // lp)[None, None, :, None]).any(-1).all()
     srt = np.sort(idx, axis=-1)
     assert not ((srt[..., 1:] == srt[..., :-1]) & (srt[..., 1:] >= 0)).any()
+
+
+@pytest.mark.parametrize("H,G,T,dk,dtype", [(64, 1, 9000, 32, torch.float32), (48, 2, 4500, 64, torch.bfloat16)])
+def test_score_topn_multipass_sampled(dev, H, G, T, dk, dtype):
+    """Many heads per group with many compressed blocks: a timestep's rows are scored
+    in several LDS passes whose Eq. 10 sums continue in head order.  Sampled rows,
+    indices and scores bit-exact."""
+    B, l, d, lp, n = 1, 32, 16, 64, 16
+    rng = np.random.default_rng(H + T)
+    q = rng.standard_normal((B, H, T, dk)).astype(np.float32)
+    be = _block_ends(T, l, d)
+    kc = rng.standard_normal((B, G, dk, be.shape[0])).astype(np.float32)
+    if dtype == torch.bfloat16:
+        q = torch.tensor(q).to(torch.bfloat16).float().numpy()
+        kc = torch.tensor(kc).to(torch.bfloat16).float().numpy()
+    cfg = NSAConfig(head_dim_qk=dk, n_heads=H, n_kv_groups=G, l=l, d=d, l_prime=lp, n=n)
+    qd = torch.tensor(q).to(dtype).to(dev)
+    kd = torch.tensor(kc).to(dtype).to(dev)
+    idx, pc, ps = (x.cpu().numpy() for x in score_and_select(qd, kd, torch.tensor(be).to(dev), 1 / math.sqrt(dk),
+                                                             cfg, return_scores=True))
+    rows = np.unique(np.concatenate([np.arange(0, 20), np.linspace(0, T - 1, 24).astype(int), [T - 1]]))
+    ridx, rpc, rps = oracle.score_topn(q[:, :, rows], kc, be, np.float32(1 / math.sqrt(dk)), l=l, d=d, lprime=lp,
+                                       n=n, positions=rows, want_scores=True)
+    np.testing.assert_array_equal(idx[:, :, rows], ridx)
+    np.testing.assert_array_equal(pc[:, :, rows], rpc)
+    np.testing.assert_array_equal(ps[:, :, rows], rps)
