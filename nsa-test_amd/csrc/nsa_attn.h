@@ -10,7 +10,8 @@ enum DType : int { kF32 = 0, kBF16 = 1 };
 
 // Columns handled by one forward / dQ workgroup (4 waves x NSUB x 16).
 constexpr int kFwdNSub = 2;
-constexpr int kFwdCols = 4 * kFwdNSub * 16;
+constexpr int kFwdWaves = 8;
+constexpr int kFwdCols = kFwdWaves * kFwdNSub * 16;
 constexpr int kDqNSub = 1;
 constexpr int kDqCols = 4 * kDqNSub * 16;
 // Distinct selection blocks a row's union bitmap can hold.

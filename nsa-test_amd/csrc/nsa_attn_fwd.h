@@ -1,7 +1,7 @@
 // Forward attention for the three NSA branches (sliding window, compression,
 // top-n selection) on gfx950.
 //
-// One workgroup = 4 waves = kFwdCols query columns of one (batch, KV group).  A
+// One workgroup = kFwdWaves waves = kFwdCols query columns of one (batch, KV group).  A
 // column is one (timestep, head) pair of the group, flattened time-major, so the
 // whole group's heads at a timestep share every K/V tile that is staged in LDS
 // (one K/V load per GQA group instead of one per head).
@@ -25,28 +25,44 @@
 
 namespace nsa {
 
+// Workgroup = kFwdWaves waves x kFwdNSub subtiles x 16 columns.  The K and V^T
+// fragments of a 64-key tile are copied global -> LDS by the direct-to-LDS loads
+// (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l), one 1 KB MFMA
+// fragment per instruction, into a double buffer: the copy of tile i+1 is in flight
+// while tile i is used, no register holds staging data, and each fragment read is a
+// conflict-free 16-byte-per-lane LDS read.  Every fragment read feeds the products of
+// all NSUB subtiles of the wave.
+template <typename T, int DK, int DV>
+struct FwdTile {
+  static constexpr int KC = Elem<T>::kKChunk;
+  static constexpr int CK = CFrag<T>::kKeys;
+  static constexpr int NKF = 4 * (DK / KC);          // K fragments (ks, kc)
+  static constexpr int NVF = (64 / CK) * (DV / 16);  // V^T fragments (kc2, j)
+  static constexpr int BYTES = (NKF + NVF) * 1024;
+  static constexpr int NBUF = 2 * BYTES <= 96 * 1024 ? 2 : 1;
+};
+
 template <typename T, int DK, int DV, int BR>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   static_assert(BR == kSliding || BR == kCompression, "selection uses attn_sel_fwd_kernel");
   using S = typename Store<T>::type;
+  using FT = FwdTile<T, DK, DV>;
   constexpr int EPF = Elem<T>::kPerFrag;
   constexpr int KC = Elem<T>::kKChunk;
   constexpr int NKC = DK / KC;
   constexpr int NSUB = kFwdNSub;
-  constexpr int KP = DK + EPF;  // padded LDS row of the K tile
-  constexpr int VP = 64 + EPF;  // padded LDS row of the V^T tile
   constexpr int CK = CFrag<T>::kKeys;
   constexpr int CT = CK / 16;
+  constexpr int NW = kFwdWaves;
   static_assert(DK % KC == 0 && DV % 16 == 0, "head dims");
 
-  __shared__ __attribute__((aligned(16))) S Ks[64 * KP];
-  __shared__ __attribute__((aligned(16))) S Vs[DV * VP];
-  __shared__ int s_be[64];
+  extern __shared__ __attribute__((aligned(16))) uint4 fwd_lds[];  // [NBUF][NKF + NVF][64]
+  __shared__ int s_be[2][64];
   __shared__ int s_misc[4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4;
   const int c16 = lane & 15;
   const int bg = blockIdx.y;
@@ -107,75 +123,78 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
     if (tid == 0) s_misc[0] = 0;
     __syncthreads();
     int mx = 0;
-    for (int i = tid; i < a.Tkv; i += 256)
+    for (int i = tid; i < a.Tkv; i += blockDim.x)
       if (a.block_ends[i] <= t_last) mx = i + 1;
     if (mx) atomicMax(&s_misc[0], mx);
     __syncthreads();
     ntiles = (s_misc[0] + 63) / 64;
   }
 
-  // ---- K rows / V^T columns of a 64-key tile: loaded into registers one tile ahead,
-  // stored to LDS once the previous tile's products are done ----
-  constexpr int NKP = (64 * (DK / EPF) + 255) / 256;
-  constexpr int NVP = (DV * (64 / EPF) + 255) / 256;
-  u32x4 pk[NKP], pv[NVP];
-  int pbe = 0x7fffffff;
+  // ---- the direct-to-LDS copy of one tile: wave w copies fragments w, w + NW, ... ----
+  auto copy_tile = [&](int key0, int buf) __attribute__((always_inline)) {
+    uint4* dst = fwd_lds + buf * (FT::NKF + FT::NVF) * 64;
+    for (int f = wave; f < FT::NKF + FT::NVF; f += NW) {
+      const S* src;
+      if (f < FT::NKF) {  // K rows of keys key0 + 16 ks + c16, features kc*KC + g4*EPF..
+        const int ks = f / NKC, kc = f % NKC;
+        src = kt + (int64_t)(key0 + ks * 16 + c16) * DK + kc * KC + g4 * EPF;
+      } else {  // V^T rows j*16 + c16, keys of C-permuted chunk kc2 (group g4)
+        const int v = f - FT::NKF, kc2 = v / (DV / 16), j = v % (DV / 16);
+        src = vt + (int64_t)(j * 16 + c16) * a.Tp + key0 + kc2 * CK + g4 * EPF;
+      }
+      copy16_to_lds(src, dst + f * 64);
+    }
+  };
   auto tile_key0 = [&](int it) -> int { return BR == kSliding ? key_lo + it * 64 : it * 64; };
-  auto load_tile = [&](int key0) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < NKP; ++j) {
-      const int c = min(tid + 256 * j, 64 * (DK / EPF) - 1);
-      pk[j] = *reinterpret_cast<const u32x4*>(kt + (int64_t)(key0 + c / (DK / EPF)) * DK + (c % (DK / EPF)) * EPF);
-    }
-#pragma unroll
-    for (int j = 0; j < NVP; ++j) {
-      const int c = min(tid + 256 * j, DV * (64 / EPF) - 1);
-      pv[j] = *reinterpret_cast<const u32x4*>(vt + (int64_t)(c / (64 / EPF)) * a.Tp + key0 + (c % (64 / EPF)) * EPF);
-    }
+  int pbe = 0x7fffffff;
+  auto load_be = [&](int key0) {
     if (BR == kCompression && tid < 64) {
       const int key = key0 + tid;
       pbe = key < a.Tkv ? a.block_ends[key] : 0x7fffffff;
     }
   };
-  if (ntiles > 0) load_tile(tile_key0(0));
+  if (ntiles > 0) {
+    copy_tile(tile_key0(0), 0);
+    load_be(tile_key0(0));
+  }
 
   for (int it = 0; it < ntiles; ++it) {
     const int key0 = tile_key0(it);
-    // ---- stage K rows and V^T columns of keys [key0, key0+64) ----
-#pragma unroll
-    for (int j = 0; j < NKP; ++j) {
-      const int c = tid + 256 * j;
-      if ((64 * (DK / EPF)) % 256 == 0 || c < 64 * (DK / EPF))
-        *reinterpret_cast<u32x4*>(&Ks[(c / (DK / EPF)) * KP + (c % (DK / EPF)) * EPF]) = pk[j];
+    const int buf = FT::NBUF == 2 ? (it & 1) : 0;
+    if (BR == kCompression && tid < 64) s_be[it & 1][tid] = pbe;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile it have landed
+    __syncthreads();                // every wave's have; tile it-1 is no longer read
+    if (FT::NBUF == 2 && it + 1 < ntiles) {
+      copy_tile(tile_key0(it + 1), buf ^ 1);
+      load_be(tile_key0(it + 1));
     }
-#pragma unroll
-    for (int j = 0; j < NVP; ++j) {
-      const int c = tid + 256 * j;
-      if ((DV * (64 / EPF)) % 256 == 0 || c < DV * (64 / EPF))
-        *reinterpret_cast<u32x4*>(&Vs[(c / (64 / EPF)) * VP + (c % (64 / EPF)) * EPF]) = pv[j];
-    }
-    if (BR == kCompression && tid < 64) s_be[tid] = pbe;
-    __syncthreads();
-    if (it + 1 < ntiles) load_tile(tile_key0(it + 1));
+    const uint4* kb = fwd_lds + buf * (FT::NKF + FT::NVF) * 64;
+    const uint4* vb = kb + FT::NKF * 64;
+    const int* sbe = s_be[it & 1];
 
     int be_max = 0;
     if (BR == kCompression) {
-      be_max = s_be[lane];
+      be_max = sbe[lane];
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) be_max = max(be_max, __shfl_xor(be_max, o));
     }
 
+    // S^T for every subtile: each K fragment read from LDS feeds NSUB products
+    f32x4 st[NSUB][4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+      for (int s = 0; s < NSUB; ++s) st[s][ks] = zero4();
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) {
+        const uint4 kf = kb[(ks * NKC + kc) * 64 + lane];
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) st[s][ks] = Mma<T>::run(st[s][ks], kf, qf[s][kc]);
+      }
+    }
+    uint4 pf[NSUB][64 / CK];
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
-      f32x4 st[4];
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        st[ks] = zero4();
-        const S* krow = &Ks[(ks * 16 + c16) * KP];
-#pragma unroll
-        for (int kc = 0; kc < NKC; ++kc) st[ks] = Mma<T>::run(st[ks], frag_std<T>(krow + kc * KC, g4), qf[s][kc]);
-      }
-
       const int t = colt[s];
       // sliding: the column sees keys [kmin_s, kmin_s + kspan_s) (branch-free test)
       const int kmin_s = max(t - a.window + 1, 0);
@@ -192,8 +211,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            st[ks][i] *= scale2;
-            mx = fmaxf(mx, st[ks][i]);
+            st[s][ks][i] *= scale2;
+            mx = fmaxf(mx, st[s][ks][i]);
           }
       } else {
 #pragma unroll
@@ -203,9 +222,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
             const int key = key0 + ks * 16 + 4 * g4 + i;
             bool ok;
             if (BR == kSliding) ok = (uint32_t)(key - kmin_s) < kspan_s;
-            else ok = colv[s] & (s_be[ks * 16 + 4 * g4 + i] <= t);
-            const float v = ok ? st[ks][i] * scale2 : -INFINITY;
-            st[ks][i] = v;
+            else ok = colv[s] & (sbe[ks * 16 + 4 * g4 + i] <= t);
+            const float v = ok ? st[s][ks][i] * scale2 : -INFINITY;
+            st[s][ks][i] = v;
             mx = fmaxf(mx, v);
           }
         }
@@ -218,8 +237,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = fast_exp2(st[ks][i] - mref);
-          st[ks][i] = p;
+          const float p = fast_exp2(st[s][ks][i] - mref);
+          st[s][ks][i] = p;
           rs += p;
         }
       }
@@ -233,18 +252,25 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
       }
       lsum[s] += rs;
       m2[s] = mnew;
+#pragma unroll
+      for (int kc2 = 0; kc2 < 64 / CK; ++kc2) pf[s][kc2] = CFrag<T>::pack(st[s][kc2 * CT], st[s][kc2 * CT + CT - 1]);
+    }
 
+    // O^T += V^T P^T: each V^T fragment read from LDS feeds NSUB products
 #pragma unroll
-      for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
-        const uint4 pf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
+    for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
 #pragma unroll
-        for (int j = 0; j < DV / 16; ++j) {
-          const uint4 vf = frag_cperm<T>(&Vs[(j * 16 + c16) * VP + kc2 * CK], g4);
-          oacc[s][j] = Mma<T>::run(oacc[s][j], vf, pf);
-        }
+      for (int j = 0; j < DV / 16; ++j) {
+        const uint4 vf = vb[(kc2 * (DV / 16) + j) * 64 + lane];
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) oacc[s][j] = Mma<T>::run(oacc[s][j], vf, pf[s][kc2]);
       }
     }
-    __syncthreads();
+    if (FT::NBUF == 1 && it + 1 < ntiles) {  // single buffer: refill once every wave is done
+      __syncthreads();
+      copy_tile(tile_key0(it + 1), 0);
+      load_be(tile_key0(it + 1));
+    }
   }
 
   // ---- epilogue: normalise, store O, L = log(l), M = max s -----------------------
@@ -268,11 +294,15 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnArgs a) {
 
 template <typename T, int DK, int DV, int BR>
 void launch_attn_fwd(const AttnArgs& a, hipStream_t s) {
-  dim3 grid((a.Tq * a.hpg + kFwdCols - 1) / kFwdCols, a.B * a.G);
   if constexpr (BR == kSelection) {
     launch_attn_sel_fwd<T, DK, DV>(a, s);  // per-wave selection kernel
   } else {
-    hipLaunchKernelGGL((attn_fwd_kernel<T, DK, DV, BR>), grid, dim3(256), 0, s, a);
+    using FT = FwdTile<T, DK, DV>;
+    const size_t lds = (size_t)FT::NBUF * FT::BYTES;
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, DK, DV, BR>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    dim3 grid((a.Tq * a.hpg + kFwdCols - 1) / kFwdCols, a.B * a.G);
+    hipLaunchKernelGGL((attn_fwd_kernel<T, DK, DV, BR>), grid, dim3(64 * kFwdWaves), lds, s, a);
   }
 }
 

@@ -185,6 +185,16 @@ __device__ __forceinline__ float wave_sum16(float v) {
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// Direct global -> LDS copy (global_load_lds_dwordx4): every lane reads 16 bytes at
+// its own `src` and lane l's bytes land at lds_base + 16 l.  lds_base must be
+// wave-uniform and 16-byte aligned; the copy completes with the wave's vmcnt.  The
+// explicit address-space casts keep the host-side instantiation of the calling
+// kernels valid.
+__device__ __forceinline__ void copy16_to_lds(const void* src, void* lds_base) {
+  __builtin_amdgcn_global_load_lds((__attribute__((address_space(1))) void*)(src),
+                                   (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
+}
+
 // Orders a wave's LDS stores before its later LDS loads of other lanes' data: waits
 // for the wave's LDS operations only (lgkmcnt(0), vmcnt / expcnt left at their
 // maximum), so global loads and stores stay in flight.
