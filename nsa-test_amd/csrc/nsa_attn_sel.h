@@ -69,7 +69,9 @@ __device__ __forceinline__ bool sel_has(const int* l, int nslots, int blk) {
 
 // ============================================================== forward
 template <typename T, int DK, int DV>
-__global__ __launch_bounds__(256) void attn_sel_fwd_kernel(AttnArgs a, int ncoltiles) {
+// Two waves per SIMD (256 registers): the second wave covers the latency of the first
+// one's fragment loads and softmax, which bound this kernel with one wave per SIMD.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_sel_fwd_kernel(AttnArgs a, int ncoltiles) {
   using S = typename Store<T>::type;
   constexpr int EPF = Elem<T>::kPerFrag;
   constexpr int KC = Elem<T>::kKChunk;
