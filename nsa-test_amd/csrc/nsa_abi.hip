@@ -55,7 +55,7 @@ struct Shape {
 };
 
 struct Layout {
-  size_t kt = 0, kn = 0, vt = 0, vn = 0, krf = 0, kcf = 0, vrf = 0, vcf = 0, lse2 = 0, delta = 0, clean = 0, chunk = 0, csr_off = 0, csr_t = 0,
+  size_t krf = 0, kcf = 0, vrf = 0, vcf = 0, lse2 = 0, delta = 0, clean = 0, chunk = 0, csr_off = 0, csr_t = 0,
          seg_off = 0, partial = 0, total = 0;
 };
 
@@ -71,22 +71,13 @@ Layout make_layout(const Shape& s, bool bwd) {
   const size_t BG = (size_t)s.Z * s.G;
   const size_t kbytes = BG * s.Tp() * s.dk * s.esz();
   const size_t vbytes = BG * s.Tp() * s.dv * s.esz();
-  if (s.br == kSelection) {  // fragment-native operands only
-    L.krf = take(kbytes);
-    if (bwd) {
-      L.kcf = take(kbytes);
-      L.vrf = take(vbytes);
-    } else {
-      L.vcf = take(vbytes);
-    }
+  // fragment-native operands (every MFMA fragment one contiguous 1 KB run)
+  L.krf = take(kbytes);
+  if (bwd) {
+    L.kcf = take(kbytes);
+    L.vrf = take(vbytes);
   } else {
-    L.kt = take(kbytes);
-    if (bwd) {
-      L.kn = take(kbytes);
-      L.vn = take(vbytes);
-    } else {
-      L.vt = take(vbytes);
-    }
+    L.vcf = take(vbytes);
   }
   if (bwd) {
     L.lse2 = take((size_t)s.Z * s.H * s.Tq * 4);
@@ -194,15 +185,13 @@ int run_fwd(const Shape& s, const FwdIO& io, float scale, int window, const int3
   a.causal = causal;
   const bool sel = s.br == kSelection;
   auto opt = [&](size_t off, bool use) -> void* { return use ? at<char>(ws, off) : nullptr; };
-  a.kt = opt(L.kt, !sel);
-  a.vt = opt(L.vt, !sel);
-  a.krf = opt(L.krf, sel);
-  a.vcf = opt(L.vcf, sel);
+  a.krf = at<char>(ws, L.krf);
+  a.vcf = at<char>(ws, L.vcf);
 
-  launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp,
-                const_cast<void*>(a.kt), nullptr, const_cast<void*>(a.krf), nullptr, st);
+  launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp, nullptr,
+                nullptr, const_cast<void*>(a.krf), nullptr, st);
   launch_repack(s.dtype, io.V, io.sv[0], io.sv[1], io.sv[2], io.sv[3], s.Z, s.G, s.Tkv, s.dv, a.Tp, nullptr,
-                const_cast<void*>(a.vt), nullptr, const_cast<void*>(a.vcf), st);
+                nullptr, nullptr, const_cast<void*>(a.vcf), st);
   if (s.br == kSelection) {
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
                      s.Tkv, fallback, causal, at<int>(ws, L.clean), nullptr, s.nblk(), st);
@@ -279,22 +268,19 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.causal = causal;
   const bool sel = s.br == kSelection;
   auto opt = [&](size_t off, bool use) -> void* { return use ? at<char>(ws, off) : nullptr; };
-  a.kt = opt(L.kt, !sel);
-  a.kn = opt(L.kn, !sel);
-  a.vn = opt(L.vn, !sel);
-  a.krf = opt(L.krf, sel);
-  a.kcf = opt(L.kcf, sel);
-  a.vrf = opt(L.vrf, sel);
+  a.krf = at<char>(ws, L.krf);
+  a.kcf = at<char>(ws, L.kcf);
+  a.vrf = at<char>(ws, L.vrf);
   a.lse2 = at<float>(ws, L.lse2);
   a.delta = at<float>(ws, L.delta);
   a.items_per_bg = s.items_per_bg();
   a.partial = at<float>(ws, L.partial);
 
   launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp,
-                const_cast<void*>(a.kt), const_cast<void*>(a.kn), const_cast<void*>(a.krf),
+                nullptr, nullptr, const_cast<void*>(a.krf),
                 const_cast<void*>(a.kcf), st);
   launch_repack(s.dtype, io.V, io.sv[0], io.sv[1], io.sv[2], io.sv[3], s.Z, s.G, s.Tkv, s.dv, a.Tp,
-                const_cast<void*>(a.vn), nullptr, const_cast<void*>(a.vrf), nullptr, st);
+                nullptr, nullptr, const_cast<void*>(a.vrf), nullptr, st);
   launch_bwd_rowstats(s.dtype, a, s.dv, st);
   if (s.br == kSelection) {
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,

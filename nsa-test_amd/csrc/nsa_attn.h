@@ -12,8 +12,8 @@ enum DType : int { kF32 = 0, kBF16 = 1 };
 constexpr int kFwdNSub = 2;
 constexpr int kFwdWaves = 8;
 constexpr int kFwdCols = kFwdWaves * kFwdNSub * 16;
-constexpr int kDqNSub = 1;
-constexpr int kDqCols = 4 * kDqNSub * 16;
+constexpr int kDqWaves = 8;
+constexpr int kDqCols = kDqWaves * 16;
 // Distinct selection blocks a row's union bitmap can hold.
 constexpr int kSelMaxBlocks = 4096;
 // Query rows staged per step of the dK/dV kernels.
@@ -25,13 +25,9 @@ struct AttnArgs {
   // queries [B,H,Tq,DK], unit stride on the feature axis
   const void* q;
   int64_t sq_b, sq_h, sq_t;
-  // group K/V re-packed by the prep kernel (compact, Tp rows, zero padded):
-  //   kt [B,G,Tp,DK]  kn [B,G,DK,Tp]  vt [B,G,DV,Tp]  vn [B,G,Tp,DV]
-  const void* kt;
-  const void* kn;
-  const void* vt;
-  const void* vn;
-  // fragment-native copies (selection kernels): K rowfrag / colfrag, V rowfrag / colfrag
+  // group K/V re-packed by the prep kernel (Tp rows, zero padded) in fragment-native
+  // layouts: every 16-byte MFMA fragment of a wave is one contiguous 1 KB run
+  //   krf K rowfrag, kcf K colfrag (K^T), vrf V rowfrag, vcf V colfrag (V^T)
   const void* krf;
   const void* kcf;
   const void* vrf;

@@ -169,22 +169,13 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   const int kw0 = key0 + wave * 16;
   const int mykey = kw0 + c16;
   uint4 kf[NKC], vf[NVC];
-  if constexpr (BR == kSelection) {  // fragment-native copies
+  {  // fragment-native copies: one coalesced 1 KB load per fragment
     const S* krf = reinterpret_cast<const S*>(a.krf) + (int64_t)bg * a.Tp * DK;
     const S* vrf = reinterpret_cast<const S*>(a.vrf) + (int64_t)bg * a.Tp * DV;
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc) kf[kc] = ld_rowfrag<T>(krf, kw0 >> 4, kc, DK, lane);
 #pragma unroll
     for (int kc = 0; kc < NVC; ++kc) vf[kc] = ld_rowfrag<T>(vrf, kw0 >> 4, kc, DV, lane);
-  } else {
-    const S* kt = reinterpret_cast<const S*>(a.kt) + (int64_t)bg * a.Tp * DK;
-    const S* vn = reinterpret_cast<const S*>(a.vn) + (int64_t)bg * a.Tp * DV;
-#pragma unroll
-    for (int kc = 0; kc < NKC; ++kc)
-      kf[kc] = *reinterpret_cast<const uint4*>(kt + (int64_t)mykey * DK + kc * KC + g4 * EPF);
-#pragma unroll
-    for (int kc = 0; kc < NVC; ++kc)
-      vf[kc] = *reinterpret_cast<const uint4*>(vn + (int64_t)mykey * DV + kc * KC + g4 * EPF);
   }
   int mybe = 0x7fffffff, wave_be_min = 0x7fffffff, wave_be_max = 0x7fffffff;
   if (BR == kCompression) {

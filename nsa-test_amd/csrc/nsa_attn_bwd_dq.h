@@ -17,33 +17,45 @@
 namespace nsa {
 
 // ============================== dQ (query-major) ===============================
+// Workgroup = kDqWaves waves x 16 query columns.  The operands of a 64-key tile --
+// K rowfrags (S^T = K Q^T), V rowfrags (dP^T = V dO^T) and K^T colfrags
+// (dQ^T += K^T dS^T) -- are copied global -> LDS by direct-to-LDS loads from the
+// fragment-native krf / vrf / kcf layouts, one 1 KB MFMA fragment per instruction, into a
+// double buffer when two fit 72 KB (else one stage, so that two workgroups share a CU),
+// and every fragment read is a conflict-free 16-byte-per-lane LDS read.
+template <typename T, int DK, int DV>
+struct DqTile {
+  static constexpr int KC = Elem<T>::kKChunk;
+  static constexpr int CK = CFrag<T>::kKeys;
+  static constexpr int NKF = 4 * (DK / KC);           // K rowfrags (ks, kc)
+  static constexpr int NVF = 4 * (DV / KC);           // V rowfrags (ks, kc)
+  static constexpr int NTF = (64 / CK) * (DK / 16);   // K^T colfrags (kc2, j)
+  static constexpr int NF = NKF + NVF + NTF;
+  static constexpr int BYTES = NF * 1024;
+  static constexpr int NBUF = 2 * BYTES <= 72 * 1024 ? 2 : 1;  // bf16 192/128: one 64 KB stage, two workgroups per CU
+};
+
 template <typename T, int DK, int DV, int BR>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
+__global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) {
   static_assert(BR == kSliding || BR == kCompression, "selection uses attn_sel_dq_kernel");
   using S = typename Store<T>::type;
+  using TL = DqTile<T, DK, DV>;
   constexpr int EPF = Elem<T>::kPerFrag;
   constexpr int KC = Elem<T>::kKChunk;
   constexpr int NKC = DK / KC;
   constexpr int NVC = DV / KC;
-  constexpr int KP = DK + EPF;
-  constexpr int NP = 64 + EPF;
-  constexpr int VP = DV + EPF;
   constexpr int CK = CFrag<T>::kKeys;
   constexpr int CT = CK / 16;
-  // bf16 reads the K^T operand from the K rows with the LDS transpose load; fp32 stages
-  // a K^T copy from the kn layout
-  constexpr bool kTr = sizeof(S) == 2;
+  constexpr int NW = kDqWaves;
   static_assert(DK % KC == 0 && DV % KC == 0, "head dims");
 
-  __shared__ __attribute__((aligned(16))) S Ks[64 * KP];                 // K rows   [key][d]
-  __shared__ __attribute__((aligned(16))) S KnS[kTr ? 8 : DK * NP];      // K^T      [d][key]
-  __shared__ __attribute__((aligned(16))) S Vns[64 * VP];                // V rows   [key][dv]
-  __shared__ int s_be[64];
+  extern __shared__ __attribute__((aligned(16))) uint4 dq_lds[];  // [NBUF][NF][64]
+  __shared__ int s_be[2][64];
   __shared__ int s_misc[4];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4;
   const int c16 = lane & 15;
   const int bg = blockIdx.y;
@@ -56,9 +68,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
   const int t_last = min(a.Tq - 1, (col_base + kDqCols - 1) / hpg);
   const float scale2 = a.scale * kLog2e;
 
-  const S* kt = reinterpret_cast<const S*>(a.kt) + (int64_t)bg * a.Tp * DK;
-  const S* kn = reinterpret_cast<const S*>(a.kn) + (int64_t)bg * DK * a.Tp;
-  const S* vn = reinterpret_cast<const S*>(a.vn) + (int64_t)bg * a.Tp * DV;
+  const S* krf = reinterpret_cast<const S*>(a.krf) + (int64_t)bg * a.Tp * DK;
+  const S* kcf = reinterpret_cast<const S*>(a.kcf) + (int64_t)bg * DK * a.Tp;
+  const S* vrf = reinterpret_cast<const S*>(a.vrf) + (int64_t)bg * a.Tp * DV;
 
   // one 16-column subtile per wave
   const int f0 = col_base + wave * 16;
@@ -100,74 +112,62 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     if (tid == 0) s_misc[0] = 0;
     __syncthreads();
     int mx = 0;
-    for (int i = tid; i < a.Tkv; i += 256)
+    for (int i = tid; i < a.Tkv; i += blockDim.x)
       if (a.block_ends[i] <= t_last) mx = i + 1;
     if (mx) atomicMax(&s_misc[0], mx);
     __syncthreads();
     ntiles = (s_misc[0] + 63) / 64;
   }
 
-  // ---- tile operands, loaded into registers one tile ahead ----
-  constexpr int NKP = (64 * (DK / EPF) + 255) / 256;
-  constexpr int NNP = kTr ? 1 : (DK * (64 / EPF) + 255) / 256;
-  constexpr int NVP = (64 * (DV / EPF) + 255) / 256;
-  u32x4 pk[NKP], pn[NNP], pv[NVP];
-  int pbe = 0x7fffffff;
-  auto tile_key0 = [&](int it) -> int { return BR == kSliding ? key_lo + it * 64 : it * 64; };
-  auto load_tile = [&](int key0) {
-#pragma unroll
-    for (int j = 0; j < NKP; ++j) {
-      const int c = min(tid + 256 * j, 64 * (DK / EPF) - 1);
-      pk[j] = *reinterpret_cast<const u32x4*>(kt + (int64_t)(key0 + c / (DK / EPF)) * DK + (c % (DK / EPF)) * EPF);
-    }
-    if constexpr (!kTr) {
-#pragma unroll
-      for (int j = 0; j < NNP; ++j) {
-        const int c = min(tid + 256 * j, DK * (64 / EPF) - 1);
-        pn[j] = *reinterpret_cast<const u32x4*>(kn + (int64_t)(c / (64 / EPF)) * a.Tp + key0 + (c % (64 / EPF)) * EPF);
+  // ---- the direct-to-LDS copy of one tile: wave w copies fragments w, w + NW, ... ----
+  auto copy_tile = [&](int key0, int buf) __attribute__((always_inline)) {
+    uint4* dst = dq_lds + buf * TL::NF * 64;
+    for (int fr = wave; fr < TL::NF; fr += NW) {
+      const S* src;
+      if (fr < TL::NKF) {  // K rowfrag (16-key group (key0 >> 4) + ks, feature chunk kc)
+        const int ks = fr / NKC, kc = fr % NKC;
+        src = krf + ((((int64_t)(key0 >> 4) + ks) * NKC + kc) * 64 + lane) * EPF;
+      } else if (fr < TL::NKF + TL::NVF) {  // V rowfrag
+        const int v = fr - TL::NKF, ks = v / NVC, kc = v % NVC;
+        src = vrf + ((((int64_t)(key0 >> 4) + ks) * NVC + kc) * 64 + lane) * EPF;
+      } else {  // K^T colfrag (key chunk key0 / CK + kc2, feature group j)
+        const int v = fr - TL::NKF - TL::NVF, kc2 = v / (DK / 16), j = v % (DK / 16);
+        src = kcf + ((((int64_t)(key0 / CK) + kc2) * (DK / 16) + j) * 64 + lane) * EPF;
       }
+      copy16_to_lds(src, dst + fr * 64);
     }
-#pragma unroll
-    for (int j = 0; j < NVP; ++j) {
-      const int c = min(tid + 256 * j, 64 * (DV / EPF) - 1);
-      pv[j] = *reinterpret_cast<const u32x4*>(vn + (int64_t)(key0 + c / (DV / EPF)) * DV + (c % (DV / EPF)) * EPF);
-    }
+  };
+  auto tile_key0 = [&](int it) -> int { return BR == kSliding ? key_lo + it * 64 : it * 64; };
+  int pbe = 0x7fffffff;
+  auto load_be = [&](int key0) {
     if (BR == kCompression && tid < 64) {
       const int key = key0 + tid;
       pbe = key < a.Tkv ? a.block_ends[key] : 0x7fffffff;
     }
   };
-  if (ntiles > 0) load_tile(tile_key0(0));
+  if (ntiles > 0) {
+    copy_tile(tile_key0(0), 0);
+    load_be(tile_key0(0));
+  }
 
   for (int it = 0; it < ntiles; ++it) {
     const int key0 = tile_key0(it);
-#pragma unroll
-    for (int j = 0; j < NKP; ++j) {
-      const int c = tid + 256 * j;
-      if ((64 * (DK / EPF)) % 256 == 0 || c < 64 * (DK / EPF))
-        *reinterpret_cast<u32x4*>(&Ks[(c / (DK / EPF)) * KP + (c % (DK / EPF)) * EPF]) = pk[j];
+    const int buf = TL::NBUF == 2 ? (it & 1) : 0;
+    if (BR == kCompression && tid < 64) s_be[it & 1][tid] = pbe;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile it have landed
+    __syncthreads();                // every wave's have; tile it-1 is no longer read
+    if (TL::NBUF == 2 && it + 1 < ntiles) {
+      copy_tile(tile_key0(it + 1), buf ^ 1);
+      load_be(tile_key0(it + 1));
     }
-    if constexpr (!kTr) {
-#pragma unroll
-      for (int j = 0; j < NNP; ++j) {
-        const int c = tid + 256 * j;
-        if ((DK * (64 / EPF)) % 256 == 0 || c < DK * (64 / EPF))
-          *reinterpret_cast<u32x4*>(&KnS[(c / (64 / EPF)) * NP + (c % (64 / EPF)) * EPF]) = pn[j];
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NVP; ++j) {
-      const int c = tid + 256 * j;
-      if ((64 * (DV / EPF)) % 256 == 0 || c < 64 * (DV / EPF))
-        *reinterpret_cast<u32x4*>(&Vns[(c / (DV / EPF)) * VP + (c % (DV / EPF)) * EPF]) = pv[j];
-    }
-    if (BR == kCompression && tid < 64) s_be[tid] = pbe;
-    __syncthreads();
-    if (it + 1 < ntiles) load_tile(tile_key0(it + 1));
+    const uint4* kb = dq_lds + buf * TL::NF * 64;
+    const uint4* vb = kb + TL::NKF * 64;
+    const uint4* tb = vb + TL::NVF * 64;
+    const int* sbe = s_be[it & 1];
 
     int be_max = 0;
     if (BR == kCompression) {
-      be_max = s_be[lane];
+      be_max = sbe[lane];
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) be_max = max(be_max, __shfl_xor(be_max, o));
     }
@@ -180,12 +180,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
     for (int ks = 0; ks < 4; ++ks) {
       st[ks] = zero4();
       dp[ks] = zero4();
-      const S* krow = &Ks[(ks * 16 + c16) * KP];
-      const S* vrow = &Vns[(ks * 16 + c16) * VP];
 #pragma unroll
-      for (int kc = 0; kc < NKC; ++kc) st[ks] = Mma<T>::run(st[ks], frag_std<T>(krow + kc * KC, g4), qf[kc]);
+      for (int kc = 0; kc < NKC; ++kc) st[ks] = Mma<T>::run(st[ks], kb[(ks * NKC + kc) * 64 + lane], qf[kc]);
 #pragma unroll
-      for (int kc = 0; kc < NVC; ++kc) dp[ks] = Mma<T>::run(dp[ks], frag_std<T>(vrow + kc * KC, g4), dof[kc]);
+      for (int kc = 0; kc < NVC; ++kc) dp[ks] = Mma<T>::run(dp[ks], vb[(ks * NVC + kc) * 64 + lane], dof[kc]);
     }
     bool all_visible = false;
     const bool full = f0 + 16 <= ncols;
@@ -204,7 +202,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
           const int key = key0 + ks * 16 + 4 * g4 + i;
           bool ok;
           if (BR == kSliding) ok = (uint32_t)(key - kmin_s) < kspan_s;
-          else ok = colv & (s_be[ks * 16 + 4 * g4 + i] <= colt);
+          else ok = colv & (sbe[ks * 16 + 4 * g4 + i] <= colt);
           p = ok ? fast_exp2(st[ks][i] * scale2 - l2) : 0.f;
         }
         st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
@@ -213,23 +211,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
 #pragma unroll
     for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
       const uint4 sf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
-      if constexpr (kTr) {
-        // A = K^T (16 features x the 32 keys of the C-permuted CFrag order) from the
-        // K rows: lanes 4*rho+q of group g4 address key kc2*32 + 4*g4 + rho (then +16)
-        const int r0 = kc2 * CK + 4 * g4 + (c16 >> 2);
-        const int f4 = 4 * (c16 & 3);
 #pragma unroll
-        for (int j = 0; j < DK / 16; ++j)
-          dqa[j] = Mma<T>::run(dqa[j], ld_tr_pair(&Ks[r0 * KP + j * 16 + f4], 16 * KP), sf);
-      } else {
-#pragma unroll
-        for (int j = 0; j < DK / 16; ++j) {
-          const uint4 kf = frag_cperm<T>(&KnS[(j * 16 + c16) * NP + kc2 * CK], g4);
-          dqa[j] = Mma<T>::run(dqa[j], kf, sf);
-        }
-      }
+      for (int j = 0; j < DK / 16; ++j) dqa[j] = Mma<T>::run(dqa[j], tb[(kc2 * (DK / 16) + j) * 64 + lane], sf);
     }
-    __syncthreads();
+    if (TL::NBUF == 1 && it + 1 < ntiles) {  // single buffer: refill once every wave is done
+      __syncthreads();
+      copy_tile(tile_key0(it + 1), 0);
+      load_be(tile_key0(it + 1));
+    }
   }
 
   if (colv) {
@@ -241,11 +230,15 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a) {
 
 template <typename T, int DK, int DV, int BR>
 void launch_attn_bwd_dq(const AttnArgs& a, hipStream_t s) {
-  dim3 grid((a.Tq * a.hpg + kDqCols - 1) / kDqCols, a.B * a.G);
   if constexpr (BR == kSelection) {
     launch_attn_sel_dq<T, DK, DV>(a, s);  // per-wave selection kernel
   } else {
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, DK, DV, BR>), grid, dim3(256), 0, s, a);
+    using TL = DqTile<T, DK, DV>;
+    const size_t lds = (size_t)TL::NBUF * TL::BYTES;
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_kernel<T, DK, DV, BR>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    dim3 grid((a.Tq * a.hpg + kDqCols - 1) / kDqCols, a.B * a.G);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<T, DK, DV, BR>), grid, dim3(64 * kDqWaves), lds, s, a);
   }
 }
 

@@ -26,9 +26,10 @@
 namespace nsa {
 
 // Workgroup = kFwdWaves waves x kFwdNSub subtiles x 16 columns.  The K and V^T
-// fragments of a 64-key tile are copied global -> LDS by the direct-to-LDS loads
-// (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l), one 1 KB MFMA
-// fragment per instruction, into a double buffer: the copy of tile i+1 is in flight
+// fragments of a 64-key tile are copied from the fragment-native krf / vcf layouts
+// (each fragment one contiguous 1 KB run) to LDS by the direct-to-LDS loads
+// (global_load_lds_dwordx4: lane l's 16 bytes land at base + 16 l), one fragment per
+// instruction, into a double buffer: the copy of tile i+1 is in flight
 // while tile i is used, no register holds staging data, and each fragment read is a
 // conflict-free 16-byte-per-lane LDS read.  Every fragment read feeds the products of
 // all NSUB subtiles of the wave.
@@ -76,8 +77,8 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   const float scale2 = a.scale * kLog2e;
 
   const S* qbase = reinterpret_cast<const S*>(a.q);
-  const S* kt = reinterpret_cast<const S*>(a.kt) + (int64_t)bg * a.Tp * DK;
-  const S* vt = reinterpret_cast<const S*>(a.vt) + (int64_t)bg * DV * a.Tp;
+  const S* krf = reinterpret_cast<const S*>(a.krf) + (int64_t)bg * a.Tp * DK;
+  const S* vcf = reinterpret_cast<const S*>(a.vcf) + (int64_t)bg * DV * a.Tp;
 
   // ---- per-lane column state -------------------------------------------------
   int colt[NSUB];
@@ -135,12 +136,12 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
     uint4* dst = fwd_lds + buf * (FT::NKF + FT::NVF) * 64;
     for (int f = wave; f < FT::NKF + FT::NVF; f += NW) {
       const S* src;
-      if (f < FT::NKF) {  // K rows of keys key0 + 16 ks + c16, features kc*KC + g4*EPF..
+      if (f < FT::NKF) {  // K rowfrag (16-key group (key0 >> 4) + ks, feature chunk kc)
         const int ks = f / NKC, kc = f % NKC;
-        src = kt + (int64_t)(key0 + ks * 16 + c16) * DK + kc * KC + g4 * EPF;
-      } else {  // V^T rows j*16 + c16, keys of C-permuted chunk kc2 (group g4)
+        src = krf + ((((int64_t)(key0 >> 4) + ks) * NKC + kc) * 64 + lane) * EPF;
+      } else {  // V^T colfrag (key chunk key0 / CK + kc2, feature group j)
         const int v = f - FT::NKF, kc2 = v / (DV / 16), j = v % (DV / 16);
-        src = vt + (int64_t)(j * 16 + c16) * a.Tp + key0 + kc2 * CK + g4 * EPF;
+        src = vcf + ((((int64_t)(key0 / CK) + kc2) * (DV / 16) + j) * 64 + lane) * EPF;
       }
       copy16_to_lds(src, dst + f * 64);
     }
