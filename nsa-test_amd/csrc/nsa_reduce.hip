@@ -57,22 +57,56 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
   }
   if (count == 0 || key0 >= key_hi) return;
   const float* base = a.partial + (int64_t)bg * a.items_per_bg * 64 * width;
-  // blockIdx.z splits the tile's 64 x width elements over kReduceSplit workgroups
-  const int per = (64 * width + kReduceSplit - 1) / kReduceSplit;
-  const int e_end = min(64 * width, (int)(blockIdx.z + 1) * per);
-  for (int e = blockIdx.z * per + threadIdx.x; e < e_end; e += 256) {
+  // blockIdx.z splits the tile's 64 x width elements (in groups of four: DK and DV are
+  // multiples of four, so a group never straddles dK / dV) over kReduceSplit workgroups
+  const int n4 = 64 * width / 4;
+  const int per = (n4 + kReduceSplit - 1) / kReduceSplit;
+  const int e_end = min(n4, (int)(blockIdx.z + 1) * per);
+  for (int e4 = blockIdx.z * per + threadIdx.x; e4 < e_end; e4 += 256) {
+    const int e = 4 * e4;
     const int kl = e / width, col = e % width;
     const int key = key0 + kl;
     if (key >= key_hi) continue;
-    float sum = 0.f;
-    for (int k = 0; k < count; ++k) sum += base[(int64_t)(first + k * step) * 64 * width + e];
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < count; ++k) {
+      const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)(first + k * step) * 64 * width + e);
+      sum.x += v.x;
+      sum.y += v.y;
+      sum.z += v.z;
+      sum.w += v.w;
+    }
+    const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
+    S* p;
+    int64_t sd;
     if (col < DK) {
-      S* p = reinterpret_cast<S*>(a.dk) + b * a.sdk_b + grp * a.sdk_g + (int64_t)key * a.sdk_t + (int64_t)col * a.sdk_d;
-      *p = Elem<T>::from_f32(Elem<T>::to_f32(*p) + sum);
+      p = reinterpret_cast<S*>(a.dk) + b * a.sdk_b + grp * a.sdk_g + (int64_t)key * a.sdk_t + (int64_t)col * a.sdk_d;
+      sd = a.sdk_d;
     } else {
-      S* p = reinterpret_cast<S*>(a.dv) + b * a.sdv_b + grp * a.sdv_g + (int64_t)key * a.sdv_t +
-             (int64_t)(col - DK) * a.sdv_d;
-      *p = Elem<T>::from_f32(Elem<T>::to_f32(*p) + sum);
+      p = reinterpret_cast<S*>(a.dv) + b * a.sdv_b + grp * a.sdv_g + (int64_t)key * a.sdv_t +
+          (int64_t)(col - DK) * a.sdv_d;
+      sd = a.sdv_d;
+    }
+    if (sd == 1 && (reinterpret_cast<uintptr_t>(p) % (4 * sizeof(S))) == 0) {  // one vector read-modify-write
+      if constexpr (sizeof(S) == 2) {
+        uint2 w = *reinterpret_cast<const uint2*>(p);
+        const float x0 = bf16_bits_to_f32((uint16_t)(w.x & 0xffffu)) + sv[0];
+        const float x1 = bf16_bits_to_f32((uint16_t)(w.x >> 16)) + sv[1];
+        const float x2 = bf16_bits_to_f32((uint16_t)(w.y & 0xffffu)) + sv[2];
+        const float x3 = bf16_bits_to_f32((uint16_t)(w.y >> 16)) + sv[3];
+        w.x = (uint32_t)f32_to_bf16_bits(x0) | ((uint32_t)f32_to_bf16_bits(x1) << 16);
+        w.y = (uint32_t)f32_to_bf16_bits(x2) | ((uint32_t)f32_to_bf16_bits(x3) << 16);
+        *reinterpret_cast<uint2*>(p) = w;
+      } else {
+        float4 w = *reinterpret_cast<const float4*>(p);
+        w.x += sv[0];
+        w.y += sv[1];
+        w.z += sv[2];
+        w.w += sv[3];
+        *reinterpret_cast<float4*>(p) = w;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) p[u * sd] = Elem<T>::from_f32(Elem<T>::to_f32(p[u * sd]) + sv[u]);
     }
   }
 }

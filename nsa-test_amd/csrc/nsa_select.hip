@@ -15,62 +15,58 @@
 namespace nsa {
 
 constexpr int kCleanMaxSlots = 64;
-constexpr int kCsrChunk = 256;  // timesteps per fill chunk
+constexpr int kCsrChunk = 64;  // timesteps per fill chunk
 
 __global__ void zero_ints_kernel(int* p, int64_t n) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i < n) p[i] = 0;
 }
 
+// SEG lanes (a power of two >= the slot count) clean one row: lane s holds slot s.  The
+// kept value of a lane is its slot unless it is invalid or repeats an earlier slot;
+// its position in the ascending output is the number of kept values below it.
+template <int SEG>
 __global__ __launch_bounds__(256) void sel_clean_kernel(const void* idx, int idx_is64, int64_t si_b, int64_t si_g,
                                                         int64_t si_t, int64_t si_n, int G, int Tq, int n_in,
                                                         int nslots, int lprime, int nblk, int fallback, int causal,
                                                         int* clean, int* chunk_cnt, int nchunks) {
-  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t nrows = (int64_t)gridDim.y * Tq;  // gridDim.y = B*G
+  constexpr int kNone = 0x7fffffff;
+  const int t = (int)(((int64_t)blockIdx.x * 256 + threadIdx.x) / SEG);
+  const int s = threadIdx.x % SEG;
   const int bg = blockIdx.y;
-  if (row >= Tq) return;
-  (void)nrows;
-  const int t = (int)row;
   const int b = bg / G, g = bg % G;
-  int vals[kCleanMaxSlots];
-  int n = 0;
-  bool any_valid = false;
-  for (int s = 0; s < n_in; ++s) {
+  const bool row_ok = t < Tq;  // lanes past the last row take part in the shuffles only
+  int raw = -1;
+  if (row_ok && s < n_in) {
     const int64_t off = b * si_b + g * si_g + (int64_t)t * si_t + s * si_n;
     const int64_t v = idx_is64 ? reinterpret_cast<const int64_t*>(idx)[off] : reinterpret_cast<const int*>(idx)[off];
-    if (v >= 0) any_valid = true;
-    vals[s] = (int)(v < -1 ? -1 : (v > 0x3fffffff ? 0x3fffffff : v));
+    raw = (int)(v < -1 ? -1 : (v > 0x3fffffff ? 0x3fffffff : v));
   }
-  if (fallback && !any_valid && n_in > 0) {
-    for (int s = 0; s < n_in; ++s) vals[s] = t / lprime;
+  int any_valid = raw >= 0;
+#pragma unroll
+  for (int o = 1; o < SEG; o <<= 1) any_valid |= __shfl_xor(any_valid, o, SEG);
+  if (fallback && !any_valid && s < n_in) raw = t / lprime;
+  const bool ok = row_ok && raw >= 0 && raw < nblk && !(causal && (int64_t)raw * lprime > t);
+  const int key = ok ? raw : kNone;
+  bool dup = false;
+#pragma unroll
+  for (int j = 0; j < SEG; ++j) {
+    const int o = __shfl(key, j, SEG);
+    dup |= j < s && o == key;
   }
-  // filter + insertion sort with de-duplication
-  int out[kCleanMaxSlots];
-  for (int s = 0; s < n_in; ++s) {
-    const int v = vals[s];
-    if (v < 0 || v >= nblk) continue;
-    if (causal && (int64_t)v * lprime > t) continue;
-    int p = n;
-    bool dup = false;
-    while (p > 0 && out[p - 1] >= v) {
-      if (out[p - 1] == v) {
-        dup = true;
-        break;
-      }
-      --p;
-    }
-    if (dup) continue;
-    for (int q = n; q > p; --q) out[q] = out[q - 1];
-    out[p] = v;
-    ++n;
+  const bool keep = key != kNone && !dup;
+  int pos = 0, nkept = 0;
+#pragma unroll
+  for (int j = 0; j < SEG; ++j) {
+    const int o = __shfl(keep ? key : kNone, j, SEG);
+    pos += o < key;
+    nkept += o != kNone;
   }
+  if (!row_ok) return;
   int* dst = clean + ((int64_t)bg * Tq + t) * nslots;
-  for (int s = 0; s < nslots; ++s) dst[s] = s < n ? out[s] : -1;
-  if (chunk_cnt) {
-    int* cc = chunk_cnt + ((int64_t)bg * nchunks + t / kCsrChunk) * nblk;
-    for (int s = 0; s < n; ++s) atomicAdd(&cc[out[s]], 1);
-  }
+  if (keep) dst[pos] = key;
+  for (int q = nkept + s; q < nslots; q += SEG) dst[q] = -1;
+  if (chunk_cnt && keep) atomicAdd(&chunk_cnt[((int64_t)bg * nchunks + t / kCsrChunk) * nblk + key], 1);
 }
 
 // Per (b,g): chunk_cnt[c][j] -> exclusive running base over chunks (+ block offset);
@@ -150,9 +146,18 @@ void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g,
     hipLaunchKernelGGL(zero_ints_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, chunk_cnt, n);
   }
   (void)Tkv;
-  dim3 grid((Tq + 255) / 256, B * G);
-  hipLaunchKernelGGL(sel_clean_kernel, grid, dim3(256), 0, st, idx, idx_is64, si_b, si_g, si_t, si_n, G, Tq, n_in,
-                     nslots, lprime, nblk, fallback, causal, clean, chunk_cnt, nchunks);
+  // lanes per row: the smallest power of two >= the slot count (at most kCleanMaxSlots)
+  const int seg = n_in <= 16 ? 16 : n_in <= 32 ? 32 : 64;
+  dim3 grid((unsigned)(((int64_t)Tq * seg + 255) / 256), B * G);
+  if (seg == 16)
+    hipLaunchKernelGGL(sel_clean_kernel<16>, grid, dim3(256), 0, st, idx, idx_is64, si_b, si_g, si_t, si_n, G, Tq,
+                       n_in, nslots, lprime, nblk, fallback, causal, clean, chunk_cnt, nchunks);
+  else if (seg == 32)
+    hipLaunchKernelGGL(sel_clean_kernel<32>, grid, dim3(256), 0, st, idx, idx_is64, si_b, si_g, si_t, si_n, G, Tq,
+                       n_in, nslots, lprime, nblk, fallback, causal, clean, chunk_cnt, nchunks);
+  else
+    hipLaunchKernelGGL(sel_clean_kernel<64>, grid, dim3(256), 0, st, idx, idx_is64, si_b, si_g, si_t, si_n, G, Tq,
+                       n_in, nslots, lprime, nblk, fallback, causal, clean, chunk_cnt, nchunks);
 }
 
 void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int nslots, int nblk, int* csr_off,
