@@ -64,8 +64,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr int NKC = DK / KC;
   constexpr int NVC = DV / KC;
   constexpr int RC = sizeof(S) == 4 ? 16 : kRowChunk;  // fp32 stages half the rows (LDS)
-  constexpr int QP = DK + EPF;
-  constexpr int OP = DV + EPF;
+  // bf16 row pitches of 32 B more than the row (416 B at dk = 192, 288 B at dv = 128):
+  // an odd multiple of 32 B modulo 256 B, so the 16 rows one transposed read touches
+  // fall on distinct banks in each half-wave
+  constexpr int QP = DK + (sizeof(S) == 2 ? 16 : EPF);
+  constexpr int OP = DV + (sizeof(S) == 2 ? 16 : EPF);
   constexpr int RP = RC + (sizeof(S) == 2 ? 8 : 4);  // 16-byte aligned transposed rows
   constexpr int CK = CFrag<T>::kKeys;
   constexpr int CT = CK / 16;
