@@ -50,7 +50,7 @@ struct Shape {
   // dK/dV work items per (b, g): key tiles x query segments
   int items_per_bg() const {
     if (br == kSelection) return nsubblk() * (nblk() + (int)(((int64_t)Tq * nslots + kSegT - 1) / kSegT));
-    return ((Tkv + 63) / 64) * dkdv_nseg(br, Tq, window);
+    return ((Tkv + dkdv_keys(br) - 1) / dkdv_keys(br)) * dkdv_nseg(br, Tq, window);
   }
 };
 
@@ -92,7 +92,7 @@ Layout make_layout(const Shape& s, bool bwd) {
       L.csr_t = take(BG * s.Tq * s.nslots * 4);
     }
   }
-  if (bwd) L.partial = take(BG * s.items_per_bg() * 64 * (size_t)(s.dk + s.dv) * 4);
+  if (bwd) L.partial = take(BG * s.items_per_bg() * dkdv_keys(s.br) * (size_t)(s.dk + s.dv) * 4);
   L.total = off;
   return L;
 }

@@ -1,6 +1,7 @@
 // dK / dV for the three NSA branches on gfx950 (key-major).
 //
-// A work item owns 64 keys of one (batch, KV group) -- 16 keys per wave, held in
+// A work item owns 128 keys (selection: one 64-key sub-block) of one (batch, KV
+// group) -- 16 keys per wave, held in
 // registers as MFMA B operands -- and one segment of the query rows that can see them
 // (rows are (timestep, head) pairs of the group).  The rows are walked in chunks of
 // RC rows, staged in LDS row-major (operand of S = Q K^T and dP = dO V^T) and
@@ -12,7 +13,7 @@
 // two rows at once, and the transposed row pitch (RC + 4) keeps those writes free of
 // bank conflicts.
 //
-// Every item writes its fp32 dK/dV partial for its 64 keys; a reduce kernel sums the
+// Every item writes its fp32 dK/dV partial for its keys; a reduce kernel sums the
 // segments of each key tile in a fixed order and accumulates into the caller's dK/dV.
 // No floating-point atomics: the result is bit-reproducible.
 //
@@ -24,10 +25,14 @@
 
 namespace nsa {
 
+// keys per dK/dV work item: the l'-aligned 64-key sub-blocks of selection, 128 keys
+// (8 waves) otherwise, so each staged query row serves twice as many keys
+__host__ __device__ constexpr int dkdv_keys(int br) { return br == kSelection ? 64 : 128; }
+
 // number of query segments per key tile (sliding and compression items)
 __host__ __device__ inline int dkdv_nseg(int br, int Tq, int window) {
   if (br == kSliding) {
-    const int span = min(window + 63, Tq + 63);
+    const int span = min(window + dkdv_keys(kSliding) - 1, Tq + dkdv_keys(kSliding) - 1);
     return (span + kSegT - 1) / kSegT;
   }
   return (Tq + kSegT - 1) / kSegT;
@@ -57,8 +62,10 @@ template <> struct PairT<float> {
 };
 
 template <typename T, int DK, int DV, int BR>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
+__global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   using S = typename Store<T>::type;
+  constexpr int KEYS = dkdv_keys(BR);  // keys of the item, 16 per wave
+  constexpr int NT = 4 * KEYS;         // threads
   constexpr int EPF = Elem<T>::kPerFrag;
   constexpr int KC = Elem<T>::kKChunk;
   constexpr int NKC = DK / KC;
@@ -82,8 +89,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   constexpr bool kTr = sizeof(S) == 2;
   constexpr int QPCS = kTr ? RC * (DK / EPF) : QPC;  // staged pieces per chunk
   constexpr int OPCS = kTr ? RC * (DV / EPF) : OPC;
-  constexpr int NQ = (QPCS + 255) / 256;
-  constexpr int NO = (OPCS + 255) / 256;
+  constexpr int NQ = (QPCS + NT - 1) / NT;
+  constexpr int NO = (OPCS + NT - 1) / NT;
   static_assert(RC % CK == 0, "row chunk");
   // bf16: two LDS stages (one barrier per chunk; about 44 KB at dk = 192, so two
   // workgroups still share a CU).  fp32 keeps one stage (its transposed copy doubles
@@ -97,7 +104,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   __shared__ int s_t[NB][RC];
   __shared__ float s_l2[NB][RC];
   __shared__ float s_dl[NB][RC];
-  __shared__ int s_be[64];
+  __shared__ int s_be[KEYS];
   __shared__ int s_tl[kSegT];  // selection: the item's query timesteps
 
   const int tid = threadIdx.x;
@@ -120,21 +127,23 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   if (BR == kSliding) {
     const int nseg = dkdv_nseg(kSliding, a.Tq, a.window);
     const int tile = item / nseg, seg = item % nseg;
-    key0 = tile * 64;
+    key0 = tile * KEYS;
     const int t_lo = key0 + seg * kSegT;
-    const int t_hi = min(a.Tq, min(key0 + (seg + 1) * kSegT, key0 + 63 + a.window));
+    const int t_hi = min(a.Tq, min(key0 + (seg + 1) * kSegT, key0 + KEYS - 1 + a.window));
     f_lo = t_lo * hpg;
     f_hi = t_hi > t_lo ? t_hi * hpg : f_lo;
   } else if (BR == kCompression) {
     const int nseg = dkdv_nseg(kCompression, a.Tq, 0);
     const int tile = item / nseg, seg = item % nseg;
-    key0 = tile * 64;
-    if (tid < 64) {
+    key0 = tile * KEYS;
+    if (tid < KEYS) {
       const int key = key0 + tid;
       s_be[tid] = key < a.Tkv ? a.block_ends[key] : 0x7fffffff;
     }
     __syncthreads();
-    int be_min = s_be[lane];
+    int be_min = 0x7fffffff;
+#pragma unroll
+    for (int c = 0; c < KEYS / 64; ++c) be_min = min(be_min, s_be[c * 64 + lane]);
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) be_min = min(be_min, __shfl_xor(be_min, o));
     const int t_lo = max(seg * kSegT, max(be_min, 0));
@@ -164,7 +173,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
     if (key0 >= blk_hi) return;  // sub-tile past the sequence end: no partial is read
     e_base = e_lo;
     const int* tlist = a.csr_t + (int64_t)bg * a.Tq * a.nslots;
-    for (int i = tid; i < e_hi - e_lo; i += 256) s_tl[i] = tlist[e_lo + i];
+    for (int i = tid; i < e_hi - e_lo; i += NT) s_tl[i] = tlist[e_lo + i];
     __syncthreads();
   }
 
@@ -223,26 +232,26 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
     const int h = grp * hpg + hdiv.mod(fe);
     return *reinterpret_cast<const uint4*>(base + e + ((int64_t)h * sh + (int64_t)t * st));
   };
-  // the piece index c = tid + 256 j is in range for every thread when the piece count
-  // is a multiple of 256 (known at compile time: no branch)
-  auto in_q = [&](int c) { return QPCS % 256 == 0 || c < QPCS; };
-  auto in_o = [&](int c) { return OPCS % 256 == 0 || c < OPCS; };
+  // the piece index c = tid + NT j is in range for every thread when the piece count
+  // is a multiple of NT (known at compile time: no branch)
+  auto in_q = [&](int c) { return QPCS % NT == 0 || c < QPCS; };
+  auto in_o = [&](int c) { return OPCS % NT == 0 || c < OPCS; };
   auto load_chunk = [&](int fc) {
     if constexpr (kTr) {
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
-        const int c = tid + 256 * j;
+        const int c = tid + NT * j;
         if (in_q(c)) pq[j][0] = load_row(fc + c / (DK / EPF), qbase, sqh, sqt, (c % (DK / EPF)) * EPF);
       }
 #pragma unroll
       for (int j = 0; j < NO; ++j) {
-        const int c = tid + 256 * j;
+        const int c = tid + NT * j;
         if (in_o(c)) po[j][0] = load_row(fc + c / (DV / EPF), obase, soh, sot, (c % (DV / EPF)) * EPF);
       }
     } else {
 #pragma unroll
     for (int j = 0; j < NQ; ++j) {
-      const int c = tid + 256 * j;
+      const int c = tid + NT * j;
       if (c < QPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
@@ -252,7 +261,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < NO; ++j) {
-      const int c = tid + 256 * j;
+      const int c = tid + NT * j;
       if (c < OPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
@@ -279,20 +288,20 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
     if constexpr (kTr) {
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
-        const int c = tid + 256 * j;
+        const int c = tid + NT * j;
         if (in_q(c))
           *reinterpret_cast<uint4*>(&Qs[buf][(c / (DK / EPF)) * QP + (c % (DK / EPF)) * EPF]) = pq[j][0];
       }
 #pragma unroll
       for (int j = 0; j < NO; ++j) {
-        const int c = tid + 256 * j;
+        const int c = tid + NT * j;
         if (in_o(c))
           *reinterpret_cast<uint4*>(&Os[buf][(c / (DV / EPF)) * OP + (c % (DV / EPF)) * EPF]) = po[j][0];
       }
     } else {
 #pragma unroll
     for (int j = 0; j < NQ; ++j) {
-      const int c = tid + 256 * j;
+      const int c = tid + NT * j;
       if (c < QPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
@@ -303,7 +312,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int j = 0; j < NO; ++j) {
-      const int c = tid + 256 * j;
+      const int c = tid + NT * j;
       if (c < OPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
@@ -408,7 +417,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
   }
 
   // ---- write this item's partial: lane holds dK^T[d = 16j + 4*g4 + i][key = mykey] ----
-  float* pp = a.partial + ((int64_t)bg * a.items_per_bg + item) * 64 * (DK + DV) +
+  float* pp = a.partial + ((int64_t)bg * a.items_per_bg + item) * KEYS * (DK + DV) +
               (int64_t)(wave * 16 + c16) * (DK + DV);
 #pragma unroll
   for (int j = 0; j < DK / 16; ++j) {
@@ -424,7 +433,7 @@ template <typename T, int DK, int DV, int BR>
 void launch_attn_bwd_dkdv(const AttnArgs& a, hipStream_t s) {
   if (a.items_per_bg <= 0) return;
   dim3 grid(a.items_per_bg, a.B * a.G);
-  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, DK, DV, BR>), grid, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((attn_bwd_dkdv_kernel<T, DK, DV, BR>), grid, dim3(4 * dkdv_keys(BR)), 0, s, a);
 }
 
 }  // namespace nsa

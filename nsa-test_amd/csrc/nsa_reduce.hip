@@ -1,7 +1,7 @@
 // dK/dV partial reduction and the dtype dispatch of the attention kernels.
 //
 // Compression and selection split a key tile's queries over several work items;
-// each item wrote fp32 partials [64 keys][DK + DV].  One workgroup per key tile
+// each item wrote fp32 partials [keys][DK + DV].  One workgroup per key tile
 // sums them in item order (fixed, so the result is reproducible) and accumulates
 // into the caller's dK / dV with their strides.
 #include "nsa_attn.h"
@@ -38,9 +38,10 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
   const int b = bg / a.G, grp = bg % a.G;
   const int width = DK + DV;
   int key0, key_hi, first, count, step;
+  const int keys = dkdv_keys(br);  // keys of one item's partial
   if (br != kSelection) {
     const int nseg = dkdv_nseg(br, a.Tq, a.window);
-    key0 = blockIdx.x * 64;
+    key0 = blockIdx.x * keys;
     key_hi = a.Tkv;
     first = blockIdx.x * nseg;
     count = nseg;
@@ -56,10 +57,10 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
     step = nsubblk;
   }
   if (count == 0 || key0 >= key_hi) return;
-  const float* base = a.partial + (int64_t)bg * a.items_per_bg * 64 * width;
-  // blockIdx.z splits the tile's 64 x width elements (in groups of four: DK and DV are
+  const float* base = a.partial + (int64_t)bg * a.items_per_bg * keys * width;
+  // blockIdx.z splits the tile's keys x width elements (in groups of four: DK and DV are
   // multiples of four, so a group never straddles dK / dV) over kReduceSplit workgroups
-  const int n4 = 64 * width / 4;
+  const int n4 = keys * width / 4;
   const int per = (n4 + kReduceSplit - 1) / kReduceSplit;
   const int e_end = min(n4, (int)(blockIdx.z + 1) * per);
   for (int e4 = blockIdx.z * per + threadIdx.x; e4 < e_end; e4 += 256) {
@@ -69,7 +70,7 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
     if (key >= key_hi) continue;
     float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int k = 0; k < count; ++k) {
-      const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)(first + k * step) * 64 * width + e);
+      const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)(first + k * step) * keys * width + e);
       sum.x += v.x;
       sum.y += v.y;
       sum.z += v.z;
@@ -113,7 +114,7 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
 
 void launch_partial_reduce(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st) {
   int tiles;
-  if (br != kSelection) tiles = (a.Tkv + 63) / 64;
+  if (br != kSelection) tiles = (a.Tkv + dkdv_keys(br) - 1) / dkdv_keys(br);
   else tiles = a.nblk * ((a.lprime + 63) / 64);
   if (tiles <= 0) return;
   dim3 grid(tiles, a.B * a.G, kReduceSplit);
