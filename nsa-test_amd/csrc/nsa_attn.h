@@ -9,10 +9,10 @@ enum Branch : int { kSliding = 0, kCompression = 1, kSelection = 2 };
 enum DType : int { kF32 = 0, kBF16 = 1 };
 
 // Columns handled by one forward / dQ workgroup (4 waves x NSUB x 16).
-constexpr int kFwdNSub = 2;
-constexpr int kFwdWaves = 8;
+constexpr int kFwdNSub = 1;
+constexpr int kFwdWaves = 16;
 constexpr int kFwdCols = kFwdWaves * kFwdNSub * 16;
-constexpr int kDqWaves = 8;
+constexpr int kDqWaves = 12;
 constexpr int kDqCols = kDqWaves * 16;
 // Distinct selection blocks a row's union bitmap can hold.
 constexpr int kSelMaxBlocks = 4096;

@@ -21,7 +21,7 @@ namespace nsa {
 // K rowfrags (S^T = K Q^T), V rowfrags (dP^T = V dO^T) and K^T colfrags
 // (dQ^T += K^T dS^T) -- are copied global -> LDS by direct-to-LDS loads from the
 // fragment-native krf / vrf / kcf layouts, one 1 KB MFMA fragment per instruction, into a
-// double buffer when two fit 72 KB (else one stage, so that two workgroups share a CU),
+// double buffer when two fit 136 KB (one workgroup of 12 waves per CU, three waves per SIMD),
 // and every fragment read is a conflict-free 16-byte-per-lane LDS read.
 template <typename T, int DK, int DV>
 struct DqTile {
@@ -32,7 +32,7 @@ struct DqTile {
   static constexpr int NTF = (64 / CK) * (DK / 16);   // K^T colfrags (kc2, j)
   static constexpr int NF = NKF + NVF + NTF;
   static constexpr int BYTES = NF * 1024;
-  static constexpr int NBUF = 2 * BYTES <= 72 * 1024 ? 2 : 1;  // bf16 192/128: one 64 KB stage, two workgroups per CU
+  static constexpr int NBUF = 2 * BYTES <= 136 * 1024 ? 2 : 1;
 };
 
 template <typename T, int DK, int DV, int BR>

@@ -40,9 +40,9 @@ struct FwdTile {
   static constexpr int NKF = 4 * (DK / KC);          // K fragments (ks, kc)
   static constexpr int NVF = (64 / CK) * (DV / 16);  // V^T fragments (kc2, j)
   static constexpr int BYTES = (NKF + NVF) * 1024;
-  // three stages when they fit: the next tile's S^T is issued before this tile's
-  // softmax (software pipelining), so two tiles are read while a third is copied
-  static constexpr int NBUF = 3 * BYTES <= 136 * 1024 ? 3 : 2 * BYTES <= 96 * 1024 ? 2 : 1;
+  // a double buffer (one WG of 16 waves per CU, four waves per SIMD); one stage when
+  // two do not fit
+  static constexpr int NBUF = 2 * BYTES <= 96 * 1024 ? 2 : 1;
 };
 
 template <typename T, int DK, int DV, int BR>
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   static_assert(DK % KC == 0 && DV % 16 == 0, "head dims");
 
   extern __shared__ __attribute__((aligned(16))) uint4 fwd_lds[];  // [NBUF][NKF + NVF][64]
-  __shared__ int s_be[3][64];
+  __shared__ int s_be[2][64];
   __shared__ int s_misc[4];
 
   const int tid = threadIdx.x;
@@ -257,58 +257,25 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   };
 
   f32x4 st[NSUB][4];
-  if constexpr (FT::NBUF == 3) {
-    // stage i % 3 holds tile i; at step i the copy of tile i+2 is in flight while the
-    // products of tile i+1's S^T overlap the softmax of tile i
-    if (ntiles > 0) {
-      copy_tile(tile_key0(0), 0);
-      load_be(tile_key0(0));
-      if (ntiles > 1) copy_tile(tile_key0(1), 1);
-      if (BR == kCompression && tid < 64) s_be[0][tid] = pbe;
-      if (ntiles > 1) load_be(tile_key0(1));
-      __builtin_amdgcn_s_waitcnt(0);
+  if (ntiles > 0) {
+    copy_tile(tile_key0(0), 0);
+    load_be(tile_key0(0));
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = FT::NBUF == 2 ? (it & 1) : 0;
+    if (BR == kCompression && tid < 64) s_be[it & 1][tid] = pbe;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile it have landed
+    __syncthreads();                // every wave's have; tile it-1 is no longer read
+    if (FT::NBUF == 2 && it + 1 < ntiles) {
+      copy_tile(tile_key0(it + 1), buf ^ 1);
+      load_be(tile_key0(it + 1));
+    }
+    compute_s(st, buf);
+    softmax_pv(st, tile_key0(it), buf, s_be[it & 1]);
+    if (FT::NBUF == 1 && it + 1 < ntiles) {  // single buffer: refill once every wave is done
       __syncthreads();
-      compute_s(st, 0);
-    }
-    for (int it = 0; it < ntiles; ++it) {
-      if (it + 1 < ntiles) {
-        if (BR == kCompression && tid < 64) s_be[(it + 1) % 3][tid] = pbe;
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile it+1 have landed
-        __syncthreads();                // every wave's have; tile it-1 is no longer read
-        if (it + 2 < ntiles) {
-          copy_tile(tile_key0(it + 2), (it + 2) % 3);
-          load_be(tile_key0(it + 2));
-        }
-      }
-      f32x4 cur[NSUB][4];
-#pragma unroll
-      for (int s = 0; s < NSUB; ++s)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) cur[s][ks] = st[s][ks];
-      if (it + 1 < ntiles) compute_s(st, (it + 1) % 3);
-      softmax_pv(cur, tile_key0(it), it % 3, s_be[it % 3]);
-    }
-  } else {
-    if (ntiles > 0) {
-      copy_tile(tile_key0(0), 0);
-      load_be(tile_key0(0));
-    }
-    for (int it = 0; it < ntiles; ++it) {
-      const int buf = FT::NBUF == 2 ? (it & 1) : 0;
-      if (BR == kCompression && tid < 64) s_be[it & 1][tid] = pbe;
-      __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile it have landed
-      __syncthreads();                // every wave's have; tile it-1 is no longer read
-      if (FT::NBUF == 2 && it + 1 < ntiles) {
-        copy_tile(tile_key0(it + 1), buf ^ 1);
-        load_be(tile_key0(it + 1));
-      }
-      compute_s(st, buf);
-      softmax_pv(st, tile_key0(it), buf, s_be[it & 1]);
-      if (FT::NBUF == 1 && it + 1 < ntiles) {  // single buffer: refill once every wave is done
-        __syncthreads();
-        copy_tile(tile_key0(it + 1), 0);
-        load_be(tile_key0(it + 1));
-      }
+      copy_tile(tile_key0(it + 1), 0);
+      load_be(tile_key0(it + 1));
     }
   }
 
