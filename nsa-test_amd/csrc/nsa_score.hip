@@ -3,8 +3,8 @@
 // with fixed blocks, in two kernels:
 //   score_logits_kernel  the Eq. 8 logits of every (row, visible compressed block) as a
 //                        register-tiled fp32 GEMM into the caller's workspace;
-//   score_rows_kernel    softmax, Eq. 9, Eq. 10 and the top-n, one workgroup per
-//                        (batch, group, TT consecutive timesteps).
+//   score_rows_kernel    softmax, Eq. 9, Eq. 10 and the top-n, one wave per
+//                        (batch, group, timestep).
 // Besides the workspace only the n indices per (b, g, t) are written (and, when the
 // caller asks for them, the p_cmp / p_slc score tensors the reference module returns
 // in attn_info).
@@ -73,7 +73,6 @@ struct ScoreArgs {
   float scale;
   int a, s, nsel, lprime, n, include_fixed;
   int ncs;  // logit row stride: NB rounded up to 64
-  int TT;   // rows kernel: timesteps per workgroup
 };
 
 constexpr int kMaxRows = 64;    // heads per group
@@ -220,76 +219,102 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
 }
 
 // ------------------------------------------------------------------ rows ----
-// One workgroup of kRowsWaves waves per (batch, group, TT consecutive timesteps); wave
-// w takes the rows r = w, w + kRowsWaves, ... of its R = TT * hpg rows.  A row lives
-// in registers: lane L holds the blocks 256 s + 4 L + u (s < NQ, u < 4), one 16-byte
-// piece per s (a coalesced 1 KB load per wave).  Per row:
+// One wave per (batch, group, timestep): a workgroup of NW waves takes NW consecutive
+// timesteps, and after the block ends are staged in LDS no wave waits for another.  A
+// wave walks its timestep's hpg rows in head order, each row in registers -- lane L
+// holds the blocks 256 s + 4 L + u (s < NQ, u < 4), one 16-byte piece per s (a
+// coalesced 1 KB load per wave), the next row's pieces loaded while the current one
+// is processed:
 //   1. invisible blocks set to -inf (logits are finite; exp32 maps -inf to 0), max;
 //   2. e = exp32(s - max), lane partials over s then u, xor butterfly;
 //   3. p = e * (1 / sum);
-//   4. Eq. 9 into the row's own workspace slot (its logits are consumed).  For the
-//      (a, s) = (2, 4) remap output j = 64 s + L reads blocks 4j..4j+4: the lane's own
-//      piece s plus the first block of the next lane's piece; other remaps go through
-//      a wave-private LDS copy of the row.
-// After a barrier, Eq. 10 adds each timestep's rows in head order from the workspace
-// (the waves of a workgroup share one CU, so its stores are visible after the
-// barrier), and one wave per timestep runs the top-n.
-// Only blocks below ncomp(t_last) are read; the logits kernel computed every block
-// visible to these rows (its tile's last timestep is not earlier than each row's own).
+//   4. Eq. 9: for the (a, s) = (2, 4) remap output j = 64 s + L reads blocks 4j..4j+4,
+//      the lane's own piece s plus the first block of the next lane's piece; other
+//      remaps go through a wave-private LDS copy of the row;
+//   5. Eq. 10: the row's Eq. 9 scores added to the timestep's running sums (heads in
+//      order), in registers for the (2, 4) remap (output j of lane j % 64), in a
+//      wave-private LDS row otherwise.
+// Then the top-n of the timestep from those sums.  Blocks past the last one visible
+// at t are not read (the logits kernel computed every visible block, and block 0).
 constexpr int kRowsWaves = 8;
 
 template <int NQ, bool FAST9>
 __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a) {
+  // LDS: sbe [NQ * 256] block ends (INT_MAX past NB); generic remap only, per wave:
+  // row copy [NQ * 256] + Eq. 10 sums [nsel rounded up to 4]
   extern __shared__ float lds[];
-  constexpr int NW = kRowsWaves;
-  constexpr int NBUF = FAST9 ? 0 : NQ * 256;  // floats of a wave's row copy
+  constexpr bool kPrefetch = NQ <= 8;  // registers for the next row's pieces
   const int tid = threadIdx.x, lane = tid & 63;
+  const int NW = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bg = blockIdx.y, b = bg / a.G, g = bg % a.G;
-  const int t0 = blockIdx.x * a.TT;
-  const int TT = min(a.TT, a.T - t0);
-  const int hpg = a.hpg;
-  const int R = TT * hpg;  // r = tt * hpg + hh
-  const int NB = a.NB, nsel = a.nsel, ncs = a.ncs;
-
-  float* wb = lds + wave * NBUF;                           // [NW][NBUF] (generic Eq. 9 only)
-  float* agg = lds + NW * NBUF;                            // [TT][nsel]
-  int* sbe = reinterpret_cast<int*>(agg + a.TT * nsel);    // [NQ*256] block ends (INT_MAX past ncomp)
-  int* topl = sbe + NQ * 256;                              // [TT][64] top-k per timestep
-  __shared__ int s_nc;
-
-  const int ncomp = score_ncomp(a, t0 + TT - 1, &s_nc);
-  const int ncol = ((ncomp + 63) >> 6) * 64;  // blocks the logits kernel computed
-  for (int i = tid; i < NQ * 256; i += blockDim.x) sbe[i] = i < ncomp ? a.block_ends[i] : 0x7fffffff;
+  const int NB = a.NB, nsel = a.nsel, ncs = a.ncs, hpg = a.hpg;
+  int* sbe = reinterpret_cast<int*>(lds);
+  for (int i = tid; i < NQ * 256; i += blockDim.x) sbe[i] = i < NB ? a.block_ends[i] : 0x7fffffff;
   __syncthreads();
-  float* lgb = a.lg + ((int64_t)bg * a.T * hpg + (int64_t)t0 * hpg) * ncs;
-  const float4 ninf4 = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+  const int t = blockIdx.x * NW + wave;
+  if (t >= a.T) return;  // whole wave; no barrier follows
+  const int nsel4 = (nsel + 3) & ~3;
+  float* wb = lds + NQ * 256 + wave * (NQ * 256 + nsel4);  // generic remap only
+  float* wag = wb + NQ * 256;
 
-  for (int r = wave; r < R; r += NW) {
-    const int t = t0 + r / hpg, h = g * hpg + r % hpg;
-    float* row = lgb + (int64_t)r * ncs;
-    float v[NQ][4];
+  int vis_hi = 0;  // 1 + the largest block index visible at t (0: none)
 #pragma unroll
-    for (int s = 0; s < NQ; ++s) {
-      const int col = 256 * s + 4 * lane;
-      const float4 x = col < ncol ? *reinterpret_cast<const float4*>(row + col) : ninf4;
-      v[s][0] = x.x;
-      v[s][1] = x.y;
-      v[s][2] = x.z;
-      v[s][3] = x.w;
-    }
+  for (int s = 0; s < NQ; ++s) {
+    const int4 be = *reinterpret_cast<const int4*>(sbe + 256 * s + 4 * lane);
+    const int i = 256 * s + 4 * lane;
+    if (be.x <= t) vis_hi = i + 1;
+    if (be.y <= t) vis_hi = i + 2;
+    if (be.z <= t) vis_hi = i + 3;
+    if (be.w <= t) vis_hi = i + 4;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) vis_hi = max(vis_hi, __shfl_xor(vis_hi, off));
+  vis_hi = __builtin_amdgcn_readfirstlane(vis_hi);  // uniform: branches on it stay scalar
+  // columns read (block 0 always: the no-visible-block rule scores it)
+  const int ncol = max(64, ((vis_hi + 63) >> 6) * 64);
+  // pieces holding a read column; the others hold only invisible blocks, whose p is an
+  // exact 0 that adds nothing to the sum, Eq. 9 or Eq. 10 (wave-uniform skip)
+  const int nact = (ncol + 255) >> 8;
+  const float* lgb = a.lg + ((int64_t)bg * a.T + t) * hpg * ncs;
+
+  float agg[FAST9 ? NQ : 1];
+#pragma unroll
+  for (int s = 0; s < (FAST9 ? NQ : 1); ++s) agg[s] = 0.0f;
+  if constexpr (!FAST9)
+    for (int j = lane; j < nsel; j += 64) wag[j] = 0.0f;
+  float4 cur[NQ], nxt[kPrefetch ? NQ : 1];
+  // one 16-byte load per active piece; columns past ncol (not computed for this row,
+  // or past the row when ncs is not a multiple of 256) are read from a clamped address
+  // and are masked below (their blocks are invisible at t)
+  auto load_row = [&](float4* v, int hh) __attribute__((always_inline)) {
+    const float* row = lgb + (int64_t)hh * ncs;
+#pragma unroll
+    for (int s = 0; s < NQ; ++s)
+      if (s < nact) v[s] = *reinterpret_cast<const float4*>(row + min(256 * s + 4 * lane, ncs - 4));
+  };
+  load_row(cur, 0);
+  for (int hh = 0; hh < hpg; ++hh) {
+    if constexpr (kPrefetch)
+      if (hh + 1 < hpg) load_row(nxt, hh + 1);
+    const int h = g * hpg + hh;
+    float v[NQ][4];
     float mx = -INFINITY;
 #pragma unroll
     for (int s = 0; s < NQ; ++s) {
+      if (s >= nact) {
+        v[s][0] = v[s][1] = v[s][2] = v[s][3] = 0.0f;
+        continue;
+      }
       const int4 be = *reinterpret_cast<const int4*>(sbe + 256 * s + 4 * lane);
-      v[s][0] = be.x <= t ? v[s][0] : -INFINITY;
-      v[s][1] = be.y <= t ? v[s][1] : -INFINITY;
-      v[s][2] = be.z <= t ? v[s][2] : -INFINITY;
-      v[s][3] = be.w <= t ? v[s][3] : -INFINITY;
+      v[s][0] = be.x <= t ? cur[s].x : -INFINITY;
+      v[s][1] = be.y <= t ? cur[s].y : -INFINITY;
+      v[s][2] = be.z <= t ? cur[s].z : -INFINITY;
+      v[s][3] = be.w <= t ? cur[s].w : -INFINITY;
       mx = fmaxf(mx, fmaxf(fmaxf(v[s][0], v[s][1]), fmaxf(v[s][2], v[s][3])));
     }
-    if (__ballot(mx != -INFINITY) == 0ull) {  // no visible block: block 0 is scored
-      mx = row[0];
+    if (vis_hi == 0) {  // no visible block (wave-uniform): block 0 is scored
+      mx = __shfl(cur[0].x, 0);
       if (lane == 0) v[0][0] = mx;
     }
 #pragma unroll
@@ -297,18 +322,20 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
     float part = 0.0f;
 #pragma unroll
     for (int s = 0; s < NQ; ++s)
+      if (s < nact)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        v[s][u] = exp32(v[s][u] - mx);
-        part += v[s][u];
-      }
+        for (int u = 0; u < 4; ++u) {
+          v[s][u] = exp32(v[s][u] - mx);
+          part += v[s][u];
+        }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) part = part + __shfl_xor(part, off);
     const float rs = 1.0f / part;
 #pragma unroll
     for (int s = 0; s < NQ; ++s)
+      if (s < nact)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[s][u] *= rs;  // blocks past ncomp: p = 0 exactly
+        for (int u = 0; u < 4; ++u) v[s][u] *= rs;  // invisible blocks: p = 0 exactly
     if (a.p_cmp) {
       float* pc = a.p_cmp + (((int64_t)b * a.H + h) * a.T + t) * NB;
 #pragma unroll
@@ -319,21 +346,24 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
           if (i < NB) pc[i] = v[s][u];
         }
     }
-    // Eq. 9 in the reference's (m, n) order, starting from 0; blocks past ncomp (or
-    // NB) add an exact +0
+    // Eq. 9 in the reference's (m, n) order, starting from 0; invisible blocks (and
+    // blocks past NB) add an exact +0
     float* psl = a.p_slc ? a.p_slc + (((int64_t)b * a.H + h) * a.T + t) * nsel : nullptr;
     if constexpr (FAST9) {  // (m, n) -> 4j + {0, 1, 1, 2, 2, 3, 3, 4}
 #pragma unroll
       for (int s = 0; s < NQ; ++s) {
+        if (s >= nact) {  // Eq. 9 scores of exact 0
+          const int j = 64 * s + lane;
+          if (psl && j < nsel) psl[j] = 0.0f;
+          continue;
+        }
         float nb = __shfl_down(v[s][0], 1);
         const float nb63 = s + 1 < NQ ? __shfl(v[s + 1 < NQ ? s + 1 : s][0], 0) : 0.0f;
         if (lane == 63) nb = nb63;
         const float s9 = (((((((0.0f + v[s][0]) + v[s][1]) + v[s][1]) + v[s][2]) + v[s][2]) + v[s][3]) + v[s][3]) + nb;
+        agg[s] += s9;
         const int j = 64 * s + lane;
-        if (j < nsel) {
-          row[j] = s9;
-          if (psl) psl[j] = s9;
-        }
+        if (psl && j < nsel) psl[j] = s9;
       }
     } else {
 #pragma unroll
@@ -345,81 +375,97 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
         for (int m = 0; m < a.s; ++m)
           for (int nn = 0; nn < a.a; ++nn) {
             const int ci = a.s * j + m + nn;
-            if (ci < ncomp) s9 += wb[ci];
+            if (ci < NB) s9 += wb[ci];
           }
-        row[j] = s9;
+        wag[j] += s9;
         if (psl) psl[j] = s9;
       }
-      wave_lds_sync();  // the copy is rewritten for the wave's next row
+      wave_lds_sync();  // the copy is rewritten for the next row
+    }
+    if constexpr (kPrefetch) {
+#pragma unroll
+      for (int s = 0; s < NQ; ++s) cur[s] = nxt[s];
+    } else if (hh + 1 < hpg) {
+      load_row(cur, hh + 1);
     }
   }
-  __syncthreads();
 
-  // Eq. 10: heads added in head order
-  for (int x = tid; x < TT * nsel; x += blockDim.x) {
-    const int tt = x / nsel, j = x % nsel;
-    const float* src = lgb + (int64_t)tt * hpg * ncs + j;
-    float ag = 0.0f;
-    for (int hh = 0; hh < hpg; ++hh) ag += src[(int64_t)hh * ncs];
-    agg[tt * nsel + j] = ag;
-  }
-  __syncthreads();
-
-  // ---- top-n (one wave per timestep) ----
+  // ---- top-n: the kk largest sums, equal sums lower index first ----
   const int kk = min(a.n, nsel);
   const int nc = a.include_fixed ? 3 : 0;
-  for (int tt = wave; tt < TT; tt += NW) {
-    const int t = t0 + tt;
-    float* ag = agg + tt * nsel;
-    int* tl = topl + tt * 64;
-    for (int rk = 0; rk < kk; ++rk) {
-      float bv = -INFINITY;
-      int bi = 0x7fffffff;
-      for (int j = lane; j < nsel; j += 64) {
-        const float v = ag[j];
-        if (v > bv || (v == bv && j < bi)) {
-          bv = v;
+  if constexpr (FAST9) {
+#pragma unroll
+    for (int s = 0; s < NQ; ++s)
+      if (64 * s + lane >= nsel) agg[s] = -INFINITY;  // past nsel: never taken (kk <= nsel)
+  }
+  int top0 = -1, top1 = -1;  // lane c holds candidate c (top0) and c + 64 (top1)
+  for (int rk = 0; rk < kk; ++rk) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    if constexpr (FAST9) {
+#pragma unroll
+      for (int s = 0; s < NQ; ++s) {
+        const int j = 64 * s + lane;
+        if (agg[s] > bv || (agg[s] == bv && j < bi)) {
+          bv = agg[s];
           bi = j;
         }
       }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off);
-        const int oi = __shfl_xor(bi, off);
-        if (ov > bv || (ov == bv && oi < bi)) {
-          bv = ov;
-          bi = oi;
+    } else {
+      for (int j = lane; j < nsel; j += 64) {
+        const float x = wag[j];
+        if (x > bv || (x == bv && j < bi)) {
+          bv = x;
+          bi = j;
         }
       }
-      if (lane == 0) {
-        tl[rk] = bi;
-        ag[bi] = -INFINITY;  // taken
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off);
+      const int oi = __shfl_xor(bi, off);
+      if (ov > bv || (ov == bv && oi < bi)) {
+        bv = ov;
+        bi = oi;
       }
+    }
+    // bi is wave-uniform: its owner marks it taken
+    if constexpr (FAST9) {
+#pragma unroll
+      for (int s = 0; s < NQ; ++s)
+        if (64 * s + lane == bi) agg[s] = -INFINITY;
+    } else {
+      if (lane == (bi & 63)) wag[bi] = -INFINITY;
       wave_lds_sync();
     }
-    // candidates: fixed [0, max(0,(t-l')/l'), t/l'] then the top-k.  The top-k are
-    // distinct, so a candidate can only repeat one of the fixed ones before it.
-    const int f1 = t >= a.lprime ? (t - a.lprime) / a.lprime : 0;
-    const int f2 = t / a.lprime;
-    const int ncand = nc + kk;
-    int64_t* o = a.out + b * a.so_b + g * a.so_g + (int64_t)t * a.so_t;
-    int kept = 0;  // candidates kept so far (wave-uniform)
-    for (int c0 = 0; c0 < ncand && kept < a.n; c0 += 64) {
-      const int c = c0 + lane;
-      int v = -1;
-      bool keep = false;
-      if (c < ncand) {
-        v = c < nc ? (c == 0 ? 0 : c == 1 ? f1 : f2) : tl[c - nc];
-        const bool dup = nc > 0 && ((c > 0 && v == 0) || (c > 1 && v == f1) || (c > 2 && v == f2));
-        keep = !dup;
-      }
-      const uint64_t km = __ballot(keep);
-      const int rank = kept + __builtin_popcountll(km & ((1ull << lane) - 1ull));
-      if (keep && rank < a.n) o[(int64_t)rank * a.so_n] = v;
-      kept += __builtin_popcountll(km);
+    const int c = nc + rk;
+    if (lane == (c & 63)) {
+      if (c < 64) top0 = bi;
+      else top1 = bi;
     }
-    for (int u = min(kept, a.n) + lane; u < a.n; u += 64) o[(int64_t)u * a.so_n] = -1;
   }
+  // candidates: fixed [0, max(0,(t-l')/l'), t/l'] then the top-k.  The top-k are
+  // distinct, so a candidate can only repeat one of the fixed ones before it.
+  const int f1 = t >= a.lprime ? (t - a.lprime) / a.lprime : 0;
+  const int f2 = t / a.lprime;
+  const int ncand = nc + kk;  // <= 67 (n <= 64)
+  int64_t* o = a.out + b * a.so_b + g * a.so_g + (int64_t)t * a.so_t;
+  int kept = 0;  // candidates kept so far (wave-uniform)
+  for (int c0 = 0; c0 < ncand && kept < a.n; c0 += 64) {
+    const int c = c0 + lane;
+    int v = -1;
+    bool keep = false;
+    if (c < ncand) {
+      v = c < nc ? (c == 0 ? 0 : c == 1 ? f1 : f2) : (c0 == 0 ? top0 : top1);
+      const bool dup = nc > 0 && ((c > 0 && v == 0) || (c > 1 && v == f1) || (c > 2 && v == f2));
+      keep = !dup;
+    }
+    const uint64_t km = __ballot(keep);
+    const int rank = kept + __builtin_popcountll(km & ((1ull << lane) - 1ull));
+    if (keep && rank < a.n) o[(int64_t)rank * a.so_n] = v;
+    kept += __builtin_popcountll(km);
+  }
+  for (int u = min(kept, a.n) + lane; u < a.n; u += 64) o[(int64_t)u * a.so_n] = -1;
 }
 
 static int score_ncs(int NB) { return NB > 0 ? ((NB + 63) / 64) * 64 : 64; }
@@ -430,35 +476,36 @@ static int score_rows_nq(int ncs) {  // 16-byte pieces per lane: a power of two 
   return nq;
 }
 
-static size_t score_rows_lds(int nq, bool fast9, int TT, int nsel) {
-  return 4 * ((size_t)(fast9 ? 0 : kRowsWaves * nq * 256) + (size_t)TT * nsel + (size_t)nq * 256 + (size_t)TT * 64);
+// LDS of a rows workgroup of nw waves
+static size_t score_rows_lds(int nq, bool fast9, int nw, int nsel) {
+  const size_t per_wave = fast9 ? 0 : (size_t)nq * 256 + (size_t)((nsel + 3) & ~3);
+  return 4 * ((size_t)nq * 256 + nw * per_wave);
 }
 
 template <int NQ, bool FAST9>
-static hipError_t launch_rows_k(const ScoreArgs& a, size_t lds, hipStream_t st) {
+static hipError_t launch_rows_k(const ScoreArgs& a, int nw, size_t lds, hipStream_t st) {
   auto fn = score_rows_kernel<NQ, FAST9>;
   hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
                                      (int)lds);
   if (e != hipSuccess) return e;
-  dim3 grid((a.T + a.TT - 1) / a.TT, a.B * a.G);
-  hipLaunchKernelGGL(fn, grid, dim3(64 * kRowsWaves), lds, st, a);
+  dim3 grid((a.T + nw - 1) / nw, a.B * a.G);
+  hipLaunchKernelGGL(fn, grid, dim3(64 * nw), lds, st, a);
   return hipGetLastError();
 }
 
 template <bool FAST9>
-static hipError_t launch_rows_q(const ScoreArgs& a, int nq, size_t lds, hipStream_t st) {
+static hipError_t launch_rows_q(const ScoreArgs& a, int nq, int nw, size_t lds, hipStream_t st) {
   switch (nq) {
-    case 1: return launch_rows_k<1, FAST9>(a, lds, st);
-    case 2: return launch_rows_k<2, FAST9>(a, lds, st);
-    case 4: return launch_rows_k<4, FAST9>(a, lds, st);
-    case 8: return launch_rows_k<8, FAST9>(a, lds, st);
-    case 16: return launch_rows_k<16, FAST9>(a, lds, st);
+    case 1: return launch_rows_k<1, FAST9>(a, nw, lds, st);
+    case 2: return launch_rows_k<2, FAST9>(a, nw, lds, st);
+    case 4: return launch_rows_k<4, FAST9>(a, nw, lds, st);
+    case 8: return launch_rows_k<8, FAST9>(a, nw, lds, st);
+    case 16: return launch_rows_k<16, FAST9>(a, nw, lds, st);
   }
   return hipErrorInvalidValue;
 }
 
-// Launches the logits GEMM and the rows kernel.  The rows kernel takes as many
-// timesteps as fit 64 rows and the LDS budget (two workgroups per CU preferred).
+// Launches the logits GEMM and the rows kernel (one wave per timestep).
 // Returns 0 on success, 1 when no configuration fits, 2 on a HIP launch error.
 int launch_score_topn(int dtype, ScoreArgs a, hipStream_t st) {
   if (a.NB > kMaxCols || a.hpg > kMaxRows) return 1;
@@ -470,14 +517,13 @@ int launch_score_topn(int dtype, ScoreArgs a, hipStream_t st) {
     else hipLaunchKernelGGL(score_logits_kernel<uint16_t>, grid, dim3(256), 0, st, a);
     if (hipGetLastError() != hipSuccess) return 2;
   }
-  int TT = 1;
-  while (TT * 2 * a.hpg <= kMaxRows && TT * 2 <= a.T) TT *= 2;
   const int nq = score_rows_nq(a.ncs);
   const bool fast9 = a.a == 2 && a.s == 4;
-  const size_t lds = score_rows_lds(nq, fast9, TT, a.nsel);
+  int nw = kRowsWaves;  // fewer waves per workgroup when the generic remap's LDS rows do not fit
+  while (nw > 1 && score_rows_lds(nq, fast9, nw, a.nsel) > 80 * 1024) nw /= 2;
+  const size_t lds = score_rows_lds(nq, fast9, nw, a.nsel);
   if (lds > 156 * 1024) return 1;
-  a.TT = TT;
-  const hipError_t e = fast9 ? launch_rows_q<true>(a, nq, lds, st) : launch_rows_q<false>(a, nq, lds, st);
+  const hipError_t e = fast9 ? launch_rows_q<true>(a, nq, nw, lds, st) : launch_rows_q<false>(a, nq, nw, lds, st);
   return e == hipSuccess ? 0 : 2;
 }
 
