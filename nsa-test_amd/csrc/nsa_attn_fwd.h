@@ -106,10 +106,11 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   }
 
   f32x4 oacc[NSUB][DV / 16];
-  float m2[NSUB], lsum[NSUB];
+  float m2[NSUB], mtrue[NSUB], lsum[NSUB];  // exponent reference, true maximum, sum
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) {
     m2[s] = -INFINITY;
+    mtrue[s] = -INFINITY;
     lsum[s] = 0.f;
 #pragma unroll
     for (int j = 0; j < DV / 16; ++j) oacc[s][j] = zero4();
@@ -193,15 +194,15 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
         all_visible = f0_full[s] && key0 + 63 <= sub_t0[s] && key0 > sub_t1[s] - a.window && key0 + 63 < a.Tkv;
       else if (BR == kCompression)
         all_visible = f0_full[s] && be_max <= sub_t0[s];
+      // the maximum is taken over the raw products (scale2 > 0 commutes with max); the
+      // exponent argument is the rounded product minus the reference (not one fma), so
+      // the column maximum maps to exp2(0) = 1 exactly
       float mx = -INFINITY;
       if (all_visible) {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            st[s][ks][i] *= scale2;
-            mx = fmaxf(mx, st[s][ks][i]);
-          }
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, st[s][ks][i]);
       } else {
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
@@ -211,35 +212,38 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
             bool ok;
             if (BR == kSliding) ok = (uint32_t)(key - kmin_s) < kspan_s;
             else ok = colv[s] & (sbe[ks * 16 + 4 * g4 + i] <= t);
-            const float v = ok ? st[s][ks][i] * scale2 : -INFINITY;
+            const float v = ok ? st[s][ks][i] : -INFINITY;
             st[s][ks][i] = v;
             mx = fmaxf(mx, v);
           }
         }
       }
-      mx = wave_max16(mx);
-      const float mnew = fmaxf(m2[s], mx);
-      const float mref = mnew == -INFINITY ? 0.f : mnew;
+      mx = wave_max16(mx) * scale2;
+      mtrue[s] = fmaxf(mtrue[s], mx);
+      // lazy rescale: the exponent reference m2 moves only when some column's maximum
+      // exceeds it by more than kLazyRescale (p <= 2^kLazyRescale meanwhile); the true
+      // maximum is tracked for M and the final sum is brought to it in the epilogue
+      if (__ballot(mx > m2[s] + kLazyRescale) != 0ull) {
+        const float mnew = fmaxf(m2[s], mtrue[s]);
+        const float alpha = m2[s] == -INFINITY ? 0.f : fast_exp2(m2[s] - mnew);
+        lsum[s] *= alpha;
+#pragma unroll
+        for (int j = 0; j < DV / 16; ++j) oacc[s][j] *= alpha;
+        m2[s] = mnew;
+      }
+      const float nref = m2[s] == -INFINITY ? 0.f : -m2[s];
       float rs = 0.f;
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = fast_exp2(st[s][ks][i] - mref);
+          const float p = fast_exp2(mul_add_rounded(st[s][ks][i], scale2, nref));
           st[s][ks][i] = p;
           rs += p;
         }
       }
       rs = wave_sum16(rs);
-      // rescale the running output only when some column's maximum moved
-      if (__ballot(mnew > m2[s]) != 0ull) {
-        const float alpha = fast_exp2(m2[s] - mref);
-        lsum[s] *= alpha;
-#pragma unroll
-        for (int j = 0; j < DV / 16; ++j) oacc[s][j] *= alpha;
-      }
       lsum[s] += rs;
-      m2[s] = mnew;
 #pragma unroll
       for (int kc2 = 0; kc2 < 64 / CK; ++kc2) pf[s][kc2] = CFrag<T>::pack(st[s][kc2 * CT], st[s][kc2 * CT + CT - 1]);
     }
@@ -285,6 +289,8 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   for (int s = 0; s < NSUB; ++s) {
     if (!colv[s]) continue;
     const float inv = lsum[s] > 0.f ? 1.f / lsum[s] : 0.f;
+    // the sum relative to the true maximum (m2 <= mtrue, equal when both are -inf)
+    if (lsum[s] > 0.f) lsum[s] *= fast_exp2(m2[s] - mtrue[s]);
     S* op = obase + b * a.so_b + (int64_t)colh[s] * a.so_h + (int64_t)colt[s] * a.so_t;
 #pragma unroll
     for (int j = 0; j < DV / 16; ++j) store4<T>(op + j * 16 + 4 * g4, oacc[s][j] * inv);
@@ -293,7 +299,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
         a.L[b * a.sl_b + (int64_t)colh[s] * a.sl_h + (int64_t)colt[s] * a.sl_t] =
             lsum[s] > 0.f ? logf(lsum[s]) : -INFINITY;
       if (a.M)
-        a.M[b * a.sm_b + (int64_t)colh[s] * a.sm_h + (int64_t)colt[s] * a.sm_t] = m2[s] * kLn2;
+        a.M[b * a.sm_b + (int64_t)colh[s] * a.sm_h + (int64_t)colt[s] * a.sm_t] = mtrue[s] * kLn2;
     }
   }
 }

@@ -116,7 +116,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   f32x4 oacc[DV / 16];
 #pragma unroll
   for (int j = 0; j < DV / 16; ++j) oacc[j] = zero4();
-  float m2 = -INFINITY, lsum = 0.f;
+  float m2 = -INFINITY, mtrue = -INFINITY, lsum = 0.f;  // exponent reference, true maximum, sum
   const int nwords = (a.nblk + 31) / 32;
   const bool one_t = w.nt == 1;
 
@@ -193,31 +193,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const bool ok = (uint32_t)(kb + ks * 16 + i) < span;
-        const float v = ok ? st[ks][i] * scale2 : -INFINITY;
+        const float v = ok ? st[ks][i] : -INFINITY;
         st[ks][i] = v;
         mx = fmaxf(mx, v);
       }
-    mx = wave_max16(mx);
-    const float mnew = fmaxf(m2, mx);
-    const float mref = mnew == -INFINITY ? 0.f : mnew;
+    // maximum over the raw products (scale2 > 0; the exponent argument is the rounded
+    // product minus the reference, so the maximum maps to exp2(0) = 1 exactly); lazy rescale of the exponent
+    // reference m2 (moves only when a column maximum exceeds it by kLazyRescale), the
+    // true maximum mtrue kept for M and the epilogue
+    mx = wave_max16(mx) * scale2;
+    mtrue = fmaxf(mtrue, mx);
+    if (__ballot(mx > m2 + kLazyRescale) != 0ull) {
+      const float mnew = fmaxf(m2, mtrue);
+      const float alpha = m2 == -INFINITY ? 0.f : fast_exp2(m2 - mnew);
+      lsum *= alpha;
+#pragma unroll
+      for (int j = 0; j < DV / 16; ++j) oacc[j] *= alpha;
+      m2 = mnew;
+    }
+    const float nref = m2 == -INFINITY ? 0.f : -m2;
     float rs = 0.f;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = fast_exp2(st[ks][i] - mref);
+        const float p = fast_exp2(mul_add_rounded(st[ks][i], scale2, nref));
         st[ks][i] = p;
         rs += p;
       }
-    rs = wave_sum16(rs);
-    if (__ballot(mnew > m2) != 0ull) {
-      const float alpha = fast_exp2(m2 - mref);
-      lsum *= alpha;
-#pragma unroll
-      for (int j = 0; j < DV / 16; ++j) oacc[j] *= alpha;
-    }
-    lsum += rs;
-    m2 = mnew;
+    lsum += wave_sum16(rs);
 #pragma unroll
     for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
       const uint4 pf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
@@ -230,13 +234,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 
   if (colv) {
     const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    if (lsum > 0.f) lsum *= fast_exp2(m2 - mtrue);  // the sum relative to the true maximum
     S* op = reinterpret_cast<S*>(a.o) + b * a.so_b + (int64_t)colh * a.so_h + (int64_t)colt * a.so_t;
 #pragma unroll
     for (int j = 0; j < DV / 16; ++j) store4<T>(op + j * 16 + 4 * g4, oacc[j] * inv);
     if (g4 == 0) {
       if (a.L)
         a.L[b * a.sl_b + (int64_t)colh * a.sl_h + (int64_t)colt * a.sl_t] = lsum > 0.f ? logf(lsum) : -INFINITY;
-      if (a.M) a.M[b * a.sm_b + (int64_t)colh * a.sm_h + (int64_t)colt * a.sm_t] = m2 * kLn2;
+      if (a.M) a.M[b * a.sm_b + (int64_t)colh * a.sm_h + (int64_t)colt * a.sm_t] = mtrue * kLn2;
     }
   }
 }

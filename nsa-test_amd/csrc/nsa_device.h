@@ -24,6 +24,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte register
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
+// forward softmax: the exponent reference moves only when a column maximum exceeds it by
+// more than this (log2 units), so probabilities stay below 2^8 between rescales
+constexpr float kLazyRescale = 8.0f;
 
 struct bf16 {  // storage-only tag type for the template parameter
   uint16_t bits;
@@ -215,6 +218,13 @@ template <> __device__ __forceinline__ void store4<bf16>(uint16_t* p, f32x4 v) {
 // 2^x on the transcendental unit (v_exp_f32); exp2(-inf) = 0.  Inputs here are <= 0,
 // results below the normal range may flush, which the softmax tolerates.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// round(x * y) + r as two rounded operations (never contracted to one fma): with r the
+// negated rounded product of a maximum, that maximum maps to exactly 0
+__device__ __forceinline__ float mul_add_rounded(float x, float y, float r) {
+#pragma clang fp contract(off)
+  return x * y + r;
+}
 
 // n / d and n % d for 0 <= n < 2^31, branch-free: q = (n * m) >> s with
 // l = ceil(log2 d), s = 31 + l, m = ceil(2^s / d).  m < 2^32 because d > 2^(l-1), and the
