@@ -281,7 +281,6 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
                 const_cast<void*>(a.kcf), st);
   launch_repack(s.dtype, io.V, io.sv[0], io.sv[1], io.sv[2], io.sv[3], s.Z, s.G, s.Tkv, s.dv, a.Tp,
                 nullptr, nullptr, const_cast<void*>(a.vrf), nullptr, st);
-  launch_bwd_rowstats(s.dtype, a, s.dv, st);
   if (s.br == kSelection) {
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
                      s.Tkv, fallback, causal, at<int>(ws, L.clean), at<int>(ws, L.chunk), s.nblk(), st);

@@ -93,8 +93,6 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
       dof[kc] = colv ? *reinterpret_cast<const uint4*>(dp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
   }
   const int64_t srow = ((int64_t)b * a.H + colh) * a.Tq + colt;
-  const float l2 = colv ? a.lse2[srow] : INFINITY;
-  const float dl = colv ? a.delta[srow] : 0.f;
   // sliding: the column sees keys [kmin_s, kmin_s + kspan_s) (branch-free test)
   const int kmin_s = max(colt - a.window + 1, 0);
   const uint32_t kspan_s = colv ? (uint32_t)max(0, min(colt, a.Tkv - 1) + 1 - kmin_s) : 0u;
@@ -149,6 +147,9 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
     copy_tile(tile_key0(0), 0);
     load_be(tile_key0(0));
   }
+  // row statistics after the first tile's copies are issued (their O loads overlap them)
+  float l2, dl;
+  dq_row_stats<T, NVC>(a, b, colh, colt, colv, dof, g4, srow, l2, dl);
 
   for (int it = 0; it < ntiles; ++it) {
     const int key0 = tile_key0(it);

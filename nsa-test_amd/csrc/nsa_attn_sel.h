@@ -15,6 +15,7 @@
 #pragma once
 #include "nsa_attn.h"
 #include "nsa_device.h"
+#include "nsa_attn_rowstats.h"
 
 namespace nsa {
 
@@ -302,8 +303,6 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
       dof[kc] = colv ? *reinterpret_cast<const uint4*>(dp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
   }
   const int64_t srow = ((int64_t)b * a.H + colh) * a.Tq + colt;
-  const float l2 = colv ? a.lse2[srow] : INFINITY;
-  const float dl = colv ? a.delta[srow] : 0.f;
 
   const S* krf = reinterpret_cast<const S*>(a.krf) + (int64_t)bg * a.Tp * DK;
   const S* kcf = reinterpret_cast<const S*>(a.kcf) + (int64_t)bg * DK * a.Tp;
@@ -348,6 +347,9 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
   };
   bool have = advance();
   if (have) load_rows(c_key0);
+  // row statistics after the first tile's loads are issued (their O loads overlap them)
+  float l2, dl;
+  dq_row_stats<T, NVC>(a, b, colh, colt, colv, dof, g4, srow, l2, dl);
   while (have) {
     const int key0 = c_key0, blk = c_blk;
     const int blk_lo = blk * a.lprime;

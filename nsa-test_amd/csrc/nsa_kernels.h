@@ -13,7 +13,6 @@ namespace nsa {
 
 void launch_repack(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t s_r, int64_t s_c, int B, int G,
                    int R, int C, int Rp, void* rowm, void* colm, void* rowf, void* colf, hipStream_t st);
-void launch_bwd_rowstats(int dtype, const AttnArgs& a, int DV, hipStream_t st);
 
 // return false when (dtype, dk, dv, branch) has no compiled kernel
 bool dispatch_attn_fwd(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);

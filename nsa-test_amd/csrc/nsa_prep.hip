@@ -1,7 +1,6 @@
 // Layout preparation kernels: re-pack the per-group K/V operands into the compact,
-// zero-padded layouts the attention kernels stage from, and the per-row backward
-// statistics.  All of these are HBM streams over group-sized (not head-sized)
-// tensors, except bwd_rowstats which reads O and dO once.
+// zero-padded layouts the attention kernels stage from.  All of these are HBM streams
+// over group-sized (not head-sized) tensors.
 #include <type_traits>
 
 #include "nsa_attn.h"
@@ -86,58 +85,6 @@ void launch_repack(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t
     hipLaunchKernelGGL(repack_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, s_b, s_g, s_r, s_c, G,
                        R, C, Rp, (uint16_t*)rowm, (uint16_t*)colm, (uint16_t*)rowf, (uint16_t*)colf);
   }
-}
-
-// Backward row statistics: delta = sum_d O*dO (fp32) and lse2 = (M+L)*log2(e)
-// (+inf when L = -inf, i.e. the row saw no key: every probability is then 0).
-template <typename T>
-__global__ __launch_bounds__(256) void bwd_rowstats_kernel(AttnArgs a, int DV, int lpr_log2) {
-  // LPR = 2^lpr_log2 lanes share one row, each reading 16-byte pieces; 256 / LPR rows
-  // per workgroup
-  using S = typename Store<T>::type;
-  constexpr int EPF = 16 / sizeof(S);
-  const int lpr = 1 << lpr_log2;
-  const int sub = threadIdx.x & (lpr - 1);
-  const int64_t row = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> lpr_log2;  // flattened (b, h, t)
-  const int64_t nrows = (int64_t)a.B * a.H * a.Tq;
-  const bool valid = row < nrows;
-  const int64_t rr = valid ? row : nrows - 1;
-  const int t = rr % a.Tq;
-  const int h = (rr / a.Tq) % a.H;
-  const int b = rr / ((int64_t)a.Tq * a.H);
-  const S* o = reinterpret_cast<const S*>(a.o) + b * a.so_b + h * a.so_h + (int64_t)t * a.so_t;
-  const S* d = reinterpret_cast<const S*>(a.dout) + b * a.sdo_b + h * a.sdo_h + (int64_t)t * a.sdo_t;
-  float acc = 0.f;
-  for (int e = sub * EPF; e < DV; e += lpr * EPF) {
-    const uint4 ov = *reinterpret_cast<const uint4*>(o + e);
-    const uint4 dv = *reinterpret_cast<const uint4*>(d + e);
-    const S* op = reinterpret_cast<const S*>(&ov);
-    const S* dp = reinterpret_cast<const S*>(&dv);
-#pragma unroll
-    for (int u = 0; u < EPF; ++u) acc += Elem<T>::to_f32(op[u]) * Elem<T>::to_f32(dp[u]);
-  }
-  for (int off = lpr >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
-  if (valid && sub == 0) {
-    float* delta = const_cast<float*>(a.delta);
-    float* lse2 = const_cast<float*>(a.lse2);
-    delta[row] = acc;
-    const float L = a.L[b * a.sl_b + h * a.sl_h + (int64_t)t * a.sl_t];
-    const float M = a.M[b * a.sm_b + h * a.sm_h + (int64_t)t * a.sm_t];
-    lse2[row] = (L == -INFINITY) ? INFINITY : (M + L) * kLog2e;
-  }
-}
-
-void launch_bwd_rowstats(int dtype, const AttnArgs& a, int DV, hipStream_t st) {
-  const int64_t nrows = (int64_t)a.B * a.H * a.Tq;
-  const int pieces = DV / (dtype == kF32 ? 4 : 8);  // DV is a multiple of 32 (padded head dims)
-  int lg = 0;
-  while ((1 << lg) < pieces && lg < 6) ++lg;
-  const int64_t rows_per_wg = 256 >> lg;
-  dim3 grid((unsigned)((nrows + rows_per_wg - 1) / rows_per_wg));
-  if (dtype == kF32)
-    hipLaunchKernelGGL(bwd_rowstats_kernel<float>, grid, dim3(256), 0, st, a, DV, lg);
-  else
-    hipLaunchKernelGGL(bwd_rowstats_kernel<bf16>, grid, dim3(256), 0, st, a, DV, lg);
 }
 
 }  // namespace nsa
