@@ -69,56 +69,84 @@ __global__ __launch_bounds__(256) void sel_clean_kernel(const void* idx, int idx
   if (chunk_cnt && keep) atomicAdd(&chunk_cnt[((int64_t)bg * nchunks + t / kCsrChunk) * nblk + key], 1);
 }
 
-// Per (b,g): chunk_cnt[c][j] -> exclusive running base over chunks (+ block offset);
-// csr_off[j] = exclusive scan of block totals; seg_off[j] = exclusive scan of
-// ceil(total_j / kSegT) work items.
-__global__ __launch_bounds__(256) void sel_csr_scan_kernel(int* chunk_cnt, int nchunks, int nblk, int* csr_off,
-                                                           int* seg_off) {
-  extern __shared__ int tot[];  // nblk
-  const int bg = blockIdx.x;
-  int* cc = chunk_cnt + (int64_t)bg * nchunks * nblk;
-  for (int j = threadIdx.x; j < nblk; j += 256) {
-    int run = 0;
-    for (int c = 0; c < nchunks; ++c) {
-      const int x = cc[(int64_t)c * nblk + j];
-      cc[(int64_t)c * nblk + j] = run;
-      run += x;
+// One wave per (b, g, block j): chunk_cnt[c][j] -> the exclusive running count of
+// block j's entries in the chunks before c (64 chunks per step, a wave prefix sum);
+// block j's total goes to tot[j].
+__global__ __launch_bounds__(256) void sel_csr_chunk_scan_kernel(int* chunk_cnt, int nchunks, int nblk, int* tot) {
+  const int lane = threadIdx.x & 63;
+  const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int bg = blockIdx.y;
+  if (j >= nblk) return;  // whole wave
+  int* cc = chunk_cnt + (int64_t)bg * nchunks * nblk + j;
+  int carry = 0;
+  for (int c0 = 0; c0 < nchunks; c0 += 64) {
+    const int c = c0 + lane;
+    const int x = c < nchunks ? cc[(int64_t)c * nblk] : 0;
+    int inc = x;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(inc, o);
+      if (lane >= o) inc += y;
     }
-    tot[j] = run;
+    if (c < nchunks) cc[(int64_t)c * nblk] = carry + inc - x;
+    carry += __shfl(inc, 63);
   }
-  __syncthreads();
+  if (lane == 0) tot[(int64_t)bg * (nblk + 1) + j] = carry;
+}
+
+// One workgroup per (b, g): csr_off[j] = exclusive prefix of the block totals (read
+// from csr_off itself, where the chunk scan left them), seg_off[j] = exclusive prefix
+// of ceil(total_j / kSegT) work items; entry nblk holds the sums.
+__global__ __launch_bounds__(256) void sel_csr_block_scan_kernel(int nblk, int* csr_off, int* seg_off) {
+  __shared__ int s_a[256], s_b[256];
+  const int tid = threadIdx.x;
+  const int bg = blockIdx.x;
   int* off = csr_off + (int64_t)bg * (nblk + 1);
   int* so = seg_off + (int64_t)bg * (nblk + 1);
-  if (threadIdx.x == 0) {
-    int run = 0, srun = 0;
-    for (int j = 0; j < nblk; ++j) {
-      off[j] = run;
-      so[j] = srun;
-      run += tot[j];
-      srun += (tot[j] + kSegT - 1) / kSegT;
-      tot[j] = off[j];
-    }
-    off[nblk] = run;
-    so[nblk] = srun;
+  const int per = (nblk + 255) / 256;  // contiguous entries per thread
+  const int j0 = min(nblk, tid * per), j1 = min(nblk, j0 + per);
+  int sa = 0, sb = 0;
+  for (int j = j0; j < j1; ++j) {
+    const int t = off[j];
+    sa += t;
+    sb += (t + kSegT - 1) / kSegT;
   }
+  s_a[tid] = sa;
+  s_b[tid] = sb;
   __syncthreads();
-  for (int j = threadIdx.x; j < nblk; j += 256) {
-    const int base = tot[j];
-    for (int c = 0; c < nchunks; ++c) cc[(int64_t)c * nblk + j] += base;
+  for (int o = 1; o < 256; o <<= 1) {  // inclusive scan over the 256 partials
+    const int xa = tid >= o ? s_a[tid - o] : 0, xb = tid >= o ? s_b[tid - o] : 0;
+    __syncthreads();
+    s_a[tid] += xa;
+    s_b[tid] += xb;
+    __syncthreads();
+  }
+  int ra = s_a[tid] - sa, rb = s_b[tid] - sb;  // exclusive bases of this thread's range
+  for (int j = j0; j < j1; ++j) {
+    const int t = off[j];
+    off[j] = ra;
+    so[j] = rb;
+    ra += t;
+    rb += (t + kSegT - 1) / kSegT;
+  }
+  if (tid == 255) {
+    off[nblk] = s_a[255];
+    so[nblk] = s_b[255];
   }
 }
 
 // One wave per (b, g, chunk of kCsrChunk timesteps): walk the timesteps in order,
 // appending t to each of its blocks' lists.  A block appears at most once per row,
 // so the lanes of one step never collide.
-__global__ __launch_bounds__(64) void sel_csr_fill_kernel(const int* clean, const int* chunk_base, int Tq,
-                                                          int nslots, int nchunks, int nblk, int* csr_t,
-                                                          int64_t csr_stride) {
+__global__ __launch_bounds__(64) void sel_csr_fill_kernel(const int* clean, const int* chunk_base,
+                                                          const int* csr_off, int Tq, int nslots, int nchunks,
+                                                          int nblk, int* csr_t, int64_t csr_stride) {
   extern __shared__ int cur[];  // nblk
   const int c = blockIdx.x, bg = blockIdx.y;
   const int lane = threadIdx.x;
   const int* cb = chunk_base + ((int64_t)bg * nchunks + c) * nblk;
-  for (int j = lane; j < nblk; j += 64) cur[j] = cb[j];
+  const int* off = csr_off + (int64_t)bg * (nblk + 1);
+  for (int j = lane; j < nblk; j += 64) cur[j] = off[j] + cb[j];
   __syncthreads();
   int* out = csr_t + (int64_t)bg * csr_stride;
   const int t0 = c * kCsrChunk;
@@ -163,10 +191,11 @@ void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g,
 void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int nslots, int nblk, int* csr_off,
                     int* csr_t, int* seg_off, hipStream_t st) {
   const int nchunks = (Tq + kCsrChunk - 1) / kCsrChunk;
-  hipLaunchKernelGGL(sel_csr_scan_kernel, dim3(B * G), dim3(256), nblk * sizeof(int), st, chunk_cnt, nchunks, nblk,
-                     csr_off, seg_off);
+  hipLaunchKernelGGL(sel_csr_chunk_scan_kernel, dim3((nblk + 3) / 4, B * G), dim3(256), 0, st, chunk_cnt, nchunks,
+                     nblk, csr_off);
+  hipLaunchKernelGGL(sel_csr_block_scan_kernel, dim3(B * G), dim3(256), 0, st, nblk, csr_off, seg_off);
   hipLaunchKernelGGL(sel_csr_fill_kernel, dim3(nchunks, B * G), dim3(64), nblk * sizeof(int), st, clean, chunk_cnt,
-                     Tq, nslots, nchunks, nblk, csr_t, (int64_t)Tq * nslots);
+                     csr_off, Tq, nslots, nchunks, nblk, csr_t, (int64_t)Tq * nslots);
 }
 
 int sel_csr_chunks(int Tq) { return (Tq + kCsrChunk - 1) / kCsrChunk; }

@@ -264,6 +264,42 @@ class SlidingWindowAttention(torch.autograd.Function):
         return dq, dk.transpose(-1, -2), dv, None, None, None
 
 
+class _LinearSplitK(torch.autograd.Function):
+    """y = x W^T (+ b) whose weight gradient, a reduction over every row of x (all
+    B*G*T tokens for the compression MLP, against a 384 x 192 output), is computed as
+    S independent row chunks by one batched GEMM with fp32 partials, then summed:
+    a single GEMM of that shape has too few output tiles to fill the GPU."""
+
+    @staticmethod
+    def forward(ctx, x, W, b):
+        ctx.save_for_backward(x, W)
+        ctx.has_b = b is not None
+        return F.linear(x, W, b)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, W = ctx.saved_tensors
+        dx = dW = db = None
+        if ctx.needs_input_grad[0]:
+            dx = dy @ W
+        dy2 = dy.reshape(-1, dy.shape[-1])
+        if ctx.needs_input_grad[1]:
+            x2 = x.reshape(-1, x.shape[-1])
+            rows = x2.shape[0]
+            S = 64
+            while S > 1 and (rows % S or rows // S < 256):
+                S //= 2
+            if S > 1 and dy2.is_cuda:
+                part = torch.bmm(dy2.view(S, rows // S, -1).transpose(1, 2), x2.view(S, rows // S, -1),
+                                 out_dtype=torch.float32)
+                dW = part.sum(0).to(W.dtype)
+            else:
+                dW = dy2.t() @ x2
+        if ctx.has_b and ctx.needs_input_grad[2]:
+            db = dy2.sum(0)
+        return dx, dW, db
+
+
 class _CompressPool(torch.autograd.Function):
     """R[i] = mean_u relu(Y[d*i+u] + C[u]),  V_cmp[i] = mean_u v[d*i+u]  (HIP)."""
 
@@ -466,11 +502,11 @@ class NSAAttention(torch.nn.Module):
         block_ends[:n_act] = torch.arange(n_act, device=dev, dtype=torch.int32) * c.d + (c.l - 1)
         l1, l2 = self.compress_mlp[0], self.compress_mlp[2]
         W1k, W1p = l1.weight[:, :dk], l1.weight[:, dk:]
-        Y = F.linear(keys, W1k.to(dt))                                            # [B,G,T,2dk]
+        Y = _LinearSplitK.apply(keys, W1k.to(dt), None)                          # [B,G,T,2dk]
         C = F.linear(self.pos_embed.weight.to(dt), W1p.to(dt),
                      l1.bias.to(dt) if l1.bias is not None else None)             # [l,2dk]
         R, Vc = _CompressPool.apply(Y, C, values, c.l, c.d, n_act)
-        Kc = F.linear(R, l2.weight.to(dt), l2.bias.to(dt) if l2.bias is not None else None)  # [B,G,n,dk]
+        Kc = _LinearSplitK.apply(R, l2.weight.to(dt), l2.bias.to(dt) if l2.bias is not None else None)  # [B,G,n,dk]
         Kc = F.pad(Kc, (0, 0, 0, n_pad - n_act)).transpose(-1, -2)               # [B,G,dk,Np]
         Vc = F.pad(Vc, (0, 0, 0, n_pad - n_act))                                 # [B,G,Np,dv]
         return Kc, Vc, block_ends, n_act

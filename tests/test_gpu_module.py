@@ -120,3 +120,21 @@ def test_compress_tokens_matches_oracle(dev, T, dtype):
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     assert rel_err(kc.float().cpu().numpy(), rk) < tol
     assert rel_err(vc.float().cpu().numpy(), rv) < tol
+
+
+@pytest.mark.parametrize("rows,dtype", [(32768, torch.bfloat16), (4096, torch.float32), (300, torch.float32)])
+def test_linear_split_k_gradients(dev, rows, dtype):
+    """The compression MLP's linear layers reduce their weight gradient over every token
+    in row chunks (one batched GEMM, fp32 partials): gradients against fp64 autograd."""
+    from nsa.kernels import _LinearSplitK
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = torch.randn(2, rows // 2, 96, device=dev, generator=g).to(dtype).requires_grad_()
+    W = (torch.randn(80, 96, device=dev, generator=g) * 0.1).to(dtype).requires_grad_()
+    b = torch.randn(80, device=dev, generator=g).to(dtype).requires_grad_()
+    dy = torch.randn(2, rows // 2, 80, device=dev, generator=g).to(dtype)
+    _LinearSplitK.apply(x, W, b).backward(dy)
+    xr, Wr, br = (t.detach().double().requires_grad_() for t in (x, W, b))
+    torch.nn.functional.linear(xr, Wr, br).backward(dy.double())
+    tol = 1e-2 if dtype == torch.bfloat16 else 1e-5
+    for got, ref in ((x.grad, xr.grad), (W.grad, Wr.grad), (b.grad, br.grad)):
+        assert rel_err(got.double().cpu().numpy(), ref.cpu().numpy()) < tol
