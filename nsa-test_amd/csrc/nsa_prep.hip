@@ -74,10 +74,89 @@ __global__ __launch_bounds__(256) void repack_kernel(const S* __restrict__ src, 
   }
 }
 
+// Fragment layouts from a source with unit feature stride and 16-byte aligned rows:
+// a 64 x 64 tile is read as 16-byte pieces into LDS (rows >= R zero), then every
+// output 16-byte piece is written in output order -- a rowfrag piece is EPF
+// consecutive features of one row (one LDS read), a colfrag piece gathers EPF rows of
+// one feature (the C-permuted key order of CFrag for bf16).
+template <typename S>
+__global__ __launch_bounds__(256) void repack_frag_kernel(const S* __restrict__ src, int64_t s_b, int64_t s_g,
+                                                          int64_t s_r, int G, int R, int C, int Rp,
+                                                          S* __restrict__ rowf, S* __restrict__ colf) {
+  using T = typename std::conditional<sizeof(S) == 2, bf16, float>::type;
+  constexpr int EPF = 16 / sizeof(S);
+  constexpr int KC = Elem<T>::kKChunk;
+  constexpr int CK = CFrag<T>::kKeys;
+  constexpr int P = 64 + EPF;  // LDS row pitch (elements): 16-byte aligned rows
+  __shared__ __attribute__((aligned(16))) S tile[64 * P];
+  const int bg = blockIdx.z;
+  const int b = bg / G, g = bg % G;
+  const int r0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
+  const S* base = src + b * s_b + g * s_g;
+  const int tid = threadIdx.x;
+  constexpr int PPR = 64 / EPF;  // 16-byte pieces per tile row
+  for (int q = tid; q < 64 * PPR; q += 256) {
+    const int rr = q / PPR, pc = (q % PPR) * EPF;
+    const int r = r0 + rr, c = c0 + pc;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (r < R && c < C) v = *reinterpret_cast<const uint4*>(base + (int64_t)r * s_r + c);
+    *reinterpret_cast<uint4*>(&tile[rr * P + pc]) = v;
+  }
+  __syncthreads();
+  const int64_t obase = (int64_t)bg * Rp * C;
+  if (rowf) {  // fragments (row16, kc) of the tile, 64 pieces each
+    constexpr int NKCT = 64 / KC;
+    for (int q = tid; q < 4 * NKCT * 64; q += 256) {
+      const int fr = q >> 6, ln = q & 63;
+      const int rr = (fr / NKCT) * 16 + (ln & 15);
+      const int cc = (fr % NKCT) * KC + (ln >> 4) * EPF;
+      const int r = r0 + rr, c = c0 + cc;
+      if (r < Rp && c < C)
+        *reinterpret_cast<uint4*>(rowf + obase + rowfrag_off<T>(r, c, C)) =
+            *reinterpret_cast<const uint4*>(&tile[rr * P + cc]);
+    }
+  }
+  if (colf) {  // fragments (key chunk, feature group) of the tile
+    for (int q = tid; q < (64 / CK) * 4 * 64; q += 256) {
+      const int fr = q >> 6, ln = q & 63;
+      const int ch = fr >> 2, fg = fr & 3;
+      const int gl = ln >> 4, f = ln & 15;
+      const int cc = fg * 16 + f;
+      const int c = c0 + cc;
+      S e[EPF];
+#pragma unroll
+      for (int p = 0; p < EPF; ++p) {
+        const int k = CK == 32 ? (p < 4 ? 4 * gl + p : 12 + 4 * gl + p) : 4 * gl + p;  // key within the chunk
+        e[p] = tile[(ch * CK + k) * P + cc];
+      }
+      const int r = r0 + ch * CK;  // the chunk's first key; the piece's keys share its offset
+      if (r < Rp && c < C) {
+        uint4 v;
+        __builtin_memcpy(&v, e, 16);
+        *reinterpret_cast<uint4*>(colf + obase + colfrag_off<T>(r + 4 * gl, c, C)) = v;
+      }
+    }
+  }
+}
+
 void launch_repack(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t s_r, int64_t s_c, int B, int G,
                    int R, int C, int Rp, void* rowm, void* colm, void* rowf, void* colf, hipStream_t st) {
   if (!rowm && !colm && !rowf && !colf) return;
   dim3 grid((Rp + 63) / 64, (C + 63) / 64, B * G);
+  {
+    const int esz = dtype == kF32 ? 4 : 2, epf = 16 / esz;
+    const bool vec = !rowm && !colm && s_c == 1 && C % epf == 0 && ((uintptr_t)src) % 16 == 0 &&
+                     (B == 1 || s_b % epf == 0) && (G == 1 || s_g % epf == 0) && (R <= 1 || s_r % epf == 0);
+    if (vec) {
+      if (dtype == kF32)
+        hipLaunchKernelGGL(repack_frag_kernel<float>, grid, dim3(256), 0, st, (const float*)src, s_b, s_g, s_r, G, R,
+                           C, Rp, (float*)rowf, (float*)colf);
+      else
+        hipLaunchKernelGGL(repack_frag_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, s_b, s_g, s_r,
+                           G, R, C, Rp, (uint16_t*)rowf, (uint16_t*)colf);
+      return;
+    }
+  }
   if (dtype == kF32) {
     hipLaunchKernelGGL(repack_kernel<float>, grid, dim3(256), 0, st, (const float*)src, s_b, s_g, s_r, s_c, G, R, C,
                        Rp, (float*)rowm, (float*)colm, (float*)rowf, (float*)colf);
