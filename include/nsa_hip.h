@@ -156,6 +156,56 @@ int nsa_sparse_selection_bwd(const void* Q, const void* K, const void* V, const 
                              int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream);
 
+/* Extensions (no counterpart in the reference): the three backward entry points above
+ * with one more argument.  dq_accumulate = 0 behaves exactly as the entry point it
+ * extends (dQ overwritten); dq_accumulate = 1 adds this branch's dQ to the values dQ
+ * already holds (same element type, added in fp32 and rounded once).  For callers that
+ * sum the branches' dQ over one shared query tensor, such as the NSA module, so no
+ * separate addition pass over dQ is needed. */
+int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const void* Out, const void* dOut,
+                           float sm_scale, const float* L, const float* M, int64_t stride_qz, int64_t stride_qh,
+                           int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
+                           int64_t stride_kn, int64_t stride_kk, int64_t stride_vz, int64_t stride_vg,
+                           int64_t stride_vn, int64_t stride_vk, int64_t stride_oz, int64_t stride_oh,
+                           int64_t stride_om, int64_t stride_ok, int64_t stride_lz, int64_t stride_lh,
+                           int64_t stride_lm, int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, void* dQ,
+                           void* dK, void* dV, int64_t stride_dqz, int64_t stride_dqh, int64_t stride_dqm,
+                           int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg, int64_t stride_dkn,
+                           int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg, int64_t stride_dvn,
+                           int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx, int window_size,
+                           int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace, size_t workspace_bytes,
+                           nsa_stream_t stream);
+
+int nsa_compression_bwd_ex(const void* Q, const void* K_blocks, const void* V_blocks, const int32_t* Block_ends,
+                        const void* Out, const void* dOut, float sm_scale, const float* L, const float* M,
+                        int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_qk,
+                        int64_t stride_kz, int64_t stride_kg, int64_t stride_kn, int64_t stride_kk,
+                        int64_t stride_vz, int64_t stride_vg, int64_t stride_vn, int64_t stride_vk,
+                        int64_t stride_oz, int64_t stride_oh, int64_t stride_om, int64_t stride_ok,
+                        int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t stride_mz,
+                        int64_t stride_mh, int64_t stride_mm, void* dQ, void* dK, void* dV, int64_t stride_dqz,
+                        int64_t stride_dqh, int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz,
+                        int64_t stride_dkg, int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz,
+                        int64_t stride_dvg, int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups,
+                        int n_ctx_q, int n_blocks, int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace,
+                        size_t workspace_bytes, nsa_stream_t stream);
+
+int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, const void* Block_indices, const void* Out,
+                             const void* dOut, float sm_scale, const float* L, const float* M, int64_t stride_qz,
+                             int64_t stride_qh, int64_t stride_qm, int64_t stride_qk, int64_t stride_kz,
+                             int64_t stride_kg, int64_t stride_kn, int64_t stride_kk, int64_t stride_vz,
+                             int64_t stride_vg, int64_t stride_vn, int64_t stride_vk, int64_t stride_oz,
+                             int64_t stride_oh, int64_t stride_om, int64_t stride_ok, int64_t stride_bz,
+                             int64_t stride_bg, int64_t stride_bm, int64_t stride_bn, int64_t stride_lz,
+                             int64_t stride_lh, int64_t stride_lm, int64_t stride_mz, int64_t stride_mh,
+                             int64_t stride_mm, void* dQ, void* dK, void* dV, int64_t stride_dqz, int64_t stride_dqh,
+                             int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg,
+                             int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
+                             int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
+                             int n_ctx_kv, int n_slots, int block_size_selection, int is_causal, int index_is_int64,
+                             int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace,
+                             size_t workspace_bytes, nsa_stream_t stream);
+
 
 /* ---- kernel timing (no reference counterpart: profiling aid) ----------------
  * nsa_timing_begin(id) records a HIP event pair on the launch stream around every

@@ -210,6 +210,7 @@ struct BwdIO {
   const float *L, *M;
   void *dQ, *dK, *dV;
   int64_t sq[4], sk[4], sv[4], so[4], sl[3], sm[3], sdq[4], sdk[4], sdv[4];
+  int dq_acc = 0;  // extension entry points only: add into dQ
 };
 
 int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int32_t* block_ends, const void* idx,
@@ -253,6 +254,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.sdq_b = io.sdq[0];
   a.sdq_h = io.sdq[1];
   a.sdq_t = io.sdq[2];
+  a.dq_acc = io.dq_acc;
   a.dk = io.dK;
   a.sdk_b = io.sdk[0];
   a.sdk_g = io.sdk[1];
@@ -455,6 +457,72 @@ int nsa_sparse_selection_bwd(const void* Q, const void* K, const void* V, const 
                              int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream) {
   NSA_BWD_IO
+  Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
+          block_size_selection};
+  if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
+  const int64_t sidx[4] = {stride_bz, stride_bg, stride_bm, stride_bn};
+  return run_bwd(s, io, sm_scale, 0, nullptr, Block_indices, sidx, index_is_int64, all_invalid_fallback,
+                 is_causal ? 1 : 0, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const void* Out, const void* dOut,
+                           float sm_scale, const float* L, const float* M, int64_t stride_qz, int64_t stride_qh,
+                           int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
+                           int64_t stride_kn, int64_t stride_kk, int64_t stride_vz, int64_t stride_vg,
+                           int64_t stride_vn, int64_t stride_vk, int64_t stride_oz, int64_t stride_oh,
+                           int64_t stride_om, int64_t stride_ok, int64_t stride_lz, int64_t stride_lh,
+                           int64_t stride_lm, int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, void* dQ,
+                           void* dK, void* dV, int64_t stride_dqz, int64_t stride_dqh, int64_t stride_dqm,
+                           int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg, int64_t stride_dkn,
+                           int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg, int64_t stride_dvn,
+                           int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx, int window_size,
+                           int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace, size_t workspace_bytes,
+                           nsa_stream_t stream) {
+  NSA_BWD_IO
+  io.dq_acc = dq_accumulate ? 1 : 0;
+  Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64, window_size};
+  return run_bwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
+                 (hipStream_t)stream);
+}
+
+int nsa_compression_bwd_ex(const void* Q, const void* K, const void* V, const int32_t* Block_ends, const void* Out,
+                        const void* dOut, float sm_scale, const float* L, const float* M, int64_t stride_qz,
+                        int64_t stride_qh, int64_t stride_qm, int64_t stride_qk, int64_t stride_kz,
+                        int64_t stride_kg, int64_t stride_kn, int64_t stride_kk, int64_t stride_vz,
+                        int64_t stride_vg, int64_t stride_vn, int64_t stride_vk, int64_t stride_oz,
+                        int64_t stride_oh, int64_t stride_om, int64_t stride_ok, int64_t stride_lz,
+                        int64_t stride_lh, int64_t stride_lm, int64_t stride_mz, int64_t stride_mh,
+                        int64_t stride_mm, void* dQ, void* dK, void* dV, int64_t stride_dqz, int64_t stride_dqh,
+                        int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg,
+                        int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
+                        int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
+                        int n_blocks, int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace,
+                        size_t workspace_bytes, nsa_stream_t stream) {
+  NSA_BWD_IO
+  io.dq_acc = dq_accumulate ? 1 : 0;
+  Shape s{kCompression, dtype, Z, H, n_kv_groups, n_ctx_q, n_blocks, head_dim_qk, head_dim_v, 0, 64};
+  if (n_blocks > 0 && !Block_ends) return fail(NSA_ERR_INVALID, "Block_ends is null");
+  return run_bwd(s, io, sm_scale, 0, Block_ends, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
+                 (hipStream_t)stream);
+}
+
+int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, const void* Block_indices, const void* Out,
+                             const void* dOut, float sm_scale, const float* L, const float* M, int64_t stride_qz,
+                             int64_t stride_qh, int64_t stride_qm, int64_t stride_qk, int64_t stride_kz,
+                             int64_t stride_kg, int64_t stride_kn, int64_t stride_kk, int64_t stride_vz,
+                             int64_t stride_vg, int64_t stride_vn, int64_t stride_vk, int64_t stride_oz,
+                             int64_t stride_oh, int64_t stride_om, int64_t stride_ok, int64_t stride_bz,
+                             int64_t stride_bg, int64_t stride_bm, int64_t stride_bn, int64_t stride_lz,
+                             int64_t stride_lh, int64_t stride_lm, int64_t stride_mz, int64_t stride_mh,
+                             int64_t stride_mm, void* dQ, void* dK, void* dV, int64_t stride_dqz, int64_t stride_dqh,
+                             int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg,
+                             int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
+                             int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
+                             int n_ctx_kv, int n_slots, int block_size_selection, int is_causal, int index_is_int64,
+                             int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace,
+                             size_t workspace_bytes, nsa_stream_t stream) {
+  NSA_BWD_IO
+  io.dq_acc = dq_accumulate ? 1 : 0;
   Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
           block_size_selection};
   if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");

@@ -398,7 +398,11 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
   if (colv) {
     S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)colt * a.sdq_t;
 #pragma unroll
-    for (int j = 0; j < DK / 16; ++j) store4<T>(dqp + j * 16 + 4 * g4, dqa[j] * a.scale);
+    for (int j = 0; j < DK / 16; ++j) {
+      f32x4 v = dqa[j] * a.scale;
+      if (a.dq_acc) v += load4<T>(dqp + j * 16 + 4 * g4);  // the caller's running dQ sum
+      store4<T>(dqp + j * 16 + 4 * g4, v);
+    }
   }
 }
 

@@ -214,6 +214,17 @@ template <> __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
 template <> __device__ __forceinline__ void store4<bf16>(uint16_t* p, f32x4 v) {
   *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
+// Load 4 consecutive T values as fp32.
+template <typename T> __device__ __forceinline__ f32x4 load4(const typename Store<T>::type* p);
+template <> __device__ __forceinline__ f32x4 load4<float>(const float* p) {
+  const float4 v = *reinterpret_cast<const float4*>(p);
+  return f32x4{v.x, v.y, v.z, v.w};
+}
+template <> __device__ __forceinline__ f32x4 load4<bf16>(const uint16_t* p) {
+  const uint2 v = *reinterpret_cast<const uint2*>(p);
+  return f32x4{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+               __uint_as_float(v.y & 0xffff0000u)};
+}
 
 // 2^x on the transcendental unit (v_exp_f32); exp2(-inf) = 0.  Inputs here are <= 0,
 // results below the normal range may flush, which the softmax tolerates.

@@ -11,6 +11,7 @@ from .kernels import (
     CompressionAttention,
     GatedMix,
     NSAAttention,
+    NSABranches,
     NSAConfig,
     SelectionAttention,
     SlidingWindowAttention,

@@ -45,6 +45,12 @@ SIGNATURES = {
     "nsa_sparse_selection_fwd": (_I, [_P, _P, _P, _P, _P, _F, _P, _P, *_S26, *[_I] * 12, _I, _P, _Z, _P]),
     "nsa_sparse_selection_bwd": (
         _I, [_P, _P, _P, _P, _P, _P, _F, _P, _P, *_S26, _P, _P, _P, *_S12, *[_I] * 12, _I, _P, _Z, _P]),
+}
+# the backward extensions: one more int (dq_accumulate) before the workspace
+for _n in ("nsa_sliding_window_bwd", "nsa_compression_bwd", "nsa_sparse_selection_bwd"):
+    _r, _a = SIGNATURES[_n]
+    SIGNATURES[_n + "_ex"] = (_r, [*_a[:-3], _I, *_a[-3:]])
+SIGNATURES.update({
     "nsa_score_topn": (_I, [_P, _P, _P, _P, _P, _P, *[_L] * 12, *[_I] * 13, _F, _P, _Z, _P]),
     "nsa_score_topn_workspace_size": (_Z, [_I] * 7),
     "nsa_timing_begin": (_I, [_I]),
@@ -53,7 +59,7 @@ SIGNATURES = {
     "nsa_gate_mix_bwd": (_I, [_P] + [_L] * 3 + [_P] * 3 + [_L] * 3 + [_P] + [_L] * 4 + [_P] * 4 + [_I] * 5 + [_P]),
     "nsa_compress_pool_fwd": (_I, [_P] * 5 + [_I] * 9 + [_P]),
     "nsa_compress_pool_bwd": (_I, [_P] * 7 + [_I] * 9 + [_P]),
-}
+})
 
 _lock = threading.Lock()
 _lib = None

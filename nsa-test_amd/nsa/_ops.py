@@ -125,9 +125,13 @@ def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=
 
 
 def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0, block_ends=None, indices=None,
-             lprime: int = 64, causal: bool = True, fallback: bool = False, dq=None, dk=None, dv=None):
-    """Backward of one NSA branch.  dq is overwritten, dk / dv ([Z,G,Tkv,*] logical
-    views) are accumulated into (allocated zeroed when not given).  Returns (dq, dk, dv)."""
+             lprime: int = 64, causal: bool = True, fallback: bool = False, dq=None, dk=None, dv=None,
+             dq_accumulate: bool = False):
+    """Backward of one NSA branch.  dq is overwritten (added to when dq_accumulate, which
+    needs dq), dk / dv ([Z,G,Tkv,*] logical views) are accumulated into (allocated
+    zeroed when not given).  Returns (dq, dk, dv)."""
+    if dq_accumulate and dq is None:
+        raise ValueError("dq_accumulate needs the dq tensor to add to")
     _check_device(q, k, v, o, do, L, M, block_ends, indices, dq, dk, dv)
     Z, H, Tq, dkw = q.shape
     G, Tkv = k.shape[1], k.shape[2]
@@ -144,6 +148,7 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     Lf = L.to(torch.float32)
     Mf = M.to(torch.float32)
     direct_dq = dq is not None and dq.dtype == cdt and dkw == DK and _rows_ok(dq)
+    acc = bool(dq_accumulate) and direct_dq  # otherwise the sum is taken below
     dqk = dq if direct_dq else torch.empty(Z, H, Tq, DK, device=dev, dtype=cdt)
     direct_dk = dk is not None and dk.dtype == cdt and dkw == DK
     direct_dv = dv is not None and dv.dtype == cdt and dvw == DV
@@ -158,24 +163,28 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     s_main = [*qk.stride(), *kk.stride(), *vk.stride(), *ok.stride()]
     s_lm = [*Lf.stride(), *Mf.stride()]
     s_grad = [*dqk.stride(), *dkk.stride(), *dvk.stride()]
+    # the reference-interface entry points, or their extensions when dQ is added to
+    sfx, tail = ("_ex", (1, _ptr(ws), ws.numel(), st)) if acc else ("", (_ptr(ws), ws.numel(), st))
     if branch == SLIDING:
-        _lib.call("nsa_sliding_window_bwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(ok), _ptr(dok), float(scale),
+        _lib.call("nsa_sliding_window_bwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(ok), _ptr(dok), float(scale),
                   _ptr(Lf), _ptr(Mf), *s_main, *s_lm, _ptr(dqk), _ptr(dkk), _ptr(dvk), *s_grad, Z, H, G, Tq,
-                  int(window), DK, DV, dt, _ptr(ws), ws.numel(), st)
+                  int(window), DK, DV, dt, *tail)
     elif branch == COMPRESSION:
         be = block_ends.to(torch.int32).contiguous()
-        _lib.call("nsa_compression_bwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(be), _ptr(ok), _ptr(dok), float(scale),
+        _lib.call("nsa_compression_bwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(be), _ptr(ok), _ptr(dok), float(scale),
                   _ptr(Lf), _ptr(Mf), *s_main, *s_lm, _ptr(dqk), _ptr(dkk), _ptr(dvk), *s_grad, Z, H, G, Tq, Tkv,
-                  DK, DV, dt, _ptr(ws), ws.numel(), st)
+                  DK, DV, dt, *tail)
     else:
         idx = indices if indices.dtype in (torch.int32, torch.int64) else indices.to(torch.int64)
-        _lib.call("nsa_sparse_selection_bwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(idx), _ptr(ok), _ptr(dok),
+        _lib.call("nsa_sparse_selection_bwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(idx), _ptr(ok), _ptr(dok),
                   float(scale), _ptr(Lf), _ptr(Mf), *s_main, *idx.stride(), *s_lm, _ptr(dqk), _ptr(dkk), _ptr(dvk),
                   *s_grad, Z, H, G, Tq, Tkv, n_slots, int(lprime), int(bool(causal)), int(idx.dtype == torch.int64),
-                  int(bool(fallback)), DK, DV, dt, _ptr(ws), ws.numel(), st)
+                  int(bool(fallback)), DK, DV, dt, *tail)
     if not direct_dq:
         r = dqk[..., :dkw]
-        if dq is not None:
+        if dq is not None and dq_accumulate:
+            dq.add_(r.to(dq.dtype))
+        elif dq is not None:
             dq.copy_(r)
         else:
             dq = r if q.dtype == cdt else r.to(q.dtype)

@@ -264,6 +264,43 @@ class SlidingWindowAttention(torch.autograd.Function):
         return dq, dk.transpose(-1, -2), dv, None, None, None
 
 
+class NSABranches(torch.autograd.Function):
+    """The three attention branches over one query tensor, as the NSA module runs them:
+    (o_cmp, o_sel, o_win) = (CompressionAttention, SelectionAttention,
+    SlidingWindowAttention) of the same q, with the same arguments and layouts as those
+    three functions.  The forward is the three branch forwards; the backward runs the
+    three branch backwards with the second and third adding their dQ into the first's
+    (the dQ kernels' accumulate mode) instead of autograd summing three dQ tensors."""
+
+    @staticmethod
+    def forward(ctx, q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win, scale, config):
+        lp = config.l_prime
+        o_c, Lc, Mc = _ops.attn_fwd(COMPRESSION, q, _kt(k_compressed), v_compressed, scale, block_ends=block_ends)
+        o_s, Ls, Ms = _ops.attn_fwd(SELECTION, q, _kt(k_sel), v_sel, scale, indices=indices, lprime=lp,
+                                    fallback=True)
+        o_w, Lw, Mw = _ops.attn_fwd(SLIDING, q, _kt(k_win), v_win, scale, window=config.w)
+        ctx.save_for_backward(q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win,
+                              o_c, Lc, Mc, o_s, Ls, Ms, o_w, Lw, Mw)
+        ctx.scale, ctx.lprime, ctx.window = scale, lp, config.w
+        return o_c, o_s, o_w
+
+    @staticmethod
+    def backward(ctx, do_c, do_s, do_w):
+        (q, kc, vc, be, ks, vs, idx, kw, vw, o_c, Lc, Mc, o_s, Ls, Ms, o_w, Lw, Mw) = ctx.saved_tensors
+        sc = ctx.scale
+        do_c = torch.zeros_like(o_c) if do_c is None else do_c
+        do_s = torch.zeros_like(o_s) if do_s is None else do_s
+        do_w = torch.zeros_like(o_w) if do_w is None else do_w
+        dq = torch.empty(q.shape, device=q.device, dtype=_ops.compute_dtype(q.dtype))
+        _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, do_c, Lc, Mc, sc, block_ends=be, dq=dq)
+        _, dks, dvs = _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, do_s, Ls, Ms, sc, indices=idx,
+                                    lprime=ctx.lprime, fallback=True, dq=dq, dq_accumulate=True)
+        _, dkw, dvw = _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, do_w, Lw, Mw, sc, window=ctx.window, dq=dq,
+                                    dq_accumulate=True)
+        return (dq.to(q.dtype), dkc.transpose(-1, -2), dvc, None, dks.transpose(-1, -2), dvs, None,
+                dkw.transpose(-1, -2), dvw, None, None)
+
+
 class _LinearSplitK(torch.autograd.Function):
     """y = x W^T (+ b) whose weight gradient, a reduction over every row of x (all
     B*G*T tokens for the compression MLP, against a 384 x 192 output), is computed as
@@ -535,9 +572,8 @@ class NSAAttention(torch.nn.Module):
             indices, p_cmp, p_slc = sel, None, None
 
         qk = q.contiguous()
-        o_cmp = CompressionAttention.apply(qk, k_cmp, v_cmp, block_ends, self.scale, c)
-        o_sel = SelectionAttention.apply(qk, k_sel.transpose(-1, -2), v_sel, indices, self.scale, c)
-        o_win = SlidingWindowAttention.apply(qk, k_win.transpose(-1, -2), v_win, self.scale, c.w, c)
+        o_cmp, o_sel, o_win = NSABranches.apply(qk, k_cmp, v_cmp, block_ends, k_sel.transpose(-1, -2), v_sel,
+                                                indices, k_win.transpose(-1, -2), v_win, self.scale, c)
 
         gates = self.gate_mlp(x).view(B, T, H, 3).permute(0, 2, 1, 3)
         gates = torch.softmax(gates, dim=-1) if c.gate_mode == "softmax" else torch.sigmoid(gates)

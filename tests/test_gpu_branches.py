@@ -319,3 +319,45 @@ def test_strided_views(dev):
     v = torch.randn(B, G, T, 2 * d, device=dev)[..., ::2]
     do = torch.randn(B, H, T, d, device=dev)
     _check(_ops.SLIDING, q, kp, v, do, 0.125, torch.float32, window=50)
+
+
+@pytest.mark.parametrize("dk,dtype", [(64, torch.float32), (192, torch.bfloat16), (48, torch.float32)])
+def test_nsa_branches_matches_separate_functions(dev, dk, dtype):
+    """NSABranches (the module's three branches with dQ summed in the dQ kernels) against
+    CompressionAttention / SelectionAttention / SlidingWindowAttention applied separately
+    (autograd summing dQ): same outputs, same gradients.  dk = 48 is zero-padded to a
+    compiled head dim, which takes the summed-on-the-host dQ path."""
+    from nsa import NSABranches
+    from nsa.kernels import CompressionAttention, SlidingWindowAttention
+    B, H, G, T, dv, l, d, lp, n, w = 1, 8, 2, 300, 64, 32, 16, 32, 4, 64
+    g = torch.Generator().manual_seed(11)
+    nb = (T - l) // d + 1
+    q = torch.randn(B, H, T, dk, generator=g).to(dtype)
+    kc = torch.randn(B, G, dk, nb, generator=g).to(dtype)
+    vc = torch.randn(B, G, nb, dv, generator=g).to(dtype)
+    be = (torch.arange(nb) * d + l - 1).to(torch.int32)
+    ks = torch.randn(B, G, dk, T, generator=g).to(dtype)
+    vs = torch.randn(B, G, T, dv, generator=g).to(dtype)
+    kw = torch.randn(B, G, dk, T, generator=g).to(dtype)
+    vw = torch.randn(B, G, T, dv, generator=g).to(dtype)
+    idx = _random_indices(12, B, G, T, T, lp, n).to(dev)
+    dos = [torch.randn(B, H, T, dv, generator=g).to(dtype).to(dev) for _ in range(3)]
+    cfg = NSAConfig(head_dim_qk=dk, head_dim_v=dv, n_heads=H, n_kv_groups=G, l=l, d=d, l_prime=lp, n=n, w=w)
+    scale = 1 / math.sqrt(dk)
+
+    def leaves():
+        return [t.to(dev).requires_grad_() for t in (q, kc, vc, ks, vs, kw, vw)]
+
+    a = leaves()
+    outs_a = NSABranches.apply(a[0], a[1], a[2], be.to(dev), a[3], a[4], idx, a[5], a[6], scale, cfg)
+    torch.autograd.backward(outs_a, dos)
+    b = leaves()
+    outs_b = (CompressionAttention.apply(b[0], b[1], b[2], be.to(dev), scale, cfg),
+              SelectionAttention.apply(b[0], b[3], b[4], idx, scale, cfg),
+              SlidingWindowAttention.apply(b[0], b[5], b[6], scale, w, cfg))
+    torch.autograd.backward(outs_b, dos)
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
+    for x, y in zip(outs_a, outs_b):
+        assert rel_err(_np(x), _np(y)) == 0.0
+    for x, y in zip(a, b):
+        assert rel_err(_np(x.grad), _np(y.grad)) < tol
