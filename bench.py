@@ -89,18 +89,17 @@ def make_workload(name, dev, seed=0):
 def nsa_step(cfg, mod, w, backward=True):
     """One NSA forward (+ backward): every kernel of the hot path runs once."""
     import torch
-    from nsa import GatedMix, NSABranches, score_and_select
+    from nsa import NSACore, score_and_select
 
     scale = 1.0 / math.sqrt(cfg.head_dim_qk)
     q = w["q"]
     kc, vc, be, _ = mod.compress_tokens(w["k_cmp_in"], w["v_cmp_in"])
     with torch.no_grad():
         idx = score_and_select(q.detach(), kc.detach(), be, scale, cfg)
-    # the three branches as NSAAttention runs them (their backward sums dQ in-kernel)
-    o_c, o_s, o_w = NSABranches.apply(q, kc, vc, be, w["k_sel"].transpose(-1, -2), w["v_sel"], idx,
-                                      w["k_win"].transpose(-1, -2), w["v_win"], scale, cfg)
     gt = torch.sigmoid(w["gate_logits"])
-    o = GatedMix.apply(o_c, o_s, o_w, gt)
+    # the three branches and the gated mix as NSAAttention runs them
+    o = NSACore.apply(q, kc, vc, be, w["k_sel"].transpose(-1, -2), w["v_sel"], idx, w["k_win"].transpose(-1, -2),
+                      w["v_win"], gt, scale, cfg)
     if backward:
         o.backward(w["dO"])
         for t in list(w.values()) + list(mod.parameters()):

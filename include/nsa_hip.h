@@ -157,11 +157,17 @@ int nsa_sparse_selection_bwd(const void* Q, const void* K, const void* V, const 
                              size_t workspace_bytes, nsa_stream_t stream);
 
 /* Extensions (no counterpart in the reference): the three backward entry points above
- * with one more argument.  dq_accumulate = 0 behaves exactly as the entry point it
- * extends (dQ overwritten); dq_accumulate = 1 adds this branch's dQ to the values dQ
- * already holds (same element type, added in fp32 and rounded once).  For callers that
- * sum the branches' dQ over one shared query tensor, such as the NSA module, so no
- * separate addition pass over dQ is needed. */
+ * with two more arguments, for callers that run the three branches over one query
+ * tensor and already hold the row sums, such as the NSA module:
+ *   dq_accumulate  0: dQ is overwritten, as by the entry point extended; 1: this
+ *                  branch's dQ is added to the values dQ already holds (same element
+ *                  type, added in fp32 and rounded once), so no separate pass sums the
+ *                  branches' dQ.
+ *   delta_in       null: as the entry point extended; otherwise the row sums
+ *                  D = sum_d Out * dOut per (z, h, t) row, fp32, contiguous [Z, H, n_ctx_q],
+ *                  which the backward then uses instead of reading Out.
+ * With dq_accumulate = 0 and delta_in = null each behaves exactly as the entry point
+ * it extends. */
 int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const void* Out, const void* dOut,
                            float sm_scale, const float* L, const float* M, int64_t stride_qz, int64_t stride_qh,
                            int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
@@ -173,7 +179,8 @@ int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const
                            int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg, int64_t stride_dkn,
                            int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg, int64_t stride_dvn,
                            int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx, int window_size,
-                           int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace, size_t workspace_bytes,
+                           int head_dim_qk, int head_dim_v, int dtype,
+                           int dq_accumulate, const float* delta_in, void* workspace, size_t workspace_bytes,
                            nsa_stream_t stream);
 
 int nsa_compression_bwd_ex(const void* Q, const void* K_blocks, const void* V_blocks, const int32_t* Block_ends,
@@ -187,7 +194,8 @@ int nsa_compression_bwd_ex(const void* Q, const void* K_blocks, const void* V_bl
                         int64_t stride_dqh, int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz,
                         int64_t stride_dkg, int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz,
                         int64_t stride_dvg, int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups,
-                        int n_ctx_q, int n_blocks, int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace,
+                        int n_ctx_q, int n_blocks, int head_dim_qk, int head_dim_v, int dtype,
+                        int dq_accumulate, const float* delta_in, void* workspace,
                         size_t workspace_bytes, nsa_stream_t stream);
 
 int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, const void* Block_indices, const void* Out,
@@ -203,7 +211,8 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
                              int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
                              int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
                              int n_ctx_kv, int n_slots, int block_size_selection, int is_causal, int index_is_int64,
-                             int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace,
+                             int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype,
+                             int dq_accumulate, const float* delta_in, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream);
 
 

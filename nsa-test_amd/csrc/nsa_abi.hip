@@ -210,7 +210,8 @@ struct BwdIO {
   const float *L, *M;
   void *dQ, *dK, *dV;
   int64_t sq[4], sk[4], sv[4], so[4], sl[3], sm[3], sdq[4], sdk[4], sdv[4];
-  int dq_acc = 0;  // extension entry points only: add into dQ
+  int dq_acc = 0;                   // extension entry points only: add into dQ
+  const float* delta_in = nullptr;  // extension entry points only: precomputed row sums
 };
 
 int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int32_t* block_ends, const void* idx,
@@ -255,6 +256,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.sdq_h = io.sdq[1];
   a.sdq_t = io.sdq[2];
   a.dq_acc = io.dq_acc;
+  a.delta_in = io.delta_in;
   a.dk = io.dK;
   a.sdk_b = io.sdk[0];
   a.sdk_g = io.sdk[1];
@@ -476,10 +478,12 @@ int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const
                            int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg, int64_t stride_dkn,
                            int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg, int64_t stride_dvn,
                            int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx, int window_size,
-                           int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace, size_t workspace_bytes,
+                           int head_dim_qk, int head_dim_v, int dtype,
+                           int dq_accumulate, const float* delta_in, void* workspace, size_t workspace_bytes,
                            nsa_stream_t stream) {
   NSA_BWD_IO
   io.dq_acc = dq_accumulate ? 1 : 0;
+  io.delta_in = delta_in;
   Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64, window_size};
   return run_bwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
                  (hipStream_t)stream);
@@ -496,10 +500,12 @@ int nsa_compression_bwd_ex(const void* Q, const void* K, const void* V, const in
                         int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz, int64_t stride_dkg,
                         int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
                         int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
-                        int n_blocks, int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace,
+                        int n_blocks, int head_dim_qk, int head_dim_v, int dtype,
+                        int dq_accumulate, const float* delta_in, void* workspace,
                         size_t workspace_bytes, nsa_stream_t stream) {
   NSA_BWD_IO
   io.dq_acc = dq_accumulate ? 1 : 0;
+  io.delta_in = delta_in;
   Shape s{kCompression, dtype, Z, H, n_kv_groups, n_ctx_q, n_blocks, head_dim_qk, head_dim_v, 0, 64};
   if (n_blocks > 0 && !Block_ends) return fail(NSA_ERR_INVALID, "Block_ends is null");
   return run_bwd(s, io, sm_scale, 0, Block_ends, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
@@ -519,10 +525,12 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
                              int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
                              int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
                              int n_ctx_kv, int n_slots, int block_size_selection, int is_causal, int index_is_int64,
-                             int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype, int dq_accumulate, void* workspace,
+                             int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype,
+                             int dq_accumulate, const float* delta_in, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream) {
   NSA_BWD_IO
   io.dq_acc = dq_accumulate ? 1 : 0;
+  io.delta_in = delta_in;
   Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
           block_size_selection};
   if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");

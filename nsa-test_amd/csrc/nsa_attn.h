@@ -46,6 +46,7 @@ struct AttnArgs {
   void* dq;
   int64_t sdq_b, sdq_h, sdq_t;
   int dq_acc;  // 1: dQ is added to the destination's values instead of overwriting them
+  const float* delta_in;  // null, or the caller's rowsum(O*dO) [B,H,Tq] compact (O is then not read)
   const float* lse2;   // [B,H,Tq] compact: (M+L)*log2(e), +inf for empty rows
   const float* delta;  // [B,H,Tq] compact: rowsum(O*dO)
   // dK/dV destination (accumulated into, any strides) or fp32 partials

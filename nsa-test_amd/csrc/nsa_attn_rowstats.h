@@ -1,5 +1,5 @@
 // Backward row statistics, computed by the dQ kernels for their own query columns:
-//   delta = sum_d O[d] * dO[d]   (fp32)
+//   delta = sum_d O[d] * dO[d]   (fp32; or the caller's precomputed sums, delta_in)
 //   lse2  = (M + L) * log2(e)    (+inf when L = -inf: the row saw no key, every p is 0)
 // The dQ kernels use them directly and store them for the dK/dV kernel, which runs
 // after dQ on the same stream (one pass over O fewer than a separate statistics
@@ -20,19 +20,23 @@ __device__ __forceinline__ void dq_row_stats(const AttnArgs& a, int b, int colh,
   using S = typename Store<T>::type;
   constexpr int EPF = Elem<T>::kPerFrag;
   constexpr int KC = Elem<T>::kKChunk;
-  const S* op = reinterpret_cast<const S*>(a.o) + b * a.so_b + (int64_t)colh * a.so_h + (int64_t)colt * a.so_t;
-  float acc = 0.f;
+  if (a.delta_in) {  // the caller's row sums: O is not read
+    dl = colv ? a.delta_in[srow] : 0.f;
+  } else {
+    const S* op = reinterpret_cast<const S*>(a.o) + b * a.so_b + (int64_t)colh * a.so_h + (int64_t)colt * a.so_t;
+    float acc = 0.f;
 #pragma unroll
-  for (int kc = 0; kc < NVC; ++kc) {
-    const uint4 ov = colv ? *reinterpret_cast<const uint4*>(op + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
-    const S* o = reinterpret_cast<const S*>(&ov);
-    const S* d = reinterpret_cast<const S*>(&dof[kc]);
+    for (int kc = 0; kc < NVC; ++kc) {
+      const uint4 ov = colv ? *reinterpret_cast<const uint4*>(op + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
+      const S* o = reinterpret_cast<const S*>(&ov);
+      const S* d = reinterpret_cast<const S*>(&dof[kc]);
 #pragma unroll
-    for (int u = 0; u < EPF; ++u) acc = fmaf(Elem<T>::to_f32(o[u]), Elem<T>::to_f32(d[u]), acc);
+      for (int u = 0; u < EPF; ++u) acc = fmaf(Elem<T>::to_f32(o[u]), Elem<T>::to_f32(d[u]), acc);
+    }
+    acc += __shfl_xor(acc, 16);
+    acc += __shfl_xor(acc, 32);
+    dl = colv ? acc : 0.f;
   }
-  acc += __shfl_xor(acc, 16);
-  acc += __shfl_xor(acc, 32);
-  dl = colv ? acc : 0.f;
   l2 = INFINITY;
   if (colv) {
     const float L = a.L[b * a.sl_b + (int64_t)colh * a.sl_h + (int64_t)colt * a.sl_t];

@@ -11,7 +11,7 @@ from .kernels import (
     CompressionAttention,
     GatedMix,
     NSAAttention,
-    NSABranches,
+    NSACore,
     NSAConfig,
     SelectionAttention,
     SlidingWindowAttention,

@@ -46,10 +46,10 @@ SIGNATURES = {
     "nsa_sparse_selection_bwd": (
         _I, [_P, _P, _P, _P, _P, _P, _F, _P, _P, *_S26, _P, _P, _P, *_S12, *[_I] * 12, _I, _P, _Z, _P]),
 }
-# the backward extensions: one more int (dq_accumulate) before the workspace
+# the backward extensions: dq_accumulate (int) and delta_in (pointer) before the workspace
 for _n in ("nsa_sliding_window_bwd", "nsa_compression_bwd", "nsa_sparse_selection_bwd"):
     _r, _a = SIGNATURES[_n]
-    SIGNATURES[_n + "_ex"] = (_r, [*_a[:-3], _I, *_a[-3:]])
+    SIGNATURES[_n + "_ex"] = (_r, [*_a[:-3], _I, _P, *_a[-3:]])
 SIGNATURES.update({
     "nsa_score_topn": (_I, [_P, _P, _P, _P, _P, _P, *[_L] * 12, *[_I] * 13, _F, _P, _Z, _P]),
     "nsa_score_topn_workspace_size": (_Z, [_I] * 7),

@@ -126,10 +126,11 @@ def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=
 
 def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0, block_ends=None, indices=None,
              lprime: int = 64, causal: bool = True, fallback: bool = False, dq=None, dk=None, dv=None,
-             dq_accumulate: bool = False):
+             dq_accumulate: bool = False, delta=None):
     """Backward of one NSA branch.  dq is overwritten (added to when dq_accumulate, which
     needs dq), dk / dv ([Z,G,Tkv,*] logical views) are accumulated into (allocated
-    zeroed when not given).  Returns (dq, dk, dv)."""
+    zeroed when not given).  delta: optional precomputed row sums sum_d o * do [Z,H,Tq]
+    (fp32), used instead of reading o.  Returns (dq, dk, dv)."""
     if dq_accumulate and dq is None:
         raise ValueError("dq_accumulate needs the dq tensor to add to")
     _check_device(q, k, v, o, do, L, M, block_ends, indices, dq, dk, dv)
@@ -164,7 +165,13 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     s_lm = [*Lf.stride(), *Mf.stride()]
     s_grad = [*dqk.stride(), *dkk.stride(), *dvk.stride()]
     # the reference-interface entry points, or their extensions when dQ is added to
-    sfx, tail = ("_ex", (1, _ptr(ws), ws.numel(), st)) if acc else ("", (_ptr(ws), ws.numel(), st))
+    dl = None if delta is None else delta.to(torch.float32).contiguous()
+    if dl is not None and tuple(dl.shape) != (Z, H, Tq):
+        raise ValueError(f"delta must be [{Z}, {H}, {Tq}], got {tuple(dl.shape)}")
+    if acc or dl is not None:
+        sfx, tail = "_ex", (int(acc), _ptr(dl), _ptr(ws), ws.numel(), st)
+    else:
+        sfx, tail = "", (_ptr(ws), ws.numel(), st)
     if branch == SLIDING:
         _lib.call("nsa_sliding_window_bwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(ok), _ptr(dok), float(scale),
                   _ptr(Lf), _ptr(Mf), *s_main, *s_lm, _ptr(dqk), _ptr(dkk), _ptr(dvk), *s_grad, Z, H, G, Tq,

@@ -264,41 +264,49 @@ class SlidingWindowAttention(torch.autograd.Function):
         return dq, dk.transpose(-1, -2), dv, None, None, None
 
 
-class NSABranches(torch.autograd.Function):
-    """The three attention branches over one query tensor, as the NSA module runs them:
-    (o_cmp, o_sel, o_win) = (CompressionAttention, SelectionAttention,
-    SlidingWindowAttention) of the same q, with the same arguments and layouts as those
-    three functions.  The forward is the three branch forwards; the backward runs the
-    three branch backwards with the second and third adding their dQ into the first's
-    (the dQ kernels' accumulate mode) instead of autograd summing three dQ tensors."""
+class NSACore(torch.autograd.Function):
+    """The attention core of NSAAttention over one query tensor: the three branches
+    (CompressionAttention, SelectionAttention and SlidingWindowAttention, with their
+    arguments and layouts) and the gated mix (GatedMix) as one function, returning the
+    mixed output.  The backward runs the mix backward, which gives each branch's output
+    gradient g_k dO and dg_k = sum_d dO o_k; the branch backwards then take
+    D_k = g_k dg_k (= sum_d o_k (g_k dO)) as their row sums instead of reading o_k again,
+    and the second and third add their dQ into the first's (the dQ kernels' accumulate
+    mode) instead of autograd summing three dQ tensors."""
 
     @staticmethod
-    def forward(ctx, q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win, scale, config):
+    def forward(ctx, q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win, gates, scale,
+                config):
+        _ops._check_device(q, gates)
         lp = config.l_prime
         o_c, Lc, Mc = _ops.attn_fwd(COMPRESSION, q, _kt(k_compressed), v_compressed, scale, block_ends=block_ends)
         o_s, Ls, Ms = _ops.attn_fwd(SELECTION, q, _kt(k_sel), v_sel, scale, indices=indices, lprime=lp,
                                     fallback=True)
         o_w, Lw, Mw = _ops.attn_fwd(SLIDING, q, _kt(k_win), v_win, scale, window=config.w)
-        ctx.save_for_backward(q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win,
-                              o_c, Lc, Mc, o_s, Ls, Ms, o_w, Lw, Mw)
-        ctx.scale, ctx.lprime, ctx.window = scale, lp, config.w
-        return o_c, o_s, o_w
+        cdt = _ops.compute_dtype(q.dtype)
+        os_ = [t.to(cdt).contiguous() for t in (o_c, o_s, o_w)]
+        g = gates.to(cdt)
+        out = _mix_fwd(os_, g)
+        ctx.save_for_backward(q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win, g,
+                              *os_, Lc, Mc, Ls, Ms, Lw, Mw)
+        ctx.scale, ctx.lprime, ctx.window, ctx.gdtype = scale, lp, config.w, gates.dtype
+        return out.to(q.dtype)
 
     @staticmethod
-    def backward(ctx, do_c, do_s, do_w):
-        (q, kc, vc, be, ks, vs, idx, kw, vw, o_c, Lc, Mc, o_s, Ls, Ms, o_w, Lw, Mw) = ctx.saved_tensors
+    def backward(ctx, dout):
+        (q, kc, vc, be, ks, vs, idx, kw, vw, g, o_c, o_s, o_w, Lc, Mc, Ls, Ms, Lw, Mw) = ctx.saved_tensors
         sc = ctx.scale
-        do_c = torch.zeros_like(o_c) if do_c is None else do_c
-        do_s = torch.zeros_like(o_s) if do_s is None else do_s
-        do_w = torch.zeros_like(o_w) if do_w is None else do_w
+        dos, dg = _mix_bwd(dout, [o_c, o_s, o_w], g)
+        deltas = [(g[..., k].float() * dg[..., k]).contiguous() for k in range(3)]
         dq = torch.empty(q.shape, device=q.device, dtype=_ops.compute_dtype(q.dtype))
-        _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, do_c, Lc, Mc, sc, block_ends=be, dq=dq)
-        _, dks, dvs = _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, do_s, Ls, Ms, sc, indices=idx,
-                                    lprime=ctx.lprime, fallback=True, dq=dq, dq_accumulate=True)
-        _, dkw, dvw = _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, do_w, Lw, Mw, sc, window=ctx.window, dq=dq,
-                                    dq_accumulate=True)
+        _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, dos[0], Lc, Mc, sc, block_ends=be, dq=dq,
+                                    delta=deltas[0])
+        _, dks, dvs = _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, dos[1], Ls, Ms, sc, indices=idx,
+                                    lprime=ctx.lprime, fallback=True, dq=dq, dq_accumulate=True, delta=deltas[1])
+        _, dkw, dvw = _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, dos[2], Lw, Mw, sc, window=ctx.window, dq=dq,
+                                    dq_accumulate=True, delta=deltas[2])
         return (dq.to(q.dtype), dkc.transpose(-1, -2), dvc, None, dks.transpose(-1, -2), dvs, None,
-                dkw.transpose(-1, -2), dvw, None, None)
+                dkw.transpose(-1, -2), dvw, dg.to(ctx.gdtype), None, None)
 
 
 class _LinearSplitK(torch.autograd.Function):
@@ -372,6 +380,34 @@ class _CompressPool(torch.autograd.Function):
 
 
 # ============================================================== selection (Eq. 9 / 10)
+def _mix_fwd(os_, g):
+    """out = sum_k g[..., k] o_k over compute-dtype contiguous branch outputs [B,H,T,dv];
+    the result is a [B,H,T,dv] view of [B,T,H,dv] storage."""
+    B, H, T, dv = os_[0].shape
+    cdt = os_[0].dtype
+    out = torch.empty(B, T, H, dv, device=os_[0].device, dtype=cdt).permute(0, 2, 1, 3)
+    so, sg, sx = os_[0].stride(), g.stride(), out.stride()
+    _lib.call("nsa_gate_mix_fwd", *[_ops._ptr(t) for t in os_], so[0], so[1], so[2], _ops._ptr(g), *sg,
+              _ops._ptr(out), sx[0], sx[1], sx[2], B, H, T, dv, _ops._dtype_code(cdt), _ops._stream(out.device))
+    return out
+
+
+def _mix_bwd(dout, os_, g):
+    """(d o_k = g[..., k] dout for k < 3, dg [B,H,T,3] fp32 with dg[..., k] = sum_d dout o_k)."""
+    cdt = os_[0].dtype
+    B, H, T, dv = os_[0].shape
+    d = dout.to(cdt)
+    if d.stride(-1) != 1 or (d.stride(2) * d.element_size()) % 16 or (d.stride(1) * d.element_size()) % 16:
+        d = d.contiguous()
+    dos = [torch.empty(B, H, T, dv, device=d.device, dtype=cdt) for _ in range(3)]
+    dg = torch.empty(B, H, T, 3, device=d.device, dtype=torch.float32)
+    sd, so, sg = d.stride(), os_[0].stride(), g.stride()
+    _lib.call("nsa_gate_mix_bwd", _ops._ptr(d), sd[0], sd[1], sd[2], *[_ops._ptr(t) for t in os_], so[0], so[1],
+              so[2], _ops._ptr(g), *sg, *[_ops._ptr(t) for t in dos], _ops._ptr(dg), B, H, T, dv,
+              _ops._dtype_code(cdt), _ops._stream(d.device))
+    return dos, dg
+
+
 class GatedMix(torch.autograd.Function):
     """o = o_cmp * g[..., 0] + o_sel * g[..., 1] + o_win * g[..., 2] (NSAAttention.forward,
     reference nsa/kernels.py:2446-2463) as one fused HIP pass each way.  Branch outputs
@@ -384,11 +420,7 @@ class GatedMix(torch.autograd.Function):
         cdt = _ops.compute_dtype(o_cmp.dtype)
         os_ = [t.to(cdt).contiguous() for t in (o_cmp, o_sel, o_win)]
         g = gates.to(cdt)
-        B, H, T, dv = os_[0].shape
-        out = torch.empty(B, T, H, dv, device=o_cmp.device, dtype=cdt).permute(0, 2, 1, 3)
-        so, sg, sx = os_[0].stride(), g.stride(), out.stride()
-        _lib.call("nsa_gate_mix_fwd", *[_ops._ptr(t) for t in os_], so[0], so[1], so[2], _ops._ptr(g), *sg,
-                  _ops._ptr(out), sx[0], sx[1], sx[2], B, H, T, dv, _ops._dtype_code(cdt), _ops._stream(o_cmp.device))
+        out = _mix_fwd(os_, g)
         ctx.save_for_backward(*os_, g)
         ctx.dtypes = (o_cmp.dtype, o_sel.dtype, o_win.dtype, gates.dtype)
         return out.to(o_cmp.dtype)
@@ -396,17 +428,7 @@ class GatedMix(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dout):
         o_c, o_s, o_w, g = ctx.saved_tensors
-        cdt = o_c.dtype
-        B, H, T, dv = o_c.shape
-        d = dout.to(cdt)
-        if d.stride(-1) != 1 or (d.stride(2) * d.element_size()) % 16 or (d.stride(1) * d.element_size()) % 16:
-            d = d.contiguous()
-        dos = [torch.empty(B, H, T, dv, device=d.device, dtype=cdt) for _ in range(3)]
-        dg = torch.empty(B, H, T, 3, device=d.device, dtype=torch.float32)
-        sd, so, sg = d.stride(), o_c.stride(), g.stride()
-        _lib.call("nsa_gate_mix_bwd", _ops._ptr(d), sd[0], sd[1], sd[2], _ops._ptr(o_c), _ops._ptr(o_s),
-                  _ops._ptr(o_w), so[0], so[1], so[2], _ops._ptr(g), *sg, *[_ops._ptr(t) for t in dos],
-                  _ops._ptr(dg), B, H, T, dv, _ops._dtype_code(cdt), _ops._stream(d.device))
+        dos, dg = _mix_bwd(dout, [o_c, o_s, o_w], g)
         dts = ctx.dtypes
         return dos[0].to(dts[0]), dos[1].to(dts[1]), dos[2].to(dts[2]), dg.to(dts[3])
 
@@ -571,13 +593,11 @@ class NSAAttention(torch.nn.Module):
         else:
             indices, p_cmp, p_slc = sel, None, None
 
-        qk = q.contiguous()
-        o_cmp, o_sel, o_win = NSABranches.apply(qk, k_cmp, v_cmp, block_ends, k_sel.transpose(-1, -2), v_sel,
-                                                indices, k_win.transpose(-1, -2), v_win, self.scale, c)
-
         gates = self.gate_mlp(x).view(B, T, H, 3).permute(0, 2, 1, 3)
         gates = torch.softmax(gates, dim=-1) if c.gate_mode == "softmax" else torch.sigmoid(gates)
-        o = GatedMix.apply(o_cmp, o_sel, o_win, gates)
+        qk = q.contiguous()
+        o = NSACore.apply(qk, k_cmp, v_cmp, block_ends, k_sel.transpose(-1, -2), v_sel, indices,
+                          k_win.transpose(-1, -2), v_win, gates, self.scale, c)
         o = o.transpose(1, 2).reshape(B, T, H * dv)
         out = self.dropout(self.o_proj(o))
         info = None

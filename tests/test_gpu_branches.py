@@ -322,13 +322,14 @@ def test_strided_views(dev):
 
 
 @pytest.mark.parametrize("dk,dtype", [(64, torch.float32), (192, torch.bfloat16), (48, torch.float32)])
-def test_nsa_branches_matches_separate_functions(dev, dk, dtype):
-    """NSABranches (the module's three branches with dQ summed in the dQ kernels) against
-    CompressionAttention / SelectionAttention / SlidingWindowAttention applied separately
-    (autograd summing dQ): same outputs, same gradients.  dk = 48 is zero-padded to a
-    compiled head dim, which takes the summed-on-the-host dQ path."""
-    from nsa import NSABranches
-    from nsa.kernels import CompressionAttention, SlidingWindowAttention
+def test_nsa_core_matches_separate_functions(dev, dk, dtype):
+    """NSACore (the module's three branches and gated mix, with the branch backwards
+    taking the mix's row sums and summing dQ in the dQ kernels) against
+    CompressionAttention / SelectionAttention / SlidingWindowAttention and GatedMix
+    applied separately (autograd summing dQ): same output, same gradients.  dk = 48 is
+    zero-padded to a compiled head dim, which takes the summed-on-the-host dQ path."""
+    from nsa import NSACore
+    from nsa.kernels import CompressionAttention, GatedMix, SlidingWindowAttention
     B, H, G, T, dv, l, d, lp, n, w = 1, 8, 2, 300, 64, 32, 16, 32, 4, 64
     g = torch.Generator().manual_seed(11)
     nb = (T - l) // d + 1
@@ -340,24 +341,25 @@ def test_nsa_branches_matches_separate_functions(dev, dk, dtype):
     vs = torch.randn(B, G, T, dv, generator=g).to(dtype)
     kw = torch.randn(B, G, dk, T, generator=g).to(dtype)
     vw = torch.randn(B, G, T, dv, generator=g).to(dtype)
+    gates = torch.sigmoid(torch.randn(B, H, T, 3, generator=g)).to(dtype)
     idx = _random_indices(12, B, G, T, T, lp, n).to(dev)
-    dos = [torch.randn(B, H, T, dv, generator=g).to(dtype).to(dev) for _ in range(3)]
+    do = torch.randn(B, H, T, dv, generator=g).to(dtype).to(dev)
     cfg = NSAConfig(head_dim_qk=dk, head_dim_v=dv, n_heads=H, n_kv_groups=G, l=l, d=d, l_prime=lp, n=n, w=w)
     scale = 1 / math.sqrt(dk)
 
     def leaves():
-        return [t.to(dev).requires_grad_() for t in (q, kc, vc, ks, vs, kw, vw)]
+        return [t.to(dev).requires_grad_() for t in (q, kc, vc, ks, vs, kw, vw, gates)]
 
     a = leaves()
-    outs_a = NSABranches.apply(a[0], a[1], a[2], be.to(dev), a[3], a[4], idx, a[5], a[6], scale, cfg)
-    torch.autograd.backward(outs_a, dos)
+    out_a = NSACore.apply(a[0], a[1], a[2], be.to(dev), a[3], a[4], idx, a[5], a[6], a[7], scale, cfg)
+    out_a.backward(do)
     b = leaves()
     outs_b = (CompressionAttention.apply(b[0], b[1], b[2], be.to(dev), scale, cfg),
               SelectionAttention.apply(b[0], b[3], b[4], idx, scale, cfg),
               SlidingWindowAttention.apply(b[0], b[5], b[6], scale, w, cfg))
-    torch.autograd.backward(outs_b, dos)
+    out_b = GatedMix.apply(*outs_b, b[7])
+    out_b.backward(do)
     tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
-    for x, y in zip(outs_a, outs_b):
-        assert rel_err(_np(x), _np(y)) == 0.0
+    assert rel_err(_np(out_a), _np(out_b)) == 0.0
     for x, y in zip(a, b):
         assert rel_err(_np(x.grad), _np(y.grad)) < tol
