@@ -223,11 +223,18 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
   }
 
   if (colv) {
+    // accumulate mode: the caller's running dQ (loaded here, not at the start: the
+    // registers are not spare in this kernel)
     S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)colt * a.sdq_t;
+    typename Raw4<T>::type dq_prev[DK / 16];
+    if (a.dq_acc) {
+#pragma unroll
+      for (int j = 0; j < DK / 16; ++j) dq_prev[j] = load4_raw<T>(dqp + j * 16 + 4 * g4);
+    }
 #pragma unroll
     for (int j = 0; j < DK / 16; ++j) {
       f32x4 v = dqa[j] * a.scale;
-      if (a.dq_acc) v += load4<T>(dqp + j * 16 + 4 * g4);  // the caller's running dQ sum
+      if (a.dq_acc) v += raw4_f32(dq_prev[j]);
       store4<T>(dqp + j * 16 + 4 * g4, v);
     }
   }

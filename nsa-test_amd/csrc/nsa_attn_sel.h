@@ -303,6 +303,16 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
       dof[kc] = colv ? *reinterpret_cast<const uint4*>(dp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
   }
   const int64_t srow = ((int64_t)b * a.H + colh) * a.Tq + colt;
+  // accumulate mode: the caller's running dQ of the column, requested now (bf16; fp32 has
+  // no spare registers and loads it in the epilogue) so that the load is complete by the
+  // epilogue: with one wave per SIMD nothing else would hide its latency
+  constexpr bool kPrefetchDq = sizeof(S) == 2;
+  typename Raw4<T>::type dq_prev[DK / 16];
+  S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)colt * a.sdq_t;
+  if (kPrefetchDq && a.dq_acc && colv) {
+#pragma unroll
+    for (int j = 0; j < DK / 16; ++j) dq_prev[j] = load4_raw<T>(dqp + j * 16 + 4 * g4);
+  }
 
   const S* krf = reinterpret_cast<const S*>(a.krf) + (int64_t)bg * a.Tp * DK;
   const S* kcf = reinterpret_cast<const S*>(a.kcf) + (int64_t)bg * DK * a.Tp;
@@ -396,11 +406,14 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
   }
 
   if (colv) {
-    S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)colt * a.sdq_t;
+    if (!kPrefetchDq && a.dq_acc) {
+#pragma unroll
+      for (int j = 0; j < DK / 16; ++j) dq_prev[j] = load4_raw<T>(dqp + j * 16 + 4 * g4);
+    }
 #pragma unroll
     for (int j = 0; j < DK / 16; ++j) {
       f32x4 v = dqa[j] * a.scale;
-      if (a.dq_acc) v += load4<T>(dqp + j * 16 + 4 * g4);  // the caller's running dQ sum
+      if (a.dq_acc) v += raw4_f32(dq_prev[j]);  // the caller's running dQ sum
       store4<T>(dqp + j * 16 + 4 * g4, v);
     }
   }

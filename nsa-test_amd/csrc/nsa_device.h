@@ -214,6 +214,22 @@ template <> __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
 template <> __device__ __forceinline__ void store4<bf16>(uint16_t* p, f32x4 v) {
   *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
+// 4 consecutive T values in storage form (8 bytes bf16, 16 bytes fp32): loaded early,
+// converted and added later.
+template <typename T> struct Raw4 { typedef uint4 type; };
+template <> struct Raw4<bf16> { typedef uint2 type; };
+template <typename T>
+__device__ __forceinline__ typename Raw4<T>::type load4_raw(const typename Store<T>::type* p) {
+  return *reinterpret_cast<const typename Raw4<T>::type*>(p);
+}
+__device__ __forceinline__ f32x4 raw4_f32(const uint4& v) {
+  return f32x4{__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
+}
+__device__ __forceinline__ f32x4 raw4_f32(const uint2& v) {
+  return f32x4{__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+               __uint_as_float(v.y & 0xffff0000u)};
+}
+
 // Load 4 consecutive T values as fp32.
 template <typename T> __device__ __forceinline__ f32x4 load4(const typename Store<T>::type* p);
 template <> __device__ __forceinline__ f32x4 load4<float>(const float* p) {
