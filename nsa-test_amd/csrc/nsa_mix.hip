@@ -23,6 +23,7 @@ struct MixArgs {
   int64_t sx_b, sx_h, sx_t;
   void* dO[3];  // backward: contiguous [B,H,T,dv]
   float* dg;    // backward: contiguous [B,H,T,3]
+  float* delta; // backward, optional: contiguous [3][B,H,T], delta_k = g_k dg_k
   int B, H, T, dv;
 };
 
@@ -114,6 +115,11 @@ __global__ __launch_bounds__(256) void gate_mix_kernel(MixArgs a, int lpr_log2) 
       a.dg[rr * 3 + 0] = dg0;
       a.dg[rr * 3 + 1] = dg1;
       a.dg[rr * 3 + 2] = dg2;
+      if (a.delta) {  // sum_d o_k (g_k dout): the branch backwards' row sums
+        a.delta[rr] = g0 * dg0;
+        a.delta[nrows + rr] = g1 * dg1;
+        a.delta[2 * nrows + rr] = g2 * dg2;
+      }
     }
   }
 }
@@ -183,8 +189,8 @@ extern "C" int nsa_gate_mix_fwd(const void* o_cmp, const void* o_sel, const void
 extern "C" int nsa_gate_mix_bwd(const void* dout, int64_t sd_b, int64_t sd_h, int64_t sd_t, const void* o_cmp,
                                 const void* o_sel, const void* o_win, int64_t so_b, int64_t so_h, int64_t so_t,
                                 const void* gates, int64_t sg_b, int64_t sg_h, int64_t sg_t, int64_t sg_k,
-                                void* do_cmp, void* do_sel, void* do_win, float* dgates, int B, int H, int T, int dv,
-                                int dtype, nsa_stream_t stream) {
+                                void* do_cmp, void* do_sel, void* do_win, float* dgates, float* delta, int B, int H,
+                                int T, int dv, int dtype, nsa_stream_t stream) {
   using namespace nsa;
   const void* ptrs[7] = {dout, o_cmp, o_sel, o_win, do_cmp, do_sel, do_win};
   if (int rc = check_mix(dtype, B, H, T, dv, ptrs, 7)) return rc;
@@ -211,6 +217,7 @@ extern "C" int nsa_gate_mix_bwd(const void* dout, int64_t sd_b, int64_t sd_h, in
   a.dO[1] = do_sel;
   a.dO[2] = do_win;
   a.dg = dgates;
+  a.delta = delta;
   a.B = B;
   a.H = H;
   a.T = T;

@@ -296,8 +296,7 @@ class NSACore(torch.autograd.Function):
     def backward(ctx, dout):
         (q, kc, vc, be, ks, vs, idx, kw, vw, g, o_c, o_s, o_w, Lc, Mc, Ls, Ms, Lw, Mw) = ctx.saved_tensors
         sc = ctx.scale
-        dos, dg = _mix_bwd(dout, [o_c, o_s, o_w], g)
-        deltas = [(g[..., k].float() * dg[..., k]).contiguous() for k in range(3)]
+        dos, dg, deltas = _mix_bwd(dout, [o_c, o_s, o_w], g, want_delta=True)
         dq = torch.empty(q.shape, device=q.device, dtype=_ops.compute_dtype(q.dtype))
         _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, dos[0], Lc, Mc, sc, block_ends=be, dq=dq,
                                     delta=deltas[0])
@@ -392,8 +391,9 @@ def _mix_fwd(os_, g):
     return out
 
 
-def _mix_bwd(dout, os_, g):
-    """(d o_k = g[..., k] dout for k < 3, dg [B,H,T,3] fp32 with dg[..., k] = sum_d dout o_k)."""
+def _mix_bwd(dout, os_, g, want_delta=False):
+    """(d o_k = g[..., k] dout for k < 3, dg [B,H,T,3] fp32 with dg[..., k] = sum_d dout o_k,
+    and with want_delta the row sums delta [3,B,H,T] fp32, delta[k] = g[..., k] dg[..., k])."""
     cdt = os_[0].dtype
     B, H, T, dv = os_[0].shape
     d = dout.to(cdt)
@@ -401,11 +401,12 @@ def _mix_bwd(dout, os_, g):
         d = d.contiguous()
     dos = [torch.empty(B, H, T, dv, device=d.device, dtype=cdt) for _ in range(3)]
     dg = torch.empty(B, H, T, 3, device=d.device, dtype=torch.float32)
+    delta = torch.empty(3, B, H, T, device=d.device, dtype=torch.float32) if want_delta else None
     sd, so, sg = d.stride(), os_[0].stride(), g.stride()
     _lib.call("nsa_gate_mix_bwd", _ops._ptr(d), sd[0], sd[1], sd[2], *[_ops._ptr(t) for t in os_], so[0], so[1],
-              so[2], _ops._ptr(g), *sg, *[_ops._ptr(t) for t in dos], _ops._ptr(dg), B, H, T, dv,
+              so[2], _ops._ptr(g), *sg, *[_ops._ptr(t) for t in dos], _ops._ptr(dg), _ops._ptr(delta), B, H, T, dv,
               _ops._dtype_code(cdt), _ops._stream(d.device))
-    return dos, dg
+    return (dos, dg, delta) if want_delta else (dos, dg)
 
 
 class GatedMix(torch.autograd.Function):
