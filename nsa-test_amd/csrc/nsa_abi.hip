@@ -47,11 +47,16 @@ struct Shape {
   int esz() const { return dtype == NSA_F32 ? 4 : 2; }
   int nblk() const { return br == kSelection ? (Tkv + lprime - 1) / lprime : 0; }
   int nsubblk() const { return (lprime + 63) / 64; }
-  // dK/dV work items per (b, g): key tiles x query segments
-  int items_per_bg() const {
-    if (br == kSelection) return nsubblk() * (nblk() + (int)(((int64_t)Tq * nslots + kSegT - 1) / kSegT));
-    return ((Tkv + dkdv_keys(br) - 1) / dkdv_keys(br)) * dkdv_nseg(br, Tq, window);
+  // dK/dV work items per (b, g): key tiles x query segments of sg entries
+  int items_for(int sg) const {
+    if (br == kSelection) return nsubblk() * (nblk() + (int)(((int64_t)Tq * nslots + sg - 1) / sg));
+    return ((Tkv + dkdv_keys(br) - 1) / dkdv_keys(br)) * dkdv_nseg(br, Tq, window, sg);
   }
+  // segment length: 128 entries when 256-entry segments leave fewer than 4096 work
+  // items in all (shorter segments then raise the parallelism by more than their extra
+  // partials cost), else 256
+  int seg() const { return (int64_t)Z * G * items_for(kSegTMax) < 4096 ? kSegTMax / 2 : kSegTMax; }
+  int items_per_bg() const { return items_for(seg()); }
 };
 
 struct Layout {
@@ -278,6 +283,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.lse2 = at<float>(ws, L.lse2);
   a.delta = at<float>(ws, L.delta);
   a.items_per_bg = s.items_per_bg();
+  a.seg = s.seg();
   a.partial = at<float>(ws, L.partial);
 
   launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp,
@@ -289,7 +295,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
                      s.Tkv, fallback, causal, at<int>(ws, L.clean), at<int>(ws, L.chunk), s.nblk(), st);
     launch_sel_csr(at<int>(ws, L.clean), at<int>(ws, L.chunk), s.Z, s.G, s.Tq, s.nslots, s.nblk(),
-                   at<int>(ws, L.csr_off), at<int>(ws, L.csr_t), at<int>(ws, L.seg_off), st);
+                   at<int>(ws, L.csr_off), at<int>(ws, L.csr_t), at<int>(ws, L.seg_off), s.seg(), st);
     a.sel = at<int>(ws, L.clean);
     a.csr_off = at<int>(ws, L.csr_off);
     a.csr_t = at<int>(ws, L.csr_t);

@@ -18,8 +18,9 @@ constexpr int kDqCols = kDqWaves * 16;
 constexpr int kSelMaxBlocks = 4096;
 // Query rows staged per step of the dK/dV kernels.
 constexpr int kRowChunk = 32;
-// Timesteps per dK/dV work item for branches that split the query axis.
-constexpr int kSegT = 256;
+// Query entries (timesteps; selection: CSR entries) per dK/dV work item: 128 or 256,
+// chosen per launch (dkdv_seg_len), at most kSegTMax.
+constexpr int kSegTMax = 256;
 
 struct AttnArgs {
   // queries [B,H,Tq,DK], unit stride on the feature axis
@@ -56,6 +57,7 @@ struct AttnArgs {
   int64_t sdv_b, sdv_g, sdv_t, sdv_d;
   float* partial;  // [items][64][DK+DV]
   int items_per_bg;
+  int seg;  // query entries per dK/dV work item
   // shapes
   int B, H, G, hpg, Tq, Tkv;
   float scale;

@@ -29,13 +29,13 @@ namespace nsa {
 // (8 waves) otherwise, so each staged query row serves twice as many keys
 __host__ __device__ constexpr int dkdv_keys(int br) { return br == kSelection ? 64 : 128; }
 
-// number of query segments per key tile (sliding and compression items)
-__host__ __device__ inline int dkdv_nseg(int br, int Tq, int window) {
+// number of query segments of seg timesteps per key tile (sliding and compression items)
+__host__ __device__ inline int dkdv_nseg(int br, int Tq, int window, int seg) {
   if (br == kSliding) {
     const int span = min(window + dkdv_keys(kSliding) - 1, Tq + dkdv_keys(kSliding) - 1);
-    return (span + kSegT - 1) / kSegT;
+    return (span + seg - 1) / seg;
   }
-  return (Tq + kSegT - 1) / kSegT;
+  return (Tq + seg - 1) / seg;
 }
 
 // the two-row transposed store of one staged 16-byte piece
@@ -105,7 +105,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   __shared__ float s_l2[NB][RC];
   __shared__ float s_dl[NB][RC];
   __shared__ int s_be[KEYS];
-  __shared__ int s_tl[kSegT];  // selection: the item's query timesteps
+  __shared__ int s_tl[kSegTMax];  // selection: the item's query timesteps
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -125,15 +125,15 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   int f_lo, f_hi;              // flattened row range (row f -> (t, head))
   int e_base = 0;              // selection: row f -> t = s_tl[f / hpg - e_base]
   if (BR == kSliding) {
-    const int nseg = dkdv_nseg(kSliding, a.Tq, a.window);
+    const int nseg = dkdv_nseg(kSliding, a.Tq, a.window, a.seg);
     const int tile = item / nseg, seg = item % nseg;
     key0 = tile * KEYS;
-    const int t_lo = key0 + seg * kSegT;
-    const int t_hi = min(a.Tq, min(key0 + (seg + 1) * kSegT, key0 + KEYS - 1 + a.window));
+    const int t_lo = key0 + seg * a.seg;
+    const int t_hi = min(a.Tq, min(key0 + (seg + 1) * a.seg, key0 + KEYS - 1 + a.window));
     f_lo = t_lo * hpg;
     f_hi = t_hi > t_lo ? t_hi * hpg : f_lo;
   } else if (BR == kCompression) {
-    const int nseg = dkdv_nseg(kCompression, a.Tq, 0);
+    const int nseg = dkdv_nseg(kCompression, a.Tq, 0, a.seg);
     const int tile = item / nseg, seg = item % nseg;
     key0 = tile * KEYS;
     if (tid < KEYS) {
@@ -146,8 +146,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     for (int c = 0; c < KEYS / 64; ++c) be_min = min(be_min, s_be[c * 64 + lane]);
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) be_min = min(be_min, __shfl_xor(be_min, o));
-    const int t_lo = max(seg * kSegT, max(be_min, 0));
-    const int t_hi = min(a.Tq, (seg + 1) * kSegT);
+    const int t_lo = max(seg * a.seg, max(be_min, 0));
+    const int t_hi = min(a.Tq, (seg + 1) * a.seg);
     f_lo = t_lo * hpg;
     f_hi = t_hi > t_lo ? t_hi * hpg : f_lo;
   } else {
@@ -164,8 +164,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     const int j = lo;
     const int k = sidx - so[j];
     const int* co = a.csr_off + (int64_t)bg * (a.nblk + 1);
-    const int e_lo = co[j] + k * kSegT;
-    const int e_hi = min(co[j + 1], e_lo + kSegT);
+    const int e_lo = co[j] + k * a.seg;
+    const int e_hi = min(co[j + 1], e_lo + a.seg);
     key0 = j * a.lprime + sub * 64;
     blk_hi = min(j * a.lprime + a.lprime, a.Tkv);
     f_lo = e_lo * hpg;

@@ -25,7 +25,7 @@ void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g,
                       int G, int Tq, int n_in, int nslots, int lprime, int Tkv, int fallback, int causal, int* clean,
                       int* chunk_cnt, int nblk, hipStream_t st);
 void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int nslots, int nblk, int* csr_off,
-                    int* csr_t, int* seg_off, hipStream_t st);
+                    int* csr_t, int* seg_off, int seg, hipStream_t st);
 int sel_csr_chunks(int Tq);
 
 // record an error message for nsa_last_error(); returns `code`

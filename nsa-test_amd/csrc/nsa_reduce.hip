@@ -40,7 +40,7 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
   int key0, key_hi, first, count, step;
   const int keys = dkdv_keys(br);  // keys of one item's partial
   if (br != kSelection) {
-    const int nseg = dkdv_nseg(br, a.Tq, a.window);
+    const int nseg = dkdv_nseg(br, a.Tq, a.window, a.seg);
     key0 = blockIdx.x * keys;
     key_hi = a.Tkv;
     first = blockIdx.x * nseg;

@@ -96,8 +96,8 @@ __global__ __launch_bounds__(256) void sel_csr_chunk_scan_kernel(int* chunk_cnt,
 
 // One workgroup per (b, g): csr_off[j] = exclusive prefix of the block totals (read
 // from csr_off itself, where the chunk scan left them), seg_off[j] = exclusive prefix
-// of ceil(total_j / kSegT) work items; entry nblk holds the sums.
-__global__ __launch_bounds__(256) void sel_csr_block_scan_kernel(int nblk, int* csr_off, int* seg_off) {
+// of ceil(total_j / seg) work items; entry nblk holds the sums.
+__global__ __launch_bounds__(256) void sel_csr_block_scan_kernel(int nblk, int seg, int* csr_off, int* seg_off) {
   __shared__ int s_a[256], s_b[256];
   const int tid = threadIdx.x;
   const int bg = blockIdx.x;
@@ -109,7 +109,7 @@ __global__ __launch_bounds__(256) void sel_csr_block_scan_kernel(int nblk, int* 
   for (int j = j0; j < j1; ++j) {
     const int t = off[j];
     sa += t;
-    sb += (t + kSegT - 1) / kSegT;
+    sb += (t + seg - 1) / seg;
   }
   s_a[tid] = sa;
   s_b[tid] = sb;
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) void sel_csr_block_scan_kernel(int nblk, int* 
     off[j] = ra;
     so[j] = rb;
     ra += t;
-    rb += (t + kSegT - 1) / kSegT;
+    rb += (t + seg - 1) / seg;
   }
   if (tid == 255) {
     off[nblk] = s_a[255];
@@ -189,11 +189,11 @@ void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g,
 }
 
 void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int nslots, int nblk, int* csr_off,
-                    int* csr_t, int* seg_off, hipStream_t st) {
+                    int* csr_t, int* seg_off, int seg, hipStream_t st) {
   const int nchunks = (Tq + kCsrChunk - 1) / kCsrChunk;
   hipLaunchKernelGGL(sel_csr_chunk_scan_kernel, dim3((nblk + 3) / 4, B * G), dim3(256), 0, st, chunk_cnt, nchunks,
                      nblk, csr_off);
-  hipLaunchKernelGGL(sel_csr_block_scan_kernel, dim3(B * G), dim3(256), 0, st, nblk, csr_off, seg_off);
+  hipLaunchKernelGGL(sel_csr_block_scan_kernel, dim3(B * G), dim3(256), 0, st, nblk, seg, csr_off, seg_off);
   hipLaunchKernelGGL(sel_csr_fill_kernel, dim3(nchunks, B * G), dim3(64), nblk * sizeof(int), st, clean, chunk_cnt,
                      csr_off, Tq, nslots, nchunks, nblk, csr_t, (int64_t)Tq * nslots);
 }
