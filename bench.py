@@ -96,10 +96,10 @@ def nsa_step(cfg, mod, w, backward=True):
     kc, vc, be, _ = mod.compress_tokens(w["k_cmp_in"], w["v_cmp_in"])
     with torch.no_grad():
         idx = score_and_select(q.detach(), kc.detach(), be, scale, cfg)
-    gt = torch.sigmoid(w["gate_logits"])
-    # the three branches and the gated mix as NSAAttention runs them
+    # the three branches, the sigmoid gates (cfg.gate_mode) and the gated mix as
+    # NSAAttention runs them
     o = NSACore.apply(q, kc, vc, be, w["k_sel"].transpose(-1, -2), w["v_sel"], idx, w["k_win"].transpose(-1, -2),
-                      w["v_win"], gt, scale, cfg)
+                      w["v_win"], w["gate_logits"], scale, cfg)
     if backward:
         o.backward(w["dO"])
         for t in list(w.values()) + list(mod.parameters()):

@@ -245,24 +245,28 @@ int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* Block_ends, 
                    int head_dim_qk, int n_blocks, int l, int d, int l_prime, int n, int include_fixed, int n_fixed,
                    int dtype, float scale, void* workspace, size_t workspace_bytes, nsa_stream_t stream);
 
-/* ---- gated mix of the three branches (NSAAttention.forward, nsa/kernels.py:2446-2463) --
+/* ---- gate activation and gated mix (NSAAttention.forward, nsa/kernels.py:2429-2463) --
  * No entry point of its own in the reference (torch elementwise ops there); fused here.
+ * gate_act selects what the gate input z [B,H,T,3] (any strides) is: 0 the gates g
+ * themselves; 1 logits, g = sigmoid(z); 2 logits, g = softmax over the three
+ * (the reference's gate_mode "sigmoid" / "softmax", nsa/kernels.py:2436-2440).
  * Forward: out[b,h,t,:] = g0 o_cmp + g1 o_sel + g2 o_win, summed in fp32 and rounded once
  * (the reference's eval path sums in float64 and rounds once).  o_* share the strides
- * so_*, gates [B,H,T,3] any strides, out any strides; every row unit-stride and 16-byte
- * aligned.  Backward: do_k = g_k dout (contiguous [B,H,T,dv]) and dgates[b,h,t,k] =
- * sum_d dout . o_k (contiguous fp32 [B,H,T,3]); delta, when not null, receives
- * delta[k][b,h,t] = g_k dgates[b,h,t,k] = sum_d o_k . do_k (contiguous fp32 [3,B,H,T]),
- * the row sums the branch backward extensions take as delta_in. */
+ * so_*, out any strides; every row unit-stride and 16-byte aligned.  Backward:
+ * do_k = g_k dout (contiguous [B,H,T,dv]); dgates (contiguous fp32 [B,H,T,3]) is the
+ * gradient of the gate input: dg_k = sum_d dout . o_k for gate_act 0, dg_k g_k (1 - g_k)
+ * for 1, g_k (dg_k - sum_j g_j dg_j) for 2; delta, when not null, receives
+ * delta[k][b,h,t] = g_k dg_k = sum_d o_k . do_k (contiguous fp32 [3,B,H,T]), the row
+ * sums the branch backward extensions take as delta_in. */
 int nsa_gate_mix_fwd(const void* o_cmp, const void* o_sel, const void* o_win, int64_t so_b, int64_t so_h,
                      int64_t so_t, const void* gates, int64_t sg_b, int64_t sg_h, int64_t sg_t, int64_t sg_k,
                      void* out, int64_t sout_b, int64_t sout_h, int64_t sout_t, int B, int H, int T, int dv,
-                     int dtype, nsa_stream_t stream);
+                     int gate_act, int dtype, nsa_stream_t stream);
 int nsa_gate_mix_bwd(const void* dout, int64_t sd_b, int64_t sd_h, int64_t sd_t, const void* o_cmp,
                      const void* o_sel, const void* o_win, int64_t so_b, int64_t so_h, int64_t so_t,
                      const void* gates, int64_t sg_b, int64_t sg_h, int64_t sg_t, int64_t sg_k, void* do_cmp,
                      void* do_sel, void* do_win, float* dgates, float* delta, int B, int H, int T, int dv,
-                     int dtype, nsa_stream_t stream);
+                     int gate_act, int dtype, nsa_stream_t stream);
 
 /* ---- compression pooling (compress_tokens, nsa/kernels.py:2119-2208) --------
  * With the first MLP layer split as W1 = [W1k | W1p]:  Y = k W1k^T  [Z,G,T,width],

@@ -1,8 +1,12 @@
 // Gated mix of the three branch outputs (reference nsa/kernels.py NSAAttention.forward:
 // o = o_cmp * g[...,0] + o_sel * g[...,1] + o_win * g[...,2]) and its backward, fused:
-// one pass over the outputs instead of a chain of broadcast elementwise kernels.
-//   forward : out = sum_k g_k o_k                         (fp32 sum, rounded once)
-//   backward: dO_k = g_k dout,  dg_k = sum_d dout . o_k   (fp32)
+// one pass over the outputs instead of a chain of broadcast elementwise kernels.  The
+// gate activation (reference nsa/kernels.py:2429-2440: sigmoid, or softmax over the
+// three gates) can be applied to raw gate logits z in the same pass (gate_act):
+//   forward : g = act(z), out = sum_k g_k o_k             (fp32 sum, rounded once)
+//   backward: dO_k = g_k dout,  dg_k = sum_d dout . o_k   (fp32), returned as the
+//             gradient of the kernel's gate input: dg (act = none), dg_k g_k (1 - g_k)
+//             (sigmoid), g_k (dg_k - sum_j g_j dg_j) (softmax)
 // Rows are (b, h, t); LPR lanes share a row and read 16-byte pieces of it.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -25,6 +29,7 @@ struct MixArgs {
   float* dg;    // backward: contiguous [B,H,T,3]
   float* delta; // backward, optional: contiguous [3][B,H,T], delta_k = g_k dg_k
   int B, H, T, dv;
+  int act;  // gate activation applied to the gate input: 0 none, 1 sigmoid, 2 softmax
 };
 
 template <typename S>
@@ -73,7 +78,19 @@ __global__ __launch_bounds__(256) void gate_mix_kernel(MixArgs a, int lpr_log2) 
   const int64_t ooff = b * a.so_b + h * a.so_h + (int64_t)t * a.so_t;
   const int64_t xoff = b * a.sx_b + h * a.sx_h + (int64_t)t * a.sx_t;
   const S* gp = reinterpret_cast<const S*>(a.g) + b * a.sg_b + h * a.sg_h + (int64_t)t * a.sg_t;
-  const float g0 = ld1<S>(gp), g1 = ld1<S>(gp + a.sg_k), g2 = ld1<S>(gp + 2 * a.sg_k);
+  float g0 = ld1<S>(gp), g1 = ld1<S>(gp + a.sg_k), g2 = ld1<S>(gp + 2 * a.sg_k);
+  if (a.act == 1) {
+    g0 = 1.f / (1.f + __expf(-g0));
+    g1 = 1.f / (1.f + __expf(-g1));
+    g2 = 1.f / (1.f + __expf(-g2));
+  } else if (a.act == 2) {
+    const float m = fmaxf(g0, fmaxf(g1, g2));
+    const float e0 = __expf(g0 - m), e1 = __expf(g1 - m), e2 = __expf(g2 - m);
+    const float inv = 1.f / (e0 + e1 + e2);
+    g0 = e0 * inv;
+    g1 = e1 * inv;
+    g2 = e2 * inv;
+  }
   float dg0 = 0.f, dg1 = 0.f, dg2 = 0.f;
   for (int e = sub * EPF; e < a.dv; e += lpr * EPF) {
     float o0[EPF], o1[EPF], o2[EPF];
@@ -112,14 +129,25 @@ __global__ __launch_bounds__(256) void gate_mix_kernel(MixArgs a, int lpr_log2) 
       dg2 += __shfl_xor(dg2, off);
     }
     if (valid && sub == 0) {
-      a.dg[rr * 3 + 0] = dg0;
-      a.dg[rr * 3 + 1] = dg1;
-      a.dg[rr * 3 + 2] = dg2;
       if (a.delta) {  // sum_d o_k (g_k dout): the branch backwards' row sums
         a.delta[rr] = g0 * dg0;
         a.delta[nrows + rr] = g1 * dg1;
         a.delta[2 * nrows + rr] = g2 * dg2;
       }
+      float z0 = dg0, z1 = dg1, z2 = dg2;  // gradient of the gate input
+      if (a.act == 1) {
+        z0 = dg0 * g0 * (1.f - g0);
+        z1 = dg1 * g1 * (1.f - g1);
+        z2 = dg2 * g2 * (1.f - g2);
+      } else if (a.act == 2) {
+        const float s = g0 * dg0 + g1 * dg1 + g2 * dg2;
+        z0 = g0 * (dg0 - s);
+        z1 = g1 * (dg1 - s);
+        z2 = g2 * (dg2 - s);
+      }
+      a.dg[rr * 3 + 0] = z0;
+      a.dg[rr * 3 + 1] = z1;
+      a.dg[rr * 3 + 2] = z2;
     }
   }
 }
@@ -156,10 +184,11 @@ static int check_mix(int dtype, int B, int H, int T, int dv, const void* const* 
 extern "C" int nsa_gate_mix_fwd(const void* o_cmp, const void* o_sel, const void* o_win, int64_t so_b, int64_t so_h,
                                 int64_t so_t, const void* gates, int64_t sg_b, int64_t sg_h, int64_t sg_t,
                                 int64_t sg_k, void* out, int64_t sout_b, int64_t sout_h, int64_t sout_t, int B, int H,
-                                int T, int dv, int dtype, nsa_stream_t stream) {
+                                int T, int dv, int gate_act, int dtype, nsa_stream_t stream) {
   using namespace nsa;
   const void* ptrs[4] = {o_cmp, o_sel, o_win, out};
   if (int rc = check_mix(dtype, B, H, T, dv, ptrs, 4)) return rc;
+  if (gate_act < 0 || gate_act > 2) return set_error(NSA_ERR_INVALID, "gate_act must be 0, 1 or 2");
   const int esz = dtype == NSA_F32 ? 4 : 2;
   if ((so_t * esz) % 16 || (so_h * esz) % 16 || (sout_t * esz) % 16 || (sout_h * esz) % 16)
     return set_error(NSA_ERR_LAYOUT, "rows must be 16-byte aligned");
@@ -183,6 +212,7 @@ extern "C" int nsa_gate_mix_fwd(const void* o_cmp, const void* o_sel, const void
   a.H = H;
   a.T = T;
   a.dv = dv;
+  a.act = gate_act;
   return launch_mix<false>(dtype, a, (hipStream_t)stream);
 }
 
@@ -190,10 +220,11 @@ extern "C" int nsa_gate_mix_bwd(const void* dout, int64_t sd_b, int64_t sd_h, in
                                 const void* o_sel, const void* o_win, int64_t so_b, int64_t so_h, int64_t so_t,
                                 const void* gates, int64_t sg_b, int64_t sg_h, int64_t sg_t, int64_t sg_k,
                                 void* do_cmp, void* do_sel, void* do_win, float* dgates, float* delta, int B, int H,
-                                int T, int dv, int dtype, nsa_stream_t stream) {
+                                int T, int dv, int gate_act, int dtype, nsa_stream_t stream) {
   using namespace nsa;
   const void* ptrs[7] = {dout, o_cmp, o_sel, o_win, do_cmp, do_sel, do_win};
   if (int rc = check_mix(dtype, B, H, T, dv, ptrs, 7)) return rc;
+  if (gate_act < 0 || gate_act > 2) return set_error(NSA_ERR_INVALID, "gate_act must be 0, 1 or 2");
   const int esz = dtype == NSA_F32 ? 4 : 2;
   if ((so_t * esz) % 16 || (so_h * esz) % 16 || (sd_t * esz) % 16 || (sd_h * esz) % 16)
     return set_error(NSA_ERR_LAYOUT, "rows must be 16-byte aligned");
@@ -218,6 +249,7 @@ extern "C" int nsa_gate_mix_bwd(const void* dout, int64_t sd_b, int64_t sd_h, in
   a.dO[2] = do_win;
   a.dg = dgates;
   a.delta = delta;
+  a.act = gate_act;
   a.B = B;
   a.H = H;
   a.T = T;

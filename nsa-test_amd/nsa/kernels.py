@@ -267,17 +267,19 @@ class SlidingWindowAttention(torch.autograd.Function):
 class NSACore(torch.autograd.Function):
     """The attention core of NSAAttention over one query tensor: the three branches
     (CompressionAttention, SelectionAttention and SlidingWindowAttention, with their
-    arguments and layouts) and the gated mix (GatedMix) as one function, returning the
-    mixed output.  The backward runs the mix backward, which gives each branch's output
+    arguments and layouts), the gate activation of config.gate_mode (sigmoid, or softmax
+    over the three gates) applied to gate_logits [B,H,T,3], and the gated mix (GatedMix),
+    as one function returning the mixed output.  The activation runs inside the mix
+    kernels (the backward returns the gradient of the logits).  The backward runs the mix backward, which gives each branch's output
     gradient g_k dO and dg_k = sum_d dO o_k; the branch backwards then take
     D_k = g_k dg_k (= sum_d o_k (g_k dO)) as their row sums instead of reading o_k again,
     and the second and third add their dQ into the first's (the dQ kernels' accumulate
     mode) instead of autograd summing three dQ tensors."""
 
     @staticmethod
-    def forward(ctx, q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win, gates, scale,
-                config):
-        _ops._check_device(q, gates)
+    def forward(ctx, q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win, gate_logits,
+                scale, config):
+        _ops._check_device(q, gate_logits)
         lp = config.l_prime
         o_c, Lc, Mc = _ops.attn_fwd(COMPRESSION, q, _kt(k_compressed), v_compressed, scale, block_ends=block_ends)
         o_s, Ls, Ms = _ops.attn_fwd(SELECTION, q, _kt(k_sel), v_sel, scale, indices=indices, lprime=lp,
@@ -285,18 +287,19 @@ class NSACore(torch.autograd.Function):
         o_w, Lw, Mw = _ops.attn_fwd(SLIDING, q, _kt(k_win), v_win, scale, window=config.w)
         cdt = _ops.compute_dtype(q.dtype)
         os_ = [t.to(cdt).contiguous() for t in (o_c, o_s, o_w)]
-        g = gates.to(cdt)
-        out = _mix_fwd(os_, g)
+        g = gate_logits.to(cdt)
+        act = GATE_ACT[config.gate_mode]
+        out = _mix_fwd(os_, g, act)
         ctx.save_for_backward(q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win, g,
                               *os_, Lc, Mc, Ls, Ms, Lw, Mw)
-        ctx.scale, ctx.lprime, ctx.window, ctx.gdtype = scale, lp, config.w, gates.dtype
+        ctx.scale, ctx.lprime, ctx.window, ctx.gdtype, ctx.act = scale, lp, config.w, gate_logits.dtype, act
         return out.to(q.dtype)
 
     @staticmethod
     def backward(ctx, dout):
         (q, kc, vc, be, ks, vs, idx, kw, vw, g, o_c, o_s, o_w, Lc, Mc, Ls, Ms, Lw, Mw) = ctx.saved_tensors
         sc = ctx.scale
-        dos, dg, deltas = _mix_bwd(dout, [o_c, o_s, o_w], g, want_delta=True)
+        dos, dg, deltas = _mix_bwd(dout, [o_c, o_s, o_w], g, want_delta=True, act=ctx.act)
         dq = torch.empty(q.shape, device=q.device, dtype=_ops.compute_dtype(q.dtype))
         _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, dos[0], Lc, Mc, sc, block_ends=be, dq=dq,
                                     delta=deltas[0])
@@ -379,21 +382,27 @@ class _CompressPool(torch.autograd.Function):
 
 
 # ============================================================== selection (Eq. 9 / 10)
-def _mix_fwd(os_, g):
-    """out = sum_k g[..., k] o_k over compute-dtype contiguous branch outputs [B,H,T,dv];
-    the result is a [B,H,T,dv] view of [B,T,H,dv] storage."""
+GATE_ACT = {"none": 0, "sigmoid": 1, "softmax": 2}  # gate_act codes of nsa_gate_mix_*
+
+
+def _mix_fwd(os_, g, act=0):
+    """out = sum_k a(g)[..., k] o_k over compute-dtype contiguous branch outputs [B,H,T,dv]
+    (a = identity, sigmoid or softmax over the 3 gates: act 0, 1, 2); the result is a
+    [B,H,T,dv] view of [B,T,H,dv] storage."""
     B, H, T, dv = os_[0].shape
     cdt = os_[0].dtype
     out = torch.empty(B, T, H, dv, device=os_[0].device, dtype=cdt).permute(0, 2, 1, 3)
     so, sg, sx = os_[0].stride(), g.stride(), out.stride()
     _lib.call("nsa_gate_mix_fwd", *[_ops._ptr(t) for t in os_], so[0], so[1], so[2], _ops._ptr(g), *sg,
-              _ops._ptr(out), sx[0], sx[1], sx[2], B, H, T, dv, _ops._dtype_code(cdt), _ops._stream(out.device))
+              _ops._ptr(out), sx[0], sx[1], sx[2], B, H, T, dv, act, _ops._dtype_code(cdt),
+              _ops._stream(out.device))
     return out
 
 
-def _mix_bwd(dout, os_, g, want_delta=False):
-    """(d o_k = g[..., k] dout for k < 3, dg [B,H,T,3] fp32 with dg[..., k] = sum_d dout o_k,
-    and with want_delta the row sums delta [3,B,H,T] fp32, delta[k] = g[..., k] dg[..., k])."""
+def _mix_bwd(dout, os_, g, want_delta=False, act=0):
+    """With gates a = act(g): (d o_k = a[..., k] dout for k < 3, the fp32 gradient [B,H,T,3]
+    of g (from sum_d dout o_k through the activation), and with want_delta the row sums
+    delta [3,B,H,T] fp32, delta[k] = a[..., k] sum_d dout o_k)."""
     cdt = os_[0].dtype
     B, H, T, dv = os_[0].shape
     d = dout.to(cdt)
@@ -405,7 +414,7 @@ def _mix_bwd(dout, os_, g, want_delta=False):
     sd, so, sg = d.stride(), os_[0].stride(), g.stride()
     _lib.call("nsa_gate_mix_bwd", _ops._ptr(d), sd[0], sd[1], sd[2], *[_ops._ptr(t) for t in os_], so[0], so[1],
               so[2], _ops._ptr(g), *sg, *[_ops._ptr(t) for t in dos], _ops._ptr(dg), _ops._ptr(delta), B, H, T, dv,
-              _ops._dtype_code(cdt), _ops._stream(d.device))
+              act, _ops._dtype_code(cdt), _ops._stream(d.device))
     return (dos, dg, delta) if want_delta else (dos, dg)
 
 
@@ -594,15 +603,17 @@ class NSAAttention(torch.nn.Module):
         else:
             indices, p_cmp, p_slc = sel, None, None
 
-        gates = self.gate_mlp(x).view(B, T, H, 3).permute(0, 2, 1, 3)
-        gates = torch.softmax(gates, dim=-1) if c.gate_mode == "softmax" else torch.sigmoid(gates)
+        gate_logits = self.gate_mlp(x).view(B, T, H, 3).permute(0, 2, 1, 3)
         qk = q.contiguous()
         o = NSACore.apply(qk, k_cmp, v_cmp, block_ends, k_sel.transpose(-1, -2), v_sel, indices,
-                          k_win.transpose(-1, -2), v_win, gates, self.scale, c)
+                          k_win.transpose(-1, -2), v_win, gate_logits, self.scale, c)
         o = o.transpose(1, 2).reshape(B, T, H * dv)
         out = self.dropout(self.o_proj(o))
         info = None
         if output_attentions:
+            with torch.no_grad():  # the activated gates, as returned by the reference
+                gates = (torch.softmax(gate_logits, dim=-1) if c.gate_mode == "softmax"
+                         else torch.sigmoid(gate_logits))
             info = {"compression_scores": p_cmp, "selection_scores": p_slc, "selected_indices": indices,
                     "gates": gates.permute(0, 2, 1, 3)}
         return out, info

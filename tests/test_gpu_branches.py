@@ -321,9 +321,10 @@ def test_strided_views(dev):
     _check(_ops.SLIDING, q, kp, v, do, 0.125, torch.float32, window=50)
 
 
-@pytest.mark.parametrize("dk,dtype", [(64, torch.float32), (192, torch.bfloat16), (48, torch.float32)])
-def test_nsa_core_matches_separate_functions(dev, dk, dtype):
-    """NSACore (the module's three branches and gated mix, with the branch backwards
+@pytest.mark.parametrize("dk,dtype,gate_mode", [(64, torch.float32, "sigmoid"), (192, torch.bfloat16, "sigmoid"),
+                                                (48, torch.float32, "softmax")])
+def test_nsa_core_matches_separate_functions(dev, dk, dtype, gate_mode):
+    """NSACore (the module's three branches, gate activation and gated mix, with the branch backwards
     taking the mix's row sums and summing dQ in the dQ kernels) against
     CompressionAttention / SelectionAttention / SlidingWindowAttention and GatedMix
     applied separately (autograd summing dQ): same output, same gradients.  dk = 48 is
@@ -341,14 +342,15 @@ def test_nsa_core_matches_separate_functions(dev, dk, dtype):
     vs = torch.randn(B, G, T, dv, generator=g).to(dtype)
     kw = torch.randn(B, G, dk, T, generator=g).to(dtype)
     vw = torch.randn(B, G, T, dv, generator=g).to(dtype)
-    gates = torch.sigmoid(torch.randn(B, H, T, 3, generator=g)).to(dtype)
+    gate_logits = torch.randn(B, H, T, 3, generator=g).to(dtype)
     idx = _random_indices(12, B, G, T, T, lp, n).to(dev)
     do = torch.randn(B, H, T, dv, generator=g).to(dtype).to(dev)
-    cfg = NSAConfig(head_dim_qk=dk, head_dim_v=dv, n_heads=H, n_kv_groups=G, l=l, d=d, l_prime=lp, n=n, w=w)
+    cfg = NSAConfig(head_dim_qk=dk, head_dim_v=dv, n_heads=H, n_kv_groups=G, l=l, d=d, l_prime=lp, n=n, w=w,
+                    gate_mode=gate_mode)
     scale = 1 / math.sqrt(dk)
 
     def leaves():
-        return [t.to(dev).requires_grad_() for t in (q, kc, vc, ks, vs, kw, vw, gates)]
+        return [t.to(dev).requires_grad_() for t in (q, kc, vc, ks, vs, kw, vw, gate_logits)]
 
     a = leaves()
     out_a = NSACore.apply(a[0], a[1], a[2], be.to(dev), a[3], a[4], idx, a[5], a[6], a[7], scale, cfg)
@@ -357,9 +359,10 @@ def test_nsa_core_matches_separate_functions(dev, dk, dtype):
     outs_b = (CompressionAttention.apply(b[0], b[1], b[2], be.to(dev), scale, cfg),
               SelectionAttention.apply(b[0], b[3], b[4], idx, scale, cfg),
               SlidingWindowAttention.apply(b[0], b[5], b[6], scale, w, cfg))
-    out_b = GatedMix.apply(*outs_b, b[7])
+    gb = torch.softmax(b[7].float(), dim=-1) if gate_mode == "softmax" else torch.sigmoid(b[7].float())
+    out_b = GatedMix.apply(*outs_b, gb.to(dtype) if dtype == torch.float32 else gb)
     out_b.backward(do)
     tol = 2e-2 if dtype == torch.bfloat16 else 1e-5
-    assert rel_err(_np(out_a), _np(out_b)) == 0.0
+    assert rel_err(_np(out_a), _np(out_b)) < (1e-2 if dtype == torch.bfloat16 else 1e-6)
     for x, y in zip(a, b):
         assert rel_err(_np(x.grad), _np(y.grad)) < tol
