@@ -156,6 +156,56 @@ int nsa_sparse_selection_bwd(const void* Q, const void* K, const void* V, const 
                              int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream);
 
+/* Decode extensions (no counterpart in the reference): the forward entry points and
+ * the scoring with the query rows placed at absolute positions q_offset ..
+ * q_offset + n_ctx_q - 1 of the key sequence (row r of Q / Out / L / M / indices is
+ * position q_offset + r; masks, fixed blocks and the all-invalid fallback use positions).
+ * For single-token decode over a cache: n_ctx_q = 1, q_offset = cache length - 1.
+ * The sliding-window form also takes the key length n_ctx_kv (the reference kernel
+ * assumes n_ctx_kv = n_ctx).  With q_offset = 0 (and n_ctx_kv = n_ctx) each behaves
+ * exactly as the entry point it extends. */
+int nsa_sliding_window_fwd_ex(const void* Q, const void* K, const void* V, void* Out, float sm_scale, float* L, float* M,
+                           int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_qk,
+                           int64_t stride_kz, int64_t stride_kg, int64_t stride_kn, int64_t stride_kk,
+                           int64_t stride_vz, int64_t stride_vg, int64_t stride_vn, int64_t stride_vk,
+                           int64_t stride_oz, int64_t stride_oh, int64_t stride_om, int64_t stride_ok,
+                           int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t stride_mz,
+                           int64_t stride_mh, int64_t stride_mm, int Z, int H, int n_kv_groups, int n_ctx,
+                           int window_size, int head_dim_qk, int head_dim_v, int dtype,
+                           int n_ctx_kv, int q_offset, void* workspace,
+                           size_t workspace_bytes, nsa_stream_t stream);
+
+int nsa_compression_fwd_ex(const void* Q, const void* K_compressed, const void* V_compressed, const int32_t* Block_ends,
+                        void* Out, float sm_scale, float* L, float* M, int64_t stride_qz, int64_t stride_qh,
+                        int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
+                        int64_t stride_kn, int64_t stride_kk, int64_t stride_vz, int64_t stride_vg,
+                        int64_t stride_vn, int64_t stride_vk, int64_t stride_oz, int64_t stride_oh,
+                        int64_t stride_om, int64_t stride_ok, int64_t stride_lz, int64_t stride_lh,
+                        int64_t stride_lm, int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, int Z, int H,
+                        int n_kv_groups, int n_ctx_q, int n_blocks, int head_dim_qk, int head_dim_v, int dtype,
+                        int q_offset, void* workspace, size_t workspace_bytes, nsa_stream_t stream);
+
+int nsa_sparse_selection_fwd_ex(const void* Q, const void* K, const void* V, const void* Block_indices, void* Out,
+                             float sm_scale, float* L, float* M, int64_t stride_qz, int64_t stride_qh,
+                             int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
+                             int64_t stride_kn, int64_t stride_kk, int64_t stride_vz, int64_t stride_vg,
+                             int64_t stride_vn, int64_t stride_vk, int64_t stride_oz, int64_t stride_oh,
+                             int64_t stride_om, int64_t stride_ok, int64_t stride_bz, int64_t stride_bg,
+                             int64_t stride_bm, int64_t stride_bn, int64_t stride_lz, int64_t stride_lh,
+                             int64_t stride_lm, int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, int Z, int H,
+                             int n_kv_groups, int n_ctx_q, int n_ctx_kv, int n_slots, int block_size_selection,
+                             int is_causal, int index_is_int64, int all_invalid_fallback, int head_dim_qk,
+                             int head_dim_v, int dtype, int q_offset, void* workspace, size_t workspace_bytes,
+                             nsa_stream_t stream);
+
+int nsa_score_topn_ex(const void* q, const void* k_cmp, const int32_t* Block_ends, int64_t* out_idx, float* p_cmp,
+                   float* p_slc, int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_qk,
+                   int64_t stride_kz, int64_t stride_kg, int64_t stride_kk, int64_t stride_kn, int64_t stride_iz,
+                   int64_t stride_ig, int64_t stride_im, int64_t stride_in, int Z, int H, int n_kv_groups, int n_ctx,
+                   int head_dim_qk, int n_blocks, int l, int d, int l_prime, int n, int include_fixed, int n_fixed,
+                   int dtype, float scale,
+                   int q_offset, void* workspace, size_t workspace_bytes, nsa_stream_t stream);
+
 /* Extensions (no counterpart in the reference): the three backward entry points above
  * with two more arguments, for callers that run the three branches over one query
  * tensor and already hold the row sums, such as the NSA module:

@@ -42,6 +42,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 struct Shape {
   int br, dtype, Z, H, G, Tq, Tkv, dk, dv, nslots, lprime;
   int window = 0;
+  int q0 = 0;  // absolute position of query row 0 (forward extensions)
   int hpg() const { return H / G; }
   int Tp() const { return ((Tkv + 63) / 64) * 64 + 64; }
   int esz() const { return dtype == NSA_F32 ? 4 : 2; }
@@ -115,6 +116,7 @@ bool row_ok(const void* p, int64_t inner, int64_t s0, int64_t s1, int64_t s2, in
 
 int validate(const Shape& s) {
   if (s.dtype != NSA_F32 && s.dtype != NSA_BF16) return fail(NSA_ERR_INVALID, "dtype %d not supported", s.dtype);
+  if (s.q0 < 0) return fail(NSA_ERR_INVALID, "q_offset=%d must be >= 0", s.q0);
   if (s.Z <= 0 || s.H <= 0 || s.G <= 0 || s.Tq < 0 || s.Tkv < 0)
     return fail(NSA_ERR_INVALID, "bad shape Z=%d H=%d G=%d Tq=%d Tkv=%d", s.Z, s.H, s.G, s.Tq, s.Tkv);
   if (s.H % s.G) return fail(NSA_ERR_INVALID, "H=%d not a multiple of n_kv_groups=%d", s.H, s.G);
@@ -138,6 +140,7 @@ AttnArgs base_args(const Shape& s, float scale) {
   a.Tq = s.Tq;
   a.Tkv = s.Tkv;
   a.Tp = s.Tp();
+  a.q0 = s.q0;
   a.scale = scale;
   a.lprime = s.lprime > 0 ? s.lprime : 1;
   a.nslots = s.nslots;
@@ -199,7 +202,7 @@ int run_fwd(const Shape& s, const FwdIO& io, float scale, int window, const int3
                 nullptr, nullptr, const_cast<void*>(a.vcf), st);
   if (s.br == kSelection) {
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
-                     s.Tkv, fallback, causal, at<int>(ws, L.clean), nullptr, s.nblk(), st);
+                     s.Tkv, fallback, causal, at<int>(ws, L.clean), nullptr, s.nblk(), s.q0, st);
     a.sel = at<int>(ws, L.clean);
   }
   if ((rc = check_hip("prep"))) return rc;
@@ -293,7 +296,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
                 nullptr, nullptr, const_cast<void*>(a.vrf), nullptr, st);
   if (s.br == kSelection) {
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
-                     s.Tkv, fallback, causal, at<int>(ws, L.clean), at<int>(ws, L.chunk), s.nblk(), st);
+                     s.Tkv, fallback, causal, at<int>(ws, L.clean), at<int>(ws, L.chunk), s.nblk(), 0, st);
     launch_sel_csr(at<int>(ws, L.clean), at<int>(ws, L.chunk), s.Z, s.G, s.Tq, s.nslots, s.nblk(),
                    at<int>(ws, L.csr_off), at<int>(ws, L.csr_t), at<int>(ws, L.seg_off), s.seg(), st);
     a.sel = at<int>(ws, L.clean);
@@ -542,6 +545,64 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
   if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
   const int64_t sidx[4] = {stride_bz, stride_bg, stride_bm, stride_bn};
   return run_bwd(s, io, sm_scale, 0, nullptr, Block_indices, sidx, index_is_int64, all_invalid_fallback,
+                 is_causal ? 1 : 0, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+int nsa_sliding_window_fwd_ex(const void* Q, const void* K, const void* V, void* Out, float sm_scale, float* L,
+float* M,
+                           int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_qk,
+                           int64_t stride_kz, int64_t stride_kg, int64_t stride_kn, int64_t stride_kk,
+                           int64_t stride_vz, int64_t stride_vg, int64_t stride_vn, int64_t stride_vk,
+                           int64_t stride_oz, int64_t stride_oh, int64_t stride_om, int64_t stride_ok,
+                           int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t stride_mz,
+                           int64_t stride_mh, int64_t stride_mm, int Z, int H, int n_kv_groups, int n_ctx,
+                           int window_size, int head_dim_qk, int head_dim_v, int dtype, int n_ctx_kv, int q_offset,
+                           void* workspace,
+                           size_t workspace_bytes, nsa_stream_t stream) {
+  NSA_FWD_IO
+  Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx_kv, head_dim_qk, head_dim_v, 0, 64, window_size};
+  s.q0 = q_offset;
+  return run_fwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
+                 (hipStream_t)stream);
+}
+
+int nsa_compression_fwd_ex(const void* Q, const void* K, const void* V, const int32_t* Block_ends, void* Out,
+                        float sm_scale, float* L, float* M, int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                        int64_t stride_qk, int64_t stride_kz, int64_t stride_kg, int64_t stride_kn,
+                        int64_t stride_kk, int64_t stride_vz, int64_t stride_vg, int64_t stride_vn,
+                        int64_t stride_vk, int64_t stride_oz, int64_t stride_oh, int64_t stride_om,
+                        int64_t stride_ok, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm,
+                        int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, int Z, int H, int n_kv_groups,
+                        int n_ctx_q, int n_blocks, int head_dim_qk, int head_dim_v, int dtype, int q_offset,
+                        void* workspace,
+                        size_t workspace_bytes, nsa_stream_t stream) {
+  NSA_FWD_IO
+  Shape s{kCompression, dtype, Z, H, n_kv_groups, n_ctx_q, n_blocks, head_dim_qk, head_dim_v, 0, 64};
+  s.q0 = q_offset;
+  if (n_blocks > 0 && !Block_ends) return fail(NSA_ERR_INVALID, "Block_ends is null");
+  return run_fwd(s, io, sm_scale, 0, Block_ends, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
+                 (hipStream_t)stream);
+}
+
+int nsa_sparse_selection_fwd_ex(const void* Q, const void* K, const void* V, const void* Block_indices, void* Out,
+                             float sm_scale, float* L, float* M, int64_t stride_qz, int64_t stride_qh,
+                             int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
+                             int64_t stride_kn, int64_t stride_kk, int64_t stride_vz, int64_t stride_vg,
+                             int64_t stride_vn, int64_t stride_vk, int64_t stride_oz, int64_t stride_oh,
+                             int64_t stride_om, int64_t stride_ok, int64_t stride_bz, int64_t stride_bg,
+                             int64_t stride_bm, int64_t stride_bn, int64_t stride_lz, int64_t stride_lh,
+                             int64_t stride_lm, int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, int Z, int H,
+                             int n_kv_groups, int n_ctx_q, int n_ctx_kv, int n_slots, int block_size_selection,
+                             int is_causal, int index_is_int64, int all_invalid_fallback, int head_dim_qk,
+                             int head_dim_v, int dtype, int q_offset, void* workspace, size_t workspace_bytes,
+                             nsa_stream_t stream) {
+  NSA_FWD_IO
+  Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
+          block_size_selection};
+  s.q0 = q_offset;
+  if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
+  const int64_t sidx[4] = {stride_bz, stride_bg, stride_bm, stride_bn};
+  return run_fwd(s, io, sm_scale, 0, nullptr, Block_indices, sidx, index_is_int64, all_invalid_fallback,
                  is_causal ? 1 : 0, workspace, workspace_bytes, (hipStream_t)stream);
 }
 

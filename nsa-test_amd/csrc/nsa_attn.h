@@ -57,6 +57,7 @@ struct AttnArgs {
   int64_t sdv_b, sdv_g, sdv_t, sdv_d;
   float* partial;  // [items][64][DK+DV]
   int items_per_bg;
+  int q0;  // absolute position of query row 0 (0 unless a caller decodes past a cache)
   int seg;  // query entries per dK/dV work item
   // shapes
   int B, H, G, hpg, Tq, Tkv;

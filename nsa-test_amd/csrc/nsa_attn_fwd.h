@@ -74,8 +74,9 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   const int hpg = a.hpg;
   const int ncols = a.Tq * hpg;
   const int col_base = blockIdx.x * kFwdCols;
-  const int t_first = col_base / hpg;
-  const int t_last = min(a.Tq - 1, (col_base + kFwdCols - 1) / hpg);
+  // positions are absolute (query row r is at a.q0 + r); rows are addressed relatively
+  const int t_first = col_base / hpg + a.q0;
+  const int t_last = min(a.Tq - 1, (col_base + kFwdCols - 1) / hpg) + a.q0;
   const float scale2 = a.scale * kLog2e;
 
   const S* qbase = reinterpret_cast<const S*>(a.q);
@@ -97,8 +98,8 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
     colv[s] = f < ncols;
     colt[s] = colv[s] ? f / hpg : 0;
     colh[s] = colv[s] ? grp * hpg + f % hpg : 0;
-    sub_t0[s] = f0 / hpg;
-    sub_t1[s] = f0 < ncols ? min(a.Tq - 1, (f0 + 15) / hpg) : -1;
+    sub_t0[s] = f0 / hpg + a.q0;
+    sub_t1[s] = f0 < ncols ? min(a.Tq - 1, (f0 + 15) / hpg) + a.q0 : -1;
     const S* qp = qbase + b * a.sq_b + (int64_t)colh[s] * a.sq_h + (int64_t)colt[s] * a.sq_t;
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc)
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
     uint4 pf[NSUB][64 / CK];
 #pragma unroll
     for (int s = 0; s < NSUB; ++s) {
-      const int t = colt[s];
+      const int t = colt[s] + a.q0;  // absolute position
       // sliding: the column sees keys [kmin_s, kmin_s + kspan_s) (branch-free test)
       const int kmin_s = max(t - a.window + 1, 0);
       const uint32_t kspan_s = colv[s] ? (uint32_t)max(0, min(t, a.Tkv - 1) + 1 - kmin_s) : 0u;

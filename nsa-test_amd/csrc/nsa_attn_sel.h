@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const bool colv = f < ncols;
   const int colt = colv ? f / hpg : w.t_first;
   const int colh = colv ? grp * hpg + f % hpg : grp * hpg;
-  const int t_last = w.t_first + w.nt - 1;
+  const int t_last = w.t_first + w.nt - 1 + a.q0;  // absolute positions: row r is at a.q0 + r
   const int* mylst = lst + (colt - w.t_first) * a.nslots;
 
   const S* qp = reinterpret_cast<const S*>(a.q) + b * a.sq_b + (int64_t)colh * a.sq_h + (int64_t)colt * a.sq_t;
@@ -182,8 +182,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 
     const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
     // end of the keys of this block the lane's column sees (blk_lo when none)
-    const int kend = colsel ? max(blk_lo, a.causal ? min(blk_hi, colt + 1) : blk_hi) : blk_lo;
-    const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first) && key0 >= blk_lo &&
+    const int kend = colsel ? max(blk_lo, a.causal ? min(blk_hi, colt + a.q0 + 1) : blk_hi) : blk_lo;
+    const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first + a.q0) && key0 >= blk_lo &&
                              key0 + 63 < blk_hi && f0 + kSelWaveCols <= ncols;
     float mx = -INFINITY;
     // lane-visible keys of this block: [blk_lo, kend); branch-free test per element

@@ -23,7 +23,7 @@ void launch_partial_reduce(int dtype, int dk, int dv, int br, const AttnArgs& a,
 // selection index cleaning and block -> query CSR
 void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g, int64_t si_t, int64_t si_n, int B,
                       int G, int Tq, int n_in, int nslots, int lprime, int Tkv, int fallback, int causal, int* clean,
-                      int* chunk_cnt, int nblk, hipStream_t st);
+                      int* chunk_cnt, int nblk, int q0, hipStream_t st);
 void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int nslots, int nblk, int* csr_off,
                     int* csr_t, int* seg_off, int seg, hipStream_t st);
 int sel_csr_chunks(int Tq);

@@ -73,6 +73,7 @@ struct ScoreArgs {
   float scale;
   int a, s, nsel, lprime, n, include_fixed;
   int ncs;  // logit row stride: NB rounded up to 64
+  int q0;   // absolute position of query row 0 (positions decide visibility and fixed blocks)
 };
 
 constexpr int kMaxRows = 64;    // heads per group
@@ -135,7 +136,7 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
   const int hpg = a.hpg;
   const int Rall = a.T * hpg;
   const int row0 = blockIdx.x * kLgTM, col0 = blockIdx.y * kLgTN;
-  const int t_last = min(a.T - 1, (row0 + kLgTM - 1) / hpg);
+  const int t_last = min(a.T - 1, (row0 + kLgTM - 1) / hpg) + a.q0;
   const int ncomp = score_ncomp(a, t_last, &s_nc);
   if (col0 >= ncomp) return;  // workgroup-uniform
 
@@ -252,8 +253,9 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
   int* sbe = reinterpret_cast<int*>(lds);
   for (int i = tid; i < NQ * 256; i += blockDim.x) sbe[i] = i < NB ? a.block_ends[i] : 0x7fffffff;
   __syncthreads();
-  const int t = blockIdx.x * NW + wave;
+  const int t = blockIdx.x * NW + wave;  // row; its position is ta
   if (t >= a.T) return;  // whole wave; no barrier follows
+  const int ta = t + a.q0;
   const int nsel4 = (nsel + 3) & ~3;
   float* wb = lds + NQ * 256 + wave * (NQ * 256 + nsel4);  // generic remap only
   float* wag = wb + NQ * 256;
@@ -263,10 +265,10 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
   for (int s = 0; s < NQ; ++s) {
     const int4 be = *reinterpret_cast<const int4*>(sbe + 256 * s + 4 * lane);
     const int i = 256 * s + 4 * lane;
-    if (be.x <= t) vis_hi = i + 1;
-    if (be.y <= t) vis_hi = i + 2;
-    if (be.z <= t) vis_hi = i + 3;
-    if (be.w <= t) vis_hi = i + 4;
+    if (be.x <= ta) vis_hi = i + 1;
+    if (be.y <= ta) vis_hi = i + 2;
+    if (be.z <= ta) vis_hi = i + 3;
+    if (be.w <= ta) vis_hi = i + 4;
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) vis_hi = max(vis_hi, __shfl_xor(vis_hi, off));
@@ -307,10 +309,10 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
         continue;
       }
       const int4 be = *reinterpret_cast<const int4*>(sbe + 256 * s + 4 * lane);
-      v[s][0] = be.x <= t ? cur[s].x : -INFINITY;
-      v[s][1] = be.y <= t ? cur[s].y : -INFINITY;
-      v[s][2] = be.z <= t ? cur[s].z : -INFINITY;
-      v[s][3] = be.w <= t ? cur[s].w : -INFINITY;
+      v[s][0] = be.x <= ta ? cur[s].x : -INFINITY;
+      v[s][1] = be.y <= ta ? cur[s].y : -INFINITY;
+      v[s][2] = be.z <= ta ? cur[s].z : -INFINITY;
+      v[s][3] = be.w <= ta ? cur[s].w : -INFINITY;
       mx = fmaxf(mx, fmaxf(fmaxf(v[s][0], v[s][1]), fmaxf(v[s][2], v[s][3])));
     }
     if (vis_hi == 0) {  // no visible block (wave-uniform): block 0 is scored
@@ -446,8 +448,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
   }
   // candidates: fixed [0, max(0,(t-l')/l'), t/l'] then the top-k.  The top-k are
   // distinct, so a candidate can only repeat one of the fixed ones before it.
-  const int f1 = t >= a.lprime ? (t - a.lprime) / a.lprime : 0;
-  const int f2 = t / a.lprime;
+  const int f1 = ta >= a.lprime ? (ta - a.lprime) / a.lprime : 0;
+  const int f2 = ta / a.lprime;
   const int ncand = nc + kk;  // <= 67 (n <= 64)
   int64_t* o = a.out + b * a.so_b + g * a.so_g + (int64_t)t * a.so_t;
   int kept = 0;  // candidates kept so far (wave-uniform)
@@ -544,19 +546,21 @@ extern "C" size_t nsa_score_topn_workspace_size(int Z, int H, int n_kv_groups, i
   return (size_t)Z * H * n_ctx * nsa::score_ncs(n_blocks) * 4;
 }
 
-extern "C" int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* block_ends, int64_t* out_idx,
+static int score_topn_impl(const void* q, const void* k_cmp, const int32_t* block_ends, int64_t* out_idx,
                               float* p_cmp, float* p_slc, int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
                               int64_t stride_qk, int64_t stride_kz, int64_t stride_kg, int64_t stride_kk,
                               int64_t stride_kn, int64_t stride_iz, int64_t stride_ig, int64_t stride_im,
                               int64_t stride_in, int Z, int H, int n_kv_groups, int n_ctx, int head_dim_qk,
                               int n_blocks, int l, int d, int l_prime, int n, int include_fixed, int n_fixed,
-                              int dtype, float scale, void* workspace, size_t workspace_bytes, nsa_stream_t stream) {
+                              int dtype, float scale,
+                              int q_offset, void* workspace, size_t workspace_bytes, nsa_stream_t stream) {
   using namespace nsa;
   if (dtype != NSA_F32 && dtype != NSA_BF16) return nsa::set_error(NSA_ERR_INVALID, "dtype not supported");
   if (Z <= 0 || H <= 0 || n_kv_groups <= 0 || H % n_kv_groups || n_ctx < 0 || head_dim_qk <= 0 || n_blocks < 0)
     return nsa::set_error(NSA_ERR_INVALID, "bad shape");
   if (d <= 0 || l <= 0 || l_prime <= 0 || l % d || l_prime % d)
     return nsa::set_error(NSA_ERR_INVALID, "need l % d == 0 and l_prime % d == 0");
+  if (q_offset < 0) return nsa::set_error(NSA_ERR_INVALID, "q_offset must be >= 0");
   if (n < 0 || n > 64) return nsa::set_error(NSA_ERR_INVALID, "n outside [0, 64]");
   {
     const int esz = dtype == NSA_F32 ? 4 : 2;
@@ -616,6 +620,7 @@ extern "C" int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* b
   a.lprime = l_prime;
   a.n = n;
   a.include_fixed = include_fixed && n_fixed > 0;
+  a.q0 = q_offset;
   if (a.hpg > kMaxRows) return nsa::set_error(NSA_ERR_UNSUPPORTED, "more than 64 heads per group");
   int rc;
   {
@@ -630,4 +635,35 @@ extern "C" int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* b
   }
   if (rc == 2) return nsa::set_error(NSA_ERR_HIP, hipGetErrorString(hipGetLastError()));
   return NSA_OK;
+}
+
+extern "C" int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* block_ends, int64_t* out_idx,
+                              float* p_cmp, float* p_slc, int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                              int64_t stride_qk, int64_t stride_kz, int64_t stride_kg, int64_t stride_kk,
+                              int64_t stride_kn, int64_t stride_iz, int64_t stride_ig, int64_t stride_im,
+                              int64_t stride_in, int Z, int H, int n_kv_groups, int n_ctx, int head_dim_qk,
+                              int n_blocks, int l, int d, int l_prime, int n, int include_fixed, int n_fixed,
+                              int dtype, float scale, void* workspace, size_t workspace_bytes, nsa_stream_t stream) {
+  return score_topn_impl(q, k_cmp, block_ends, out_idx, p_cmp, p_slc, stride_qz, stride_qh, stride_qm, stride_qk,
+                         stride_kz, stride_kg, stride_kk, stride_kn, stride_iz, stride_ig, stride_im, stride_in, Z,
+                         H, n_kv_groups,
+                         n_ctx, head_dim_qk, n_blocks, l, d, l_prime, n, include_fixed, n_fixed, dtype, scale, 0,
+                         workspace,
+                         workspace_bytes, stream);
+}
+
+extern "C" int nsa_score_topn_ex(const void* q, const void* k_cmp, const int32_t* block_ends, int64_t* out_idx,
+                              float* p_cmp, float* p_slc, int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                              int64_t stride_qk, int64_t stride_kz, int64_t stride_kg, int64_t stride_kk,
+                              int64_t stride_kn, int64_t stride_iz, int64_t stride_ig, int64_t stride_im,
+                              int64_t stride_in, int Z, int H, int n_kv_groups, int n_ctx, int head_dim_qk,
+                              int n_blocks, int l, int d, int l_prime, int n, int include_fixed, int n_fixed,
+                              int dtype, float scale,
+                              int q_offset, void* workspace, size_t workspace_bytes, nsa_stream_t stream) {
+  return score_topn_impl(q, k_cmp, block_ends, out_idx, p_cmp, p_slc, stride_qz, stride_qh, stride_qm, stride_qk,
+                         stride_kz, stride_kg, stride_kk, stride_kn, stride_iz, stride_ig, stride_im, stride_in, Z,
+                         H, n_kv_groups,
+                         n_ctx, head_dim_qk, n_blocks, l, d, l_prime, n, include_fixed, n_fixed, dtype, scale,
+                         q_offset, workspace,
+                         workspace_bytes, stream);
 }

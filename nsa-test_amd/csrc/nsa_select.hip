@@ -29,7 +29,7 @@ template <int SEG>
 __global__ __launch_bounds__(256) void sel_clean_kernel(const void* idx, int idx_is64, int64_t si_b, int64_t si_g,
                                                         int64_t si_t, int64_t si_n, int G, int Tq, int n_in,
                                                         int nslots, int lprime, int nblk, int fallback, int causal,
-                                                        int* clean, int* chunk_cnt, int nchunks) {
+                                                        int* clean, int* chunk_cnt, int nchunks, int q0) {
   constexpr int kNone = 0x7fffffff;
   const int t = (int)(((int64_t)blockIdx.x * 256 + threadIdx.x) / SEG);
   const int s = threadIdx.x % SEG;
@@ -45,8 +45,9 @@ __global__ __launch_bounds__(256) void sel_clean_kernel(const void* idx, int idx
   int any_valid = raw >= 0;
 #pragma unroll
   for (int o = 1; o < SEG; o <<= 1) any_valid |= __shfl_xor(any_valid, o, SEG);
-  if (fallback && !any_valid && s < n_in) raw = t / lprime;
-  const bool ok = row_ok && raw >= 0 && raw < nblk && !(causal && (int64_t)raw * lprime > t);
+  const int ta = t + q0;  // absolute position of row t
+  if (fallback && !any_valid && s < n_in) raw = ta / lprime;
+  const bool ok = row_ok && raw >= 0 && raw < nblk && !(causal && (int64_t)raw * lprime > ta);
   const int key = ok ? raw : kNone;
   bool dup = false;
 #pragma unroll
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(64) void sel_csr_fill_kernel(const int* clean, cons
 
 void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g, int64_t si_t, int64_t si_n, int B,
                       int G, int Tq, int n_in, int nslots, int lprime, int Tkv, int fallback, int causal, int* clean,
-                      int* chunk_cnt, int nblk, hipStream_t st) {
+                      int* chunk_cnt, int nblk, int q0, hipStream_t st) {
   const int nchunks = (Tq + kCsrChunk - 1) / kCsrChunk;
   if (chunk_cnt) {
     const int64_t n = (int64_t)B * G * nchunks * nblk;
@@ -179,13 +180,13 @@ void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g,
   dim3 grid((unsigned)(((int64_t)Tq * seg + 255) / 256), B * G);
   if (seg == 16)
     hipLaunchKernelGGL(sel_clean_kernel<16>, grid, dim3(256), 0, st, idx, idx_is64, si_b, si_g, si_t, si_n, G, Tq,
-                       n_in, nslots, lprime, nblk, fallback, causal, clean, chunk_cnt, nchunks);
+                       n_in, nslots, lprime, nblk, fallback, causal, clean, chunk_cnt, nchunks, q0);
   else if (seg == 32)
     hipLaunchKernelGGL(sel_clean_kernel<32>, grid, dim3(256), 0, st, idx, idx_is64, si_b, si_g, si_t, si_n, G, Tq,
-                       n_in, nslots, lprime, nblk, fallback, causal, clean, chunk_cnt, nchunks);
+                       n_in, nslots, lprime, nblk, fallback, causal, clean, chunk_cnt, nchunks, q0);
   else
     hipLaunchKernelGGL(sel_clean_kernel<64>, grid, dim3(256), 0, st, idx, idx_is64, si_b, si_g, si_t, si_n, G, Tq,
-                       n_in, nslots, lprime, nblk, fallback, causal, clean, chunk_cnt, nchunks);
+                       n_in, nslots, lprime, nblk, fallback, causal, clean, chunk_cnt, nchunks, q0);
 }
 
 void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int nslots, int nblk, int* csr_off,

@@ -12,6 +12,7 @@ from .kernels import (
     GatedMix,
     NSAAttention,
     NSACore,
+    NSAKVCache,
     NSAConfig,
     SelectionAttention,
     SlidingWindowAttention,

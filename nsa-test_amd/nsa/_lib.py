@@ -50,9 +50,15 @@ SIGNATURES = {
 for _n in ("nsa_sliding_window_bwd", "nsa_compression_bwd", "nsa_sparse_selection_bwd"):
     _r, _a = SIGNATURES[_n]
     SIGNATURES[_n + "_ex"] = (_r, [*_a[:-3], _I, _P, *_a[-3:]])
+# the forward / scoring decode extensions: q_offset (sliding also n_ctx_kv) before the workspace
+for _n, _extra in (("nsa_sliding_window_fwd", [_I, _I]), ("nsa_compression_fwd", [_I]),
+                   ("nsa_sparse_selection_fwd", [_I])):
+    _r, _a = SIGNATURES[_n]
+    SIGNATURES[_n + "_ex"] = (_r, [*_a[:-3], *_extra, *_a[-3:]])
 SIGNATURES.update({
     "nsa_score_topn": (_I, [_P, _P, _P, _P, _P, _P, *[_L] * 12, *[_I] * 13, _F, _P, _Z, _P]),
     "nsa_score_topn_workspace_size": (_Z, [_I] * 7),
+    "nsa_score_topn_ex": (_I, [_P, _P, _P, _P, _P, _P, *[_L] * 12, *[_I] * 13, _F, _I, _P, _Z, _P]),
     "nsa_timing_begin": (_I, [_I]),
     "nsa_timing_end": (_I, [_P, _P]),
     "nsa_gate_mix_fwd": (_I, [_P] * 3 + [_L] * 3 + [_P] + [_L] * 4 + [_P] + [_L] * 3 + [_I] * 6 + [_P]),

@@ -77,9 +77,12 @@ def _branch_extra(branch, Tkv, block_ends, indices, lprime):
 
 
 def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=None, indices=None,
-             lprime: int = 64, causal: bool = True, fallback: bool = False, out=None, L=None, M=None):
+             lprime: int = 64, causal: bool = True, fallback: bool = False, out=None, L=None, M=None,
+             q_offset: int = 0):
     """Forward of one NSA branch.  Returns (out, L, M); `out`, `L`, `M` are written in
-    place when given (with their own strides)."""
+    place when given (with their own strides).  q_offset: absolute position of query row
+    0 in the key sequence (decode past a cache; the sliding window then takes its key
+    length from k)."""
     _check_device(q, k, v, block_ends, indices, out, L, M)
     Z, H, Tq, dk = q.shape
     G, Tkv = k.shape[1], k.shape[2]
@@ -102,19 +105,26 @@ def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=
     common_strides = [*qk.stride(), *kk.stride(), *vk.stride(), *o.stride()]
     lm_strides = [*Lk.stride(), *Mk.stride()]
     st = _stream(dev)
+    if q_offset < 0:
+        raise ValueError("q_offset must be >= 0")
+    # the reference-interface entry points, or their decode extensions
+    dec = q_offset != 0 or (branch == SLIDING and Tq != Tkv)
+    sfx, tail = ("_ex", (int(q_offset), _ptr(ws), ws.numel(), st)) if dec else ("", (_ptr(ws), ws.numel(), st))
     if branch == SLIDING:
-        _lib.call("nsa_sliding_window_fwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(o), float(scale), _ptr(Lk), _ptr(Mk),
-                  *common_strides, *lm_strides, Z, H, G, Tq, int(window), DK, DV, dt, _ptr(ws), ws.numel(), st)
+        if dec:
+            tail = (Tkv, *tail)
+        _lib.call("nsa_sliding_window_fwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(o), float(scale), _ptr(Lk),
+                  _ptr(Mk), *common_strides, *lm_strides, Z, H, G, Tq, int(window), DK, DV, dt, *tail)
     elif branch == COMPRESSION:
         be = block_ends.to(torch.int32).contiguous()
-        _lib.call("nsa_compression_fwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(be), _ptr(o), float(scale), _ptr(Lk),
-                  _ptr(Mk), *common_strides, *lm_strides, Z, H, G, Tq, Tkv, DK, DV, dt, _ptr(ws), ws.numel(), st)
+        _lib.call("nsa_compression_fwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(be), _ptr(o), float(scale),
+                  _ptr(Lk), _ptr(Mk), *common_strides, *lm_strides, Z, H, G, Tq, Tkv, DK, DV, dt, *tail)
     else:
         idx = indices if indices.dtype in (torch.int32, torch.int64) else indices.to(torch.int64)
-        _lib.call("nsa_sparse_selection_fwd", _ptr(qk), _ptr(kk), _ptr(vk), _ptr(idx), _ptr(o), float(scale),
+        _lib.call("nsa_sparse_selection_fwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(idx), _ptr(o), float(scale),
                   _ptr(Lk), _ptr(Mk), *common_strides, *idx.stride(), *lm_strides, Z, H, G, Tq, Tkv, n_slots,
                   int(lprime), int(bool(causal)), int(idx.dtype == torch.int64), int(bool(fallback)), DK, DV, dt,
-                  _ptr(ws), ws.numel(), st)
+                  *tail)
     if direct_out:
         return o, Lk, Mk
     res = o[..., :dv]

@@ -495,11 +495,12 @@ def select_top_k_blocks_per_query_with_gqa(selection_scores: torch.Tensor, confi
 
 
 def score_and_select(q: torch.Tensor, k_compressed: torch.Tensor, block_ends: torch.Tensor, scale: float,
-                     config: NSAConfig, return_scores: bool = False):
+                     config: NSAConfig, return_scores: bool = False, q_offset: int = 0):
     """Fused Eq. 8 -> 9 -> 10 -> top-n on the GPU (one HIP kernel).
 
     q [B,H,T,dk], k_compressed [B,G,dk,N], block_ends [N] -> indices [B,G,T,n] int64
-    (and the fp32 p_cmp [B,H,T,N] / p_slc [B,H,T,nsel] when return_scores)."""
+    (and the fp32 p_cmp [B,H,T,N] / p_slc [B,H,T,nsel] when return_scores).  q_offset:
+    absolute position of query row 0 (decode past a cache)."""
     _ops._check_device(q, k_compressed, block_ends)
     B, H, T, dk = q.shape
     G, N = k_compressed.shape[1], k_compressed.shape[-1]
@@ -515,13 +516,51 @@ def score_and_select(q: torch.Tensor, k_compressed: torch.Tensor, block_ends: to
     ps = torch.empty(B, H, T, nsel, device=q.device, dtype=torch.float32) if return_scores else None
     ws_bytes = _lib.load().nsa_score_topn_workspace_size(B, H, G, T, dk, N, config.n)
     ws = torch.empty(ws_bytes, device=q.device, dtype=torch.uint8)
-    _lib.call("nsa_score_topn", _ops._ptr(qc), _ops._ptr(kc), _ops._ptr(be), _ops._ptr(out), _ops._ptr(pc),
+    if q_offset < 0:
+        raise ValueError("q_offset must be >= 0")
+    name, off = ("nsa_score_topn_ex", (int(q_offset),)) if q_offset else ("nsa_score_topn", ())
+    _lib.call(name, _ops._ptr(qc), _ops._ptr(kc), _ops._ptr(be), _ops._ptr(out), _ops._ptr(pc),
               _ops._ptr(ps), *qc.stride(), *kc.stride(), *out.stride(), B, H, G, T, dk, N, config.l, config.d,
               config.l_prime, config.n, int(bool(config.include_fixed_in_selection)), int(config.n_fixed),
-              _ops._dtype_code(cdt), float(scale), _ops._ptr(ws), ws_bytes, _ops._stream(q.device))
+              _ops._dtype_code(cdt), float(scale), *off, _ops._ptr(ws), ws_bytes, _ops._stream(q.device))
     if return_scores:
         return out, pc, ps
     return out
+
+
+# ========================================================================= decode state
+def _n_pad(n_act: int) -> int:
+    n = 1
+    while n < n_act:
+        n *= 2
+    return n
+
+
+class NSAKVCache:
+    """Decode state of one NSAAttention layer (not in the reference, whose module only
+    runs whole sequences): the projected keys / values of every past token for the three
+    branches ([B,G,max_len,d] each) and the compressed tokens of every completed block
+    (K_cmp [B,G,dk,Np], V_cmp [B,G,Np,dv], block_ends [Np], Np a power of two covering
+    max_len, unused entries 999999 as compress_tokens pads them).  Filled by
+    NSAAttention.prefill and extended one token at a time by NSAAttention.decode."""
+
+    def __init__(self, config: NSAConfig, batch: int, max_len: int, device, dtype):
+        c = config
+        G, dk, dv = c.n_kv_groups, c.head_dim_qk, c.head_dim_v
+        self.config, self.max_len, self.length = config, max_len, 0
+
+        def buf(d):
+            return torch.zeros(batch, G, max_len, d, device=device, dtype=dtype)
+
+        self.k_cmp_in, self.v_cmp_in = buf(dk), buf(dv)
+        self.k_sel, self.v_sel = buf(dk), buf(dv)
+        self.k_win, self.v_win = buf(dk), buf(dv)
+        n_max = max((max_len - c.l) // c.d + 1, 0)
+        np_max = _n_pad(max(n_max, 1))
+        self.K_cmp = torch.zeros(batch, G, dk, np_max, device=device, dtype=dtype)
+        self.V_cmp = torch.zeros(batch, G, np_max, dv, device=device, dtype=dtype)
+        self.block_ends = torch.full((np_max,), 999999, device=device, dtype=torch.int32)
+        self.n_act = 0
 
 
 # ========================================================================= the module
@@ -579,6 +618,86 @@ class NSAAttention(torch.nn.Module):
         Kc = F.pad(Kc, (0, 0, 0, n_pad - n_act)).transpose(-1, -2)               # [B,G,dk,Np]
         Vc = F.pad(Vc, (0, 0, 0, n_pad - n_act))                                 # [B,G,Np,dv]
         return Kc, Vc, block_ends, n_act
+
+    # ------------------------------------------------------------------ decode
+    def _project_kv(self, x: torch.Tensor):
+        c = self.config
+        B, T, _ = x.shape
+        G, dk, dv = c.n_kv_groups, c.head_dim_qk, c.head_dim_v
+
+        def heads(proj, width):
+            return proj(x).view(B, T, G, width).transpose(1, 2)
+
+        return (heads(self.k_compress, dk), heads(self.v_compress, dv), heads(self.k_select, dk),
+                heads(self.v_select, dv), heads(self.k_sliding, dk), heads(self.v_sliding, dv))
+
+    def _add_blocks(self, cache: NSAKVCache) -> None:
+        """Compress every block the cache's tokens complete (block i covers tokens
+        i*d .. i*d+l-1), with compress_tokens on the block's own l tokens."""
+        c = self.config
+        while cache.n_act * c.d + c.l <= cache.length:
+            i = cache.n_act
+            lo = i * c.d
+            kc, vc, _, n1 = self.compress_tokens(cache.k_cmp_in[:, :, lo:lo + c.l], cache.v_cmp_in[:, :, lo:lo + c.l])
+            assert n1 == 1
+            cache.K_cmp[..., i] = kc[..., 0]
+            cache.V_cmp[:, :, i] = vc[:, :, 0]
+            cache.block_ends[i] = lo + c.l - 1
+            cache.n_act += 1
+
+    @torch.no_grad()
+    def prefill(self, hidden_states: torch.Tensor, cache: NSAKVCache) -> None:
+        """Append the projected keys / values of hidden_states [B,T,D] to the cache and
+        compress the blocks they complete (no attention output: run forward for that)."""
+        B, T, _ = hidden_states.shape
+        t0 = cache.length
+        if t0 + T > cache.max_len:
+            raise ValueError(f"cache holds {cache.max_len} tokens, {t0 + T} requested")
+        bufs = (cache.k_cmp_in, cache.v_cmp_in, cache.k_sel, cache.v_sel, cache.k_win, cache.v_win)
+        for dst, src in zip(bufs, self._project_kv(hidden_states)):
+            dst[:, :, t0:t0 + T] = src.to(dst.dtype)
+        cache.length = t0 + T
+        self._add_blocks(cache)
+
+    @torch.no_grad()
+    def decode(self, hidden_states: torch.Tensor, cache: NSAKVCache, output_attentions: bool = False):
+        """One decode step (not in the reference): hidden_states [B,1,D] is the token at
+        position t = cache.length.  Its keys / values join the cache, then the three
+        branches, the gates and the mix run for its query alone at absolute position t,
+        through the HIP kernels' decode extensions (scoring, attention forward with
+        q_offset = t).  Returns (out [B,1,D], info) as forward does for that row."""
+        c = self.config
+        B, T, D = hidden_states.shape
+        if T != 1:
+            raise ValueError("decode takes one token per step")
+        H, dk, dv = c.n_heads, c.head_dim_qk, c.head_dim_v
+        t = cache.length
+        self.prefill(hidden_states, cache)
+        x = hidden_states
+        q = self.q_proj(x).view(B, 1, H, dk).transpose(1, 2).contiguous()           # [B,H,1,dk]
+        n_pad = _n_pad(max(cache.n_act, 1)) if cache.n_act > 0 else 1
+        kc = cache.K_cmp[..., :n_pad]
+        vc = cache.V_cmp[:, :, :n_pad]
+        be = cache.block_ends[:n_pad]
+        sel = score_and_select(q, kc, be, self.scale, c, return_scores=output_attentions, q_offset=t)
+        indices = sel[0] if output_attentions else sel
+        n = t + 1
+        o_c, _, _ = _ops.attn_fwd(COMPRESSION, q, _kt(kc), vc, self.scale, block_ends=be, q_offset=t)
+        o_s, _, _ = _ops.attn_fwd(SELECTION, q, cache.k_sel[:, :, :n], cache.v_sel[:, :, :n], self.scale,
+                                  indices=indices, lprime=c.l_prime, fallback=True, q_offset=t)
+        o_w, _, _ = _ops.attn_fwd(SLIDING, q, cache.k_win[:, :, :n], cache.v_win[:, :, :n], self.scale, window=c.w,
+                                  q_offset=t)
+        gate_logits = self.gate_mlp(x).view(B, 1, H, 3).permute(0, 2, 1, 3)
+        cdt = _ops.compute_dtype(q.dtype)
+        os_ = [o.to(cdt).contiguous() for o in (o_c, o_s, o_w)]
+        o = _mix_fwd(os_, gate_logits.to(cdt), GATE_ACT[c.gate_mode]).to(q.dtype)
+        out = self.o_proj(o.transpose(1, 2).reshape(B, 1, H * dv))
+        info = None
+        if output_attentions:
+            gates = torch.softmax(gate_logits, dim=-1) if c.gate_mode == "softmax" else torch.sigmoid(gate_logits)
+            info = {"compression_scores": sel[1], "selection_scores": sel[2], "selected_indices": indices,
+                    "gates": gates.permute(0, 2, 1, 3)}
+        return out, info
 
     def forward(self, hidden_states: torch.Tensor, attention_mask: Optional[torch.Tensor] = None,
                 output_attentions: bool = False) -> Tuple[torch.Tensor, Optional[Dict]]:
