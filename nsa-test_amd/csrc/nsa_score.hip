@@ -69,6 +69,7 @@ struct ScoreArgs {
   float* p_cmp;  // optional [B,H,T,NB]
   float* p_slc;  // optional [B,H,T,nsel]
   float* lg;     // workspace: scaled logits [B*G][T*hpg][ncs], row r = t * hpg + head in group
+  int* tile_nc;  // workspace: per kLgTM-row tile, the compressed blocks [0, n) it must compute
   int B, H, G, hpg, T, dk, NB;
   float scale;
   int a, s, nsel, lprime, n, include_fixed;
@@ -121,6 +122,17 @@ __device__ __forceinline__ int score_ncomp(const ScoreArgs& a, int t_last, int* 
 // to the tile's last timestep exit at once (the causal triangle is never computed).
 constexpr int kLgTM = 256, kLgTN = 64, kLgEK = 32;
 
+// Per kLgTM-row tile of the logits (rows r = t * hpg + head, the same for every batch
+// and group): the number of compressed blocks holding every block visible to the tile's
+// last timestep, computed once here instead of by each of the tile's column workgroups.
+__global__ __launch_bounds__(256) void score_tile_ncomp_kernel(ScoreArgs a) {
+  __shared__ int s_nc;
+  const int row0 = blockIdx.x * kLgTM;
+  const int t_last = min(a.T - 1, (row0 + kLgTM - 1) / a.hpg) + a.q0;
+  const int nc = score_ncomp(a, t_last, &s_nc);
+  if (threadIdx.x == 0) a.tile_nc[blockIdx.x] = nc;
+}
+
 template <typename S>
 __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
   constexpr int EPL = 16 / sizeof(S);           // elements per 16-byte piece
@@ -129,16 +141,13 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
   constexpr int AP = kLgTM + 4, BP = kLgTN + 4;  // padded LDS rows (16-byte aligned)
   __shared__ __attribute__((aligned(16))) float As[kLgEK * AP];  // [e][row]
   __shared__ __attribute__((aligned(16))) float Bs[kLgEK * BP];  // [e][col]
-  __shared__ int s_nc;
 
   const int tid = threadIdx.x;
   const int bg = blockIdx.z, b = bg / a.G, g = bg % a.G;
   const int hpg = a.hpg;
   const int Rall = a.T * hpg;
   const int row0 = blockIdx.x * kLgTM, col0 = blockIdx.y * kLgTN;
-  const int t_last = min(a.T - 1, (row0 + kLgTM - 1) / hpg) + a.q0;
-  const int ncomp = score_ncomp(a, t_last, &s_nc);
-  if (col0 >= ncomp) return;  // workgroup-uniform
+  if (col0 >= a.tile_nc[blockIdx.x]) return;  // workgroup-uniform: past the visible frontier
 
   // the thread's staging row (A) and column (B)
   const int arow = min(row0 + tid, Rall - 1);
@@ -515,6 +524,7 @@ int launch_score_topn(int dtype, ScoreArgs a, hipStream_t st) {
   {
     const int Rall = a.T * a.hpg;
     const dim3 grid((Rall + kLgTM - 1) / kLgTM, a.ncs / kLgTN, a.B * a.G);
+    hipLaunchKernelGGL(score_tile_ncomp_kernel, dim3(grid.x), dim3(256), 0, st, a);
     if (dtype == kF32) hipLaunchKernelGGL(score_logits_kernel<float>, grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL(score_logits_kernel<uint16_t>, grid, dim3(256), 0, st, a);
     if (hipGetLastError() != hipSuccess) return 2;
@@ -536,14 +546,22 @@ int launch_score_topn(int dtype, ScoreArgs a, hipStream_t st) {
 
 #include "nsa_kernels.h"
 
-// the fp32 logits of every (row, compressed block): Z*H*T rows of NB rounded up to 64
+// the fp32 logits of every (row, compressed block): Z*H*T rows of NB rounded up to 64,
+// then one int per kLgTM-row logits tile of a group
+static size_t score_ws_logits(int Z, int H, int n_ctx, int n_blocks) {
+  return (size_t)Z * H * n_ctx * nsa::score_ncs(n_blocks) * 4;
+}
+static size_t score_ws_bytes(int Z, int H, int G, int n_ctx, int n_blocks) {
+  const size_t ntiles = ((size_t)n_ctx * (H / G) + nsa::kLgTM - 1) / nsa::kLgTM;
+  return score_ws_logits(Z, H, n_ctx, n_blocks) + ((ntiles * 4 + 255) & ~(size_t)255);
+}
+
 extern "C" size_t nsa_score_topn_workspace_size(int Z, int H, int n_kv_groups, int n_ctx, int head_dim_qk,
                                                 int n_blocks, int n) {
-  (void)n_kv_groups;
   (void)head_dim_qk;
   (void)n;
-  if (Z <= 0 || H <= 0 || n_ctx <= 0 || n_blocks < 0) return 0;
-  return (size_t)Z * H * n_ctx * nsa::score_ncs(n_blocks) * 4;
+  if (Z <= 0 || H <= 0 || n_kv_groups <= 0 || H % n_kv_groups || n_ctx <= 0 || n_blocks < 0) return 0;
+  return score_ws_bytes(Z, H, n_kv_groups, n_ctx, n_blocks);
 }
 
 static int score_topn_impl(const void* q, const void* k_cmp, const int32_t* block_ends, int64_t* out_idx,
@@ -578,7 +596,7 @@ static int score_topn_impl(const void* q, const void* k_cmp, const int32_t* bloc
   }
   if (n_ctx == 0) return NSA_OK;
   {
-    const size_t need = (size_t)Z * H * n_ctx * score_ncs(n_blocks) * 4;
+    const size_t need = score_ws_bytes(Z, H, n_kv_groups, n_ctx, n_blocks);
     if (workspace_bytes < need || (need && (!workspace || ((uintptr_t)workspace) % 16))) {
       char msg[128];
       snprintf(msg, sizeof(msg), "workspace of %zu bytes (16-byte aligned) required, %zu given", need,
@@ -588,6 +606,7 @@ static int score_topn_impl(const void* q, const void* k_cmp, const int32_t* bloc
   }
   ScoreArgs a{};
   a.lg = static_cast<float*>(workspace);
+  a.tile_nc = reinterpret_cast<int*>(static_cast<char*>(workspace) + score_ws_logits(Z, H, n_ctx, n_blocks));
   a.q = q;
   a.sq_b = stride_qz;
   a.sq_h = stride_qh;
