@@ -1,8 +1,8 @@
 // Fused selection scoring on gfx950: Eq. 8 (compressed-attention probabilities),
 // Eq. 9 (triangular remap to selection blocks), Eq. 10 (GQA head sum) and the top-n
 // with fixed blocks, in two kernels:
-//   score_logits_kernel  the Eq. 8 logits of every (row, visible compressed block) as a
-//                        register-tiled fp32 GEMM into the caller's workspace;
+//   score_logits_kernel  the Eq. 8 logits of every (row, visible compressed block) as an
+//                        fp32 MFMA GEMM into the caller's workspace;
 //   score_rows_kernel    softmax, Eq. 9, Eq. 10 and the top-n, one wave per
 //                        (batch, group, timestep).
 // Besides the workspace only the n indices per (b, g, t) are written (and, when the
@@ -112,14 +112,18 @@ __device__ __forceinline__ int score_ncomp(const ScoreArgs& a, int t_last, int* 
 }
 
 // ---------------------------------------------------------------- logits ----
-// Eq. 8 logits of one group as a register-tiled fp32 GEMM on the vector ALU:
+// Eq. 8 logits of one group as an fp32 GEMM on the matrix cores:
 // lg[r][i] = scale * (sum over e = 0..dk-1 of q[r][e] k[i][e]), each element one
 // sequential fma chain in e order (the accumulation order the indices are defined by).
-// Workgroup = 256 query rows x 64 compressed blocks; the operands are staged through
-// LDS as fp32 in EK-feature chunks (the next chunk is loaded into registers while the
-// current one is used) and each lane owns an 8 x 8 tile, so one feature step costs a
-// lane four 16-byte LDS reads for 64 FMAs.  Column tiles past the last block visible
-// to the tile's last timestep exit at once (the causal triangle is never computed).
+// v_mfma_f32_16x16x4_f32 computes D = C + sum_k A[m][k] B[k][n] as four IEEE fp32
+// fmas in k order 0..3, each rounded (subnormals kept), so the chain of MFMAs over the
+// feature steps e = 4j..4j+3 (slot k = e - 4j) is exactly that fma chain.
+// Workgroup = 256 query rows x 64 compressed blocks, 4 waves of 64 rows x 64 blocks
+// (4 x 4 MFMA tiles, blocks as the M operand so a lane holds 4 consecutive blocks of
+// one row); the operands are staged through LDS as fp32 in EK-feature chunks (the next
+// chunk is loaded into registers while the current one is used).  Column tiles past
+// the last block visible to the tile's last timestep exit at once (the causal
+// triangle is never computed).
 constexpr int kLgTM = 256, kLgTN = 64, kLgEK = 32;
 
 // Per kLgTM-row tile of the logits (rows r = t * hpg + head, the same for every batch
@@ -138,7 +142,7 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
   constexpr int EPL = 16 / sizeof(S);           // elements per 16-byte piece
   constexpr int APT = kLgEK / EPL;              // A pieces per thread (its row's chunk)
   constexpr int BPT = kLgTN * (kLgEK / EPL) / 256;  // B pieces per thread
-  constexpr int AP = kLgTM + 4, BP = kLgTN + 4;  // padded LDS rows (16-byte aligned)
+  constexpr int AP = kLgTM + 16, BP = kLgTN + 16;  // padded LDS rows: the 4 k slots of a read hit distinct banks
   __shared__ __attribute__((aligned(16))) float As[kLgEK * AP];  // [e][row]
   __shared__ __attribute__((aligned(16))) float Bs[kLgEK * BP];  // [e][col]
 
@@ -185,12 +189,13 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
     }
   };
 
-  const int tr = tid >> 3, tc = tid & 7;  // lane tile: rows tr*8.., columns tc*8..
-  float acc[8][8];
+  const int lane = tid & 63, li = lane & 15, kk = lane >> 4;
+  const int wr0 = (tid >> 6) * 64;  // the wave's first row in the tile
+  f32x4 acc[4][4];                  // [block tile mt][row tile nt]
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int m = 0; m < 4; ++m)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[i][j] = 0.0f;
+    for (int n = 0; n < 4; ++n) acc[m][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // a chunk past dk holds zeros: fma(0, 0, acc) == acc (acc is never -0), so the
   // padded steps leave every chain exactly as the dk-step one
@@ -200,30 +205,32 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
     store();
     __syncthreads();
     if (e0 + kLgEK < dk) load(e0 + kLgEK);
-#pragma unroll 8
-    for (int e = 0; e < kLgEK; ++e) {
-      const float4 q0 = *reinterpret_cast<const float4*>(&As[e * AP + tr * 8]);
-      const float4 q1 = *reinterpret_cast<const float4*>(&As[e * AP + tr * 8 + 4]);
-      const float4 k0 = *reinterpret_cast<const float4*>(&Bs[e * BP + tc * 8]);
-      const float4 k1 = *reinterpret_cast<const float4*>(&Bs[e * BP + tc * 8 + 4]);
-      const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-      const float kv[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
+    for (int j4 = 0; j4 < kLgEK; j4 += 4) {
+      const int e = j4 + kk;  // this lane's k slot
+      float kv[4], qv[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[i][j] = fmaf(qv[i], kv[j], acc[i][j]);
+      for (int m = 0; m < 4; ++m) kv[m] = Bs[e * BP + m * 16 + li];
+#pragma unroll
+      for (int n = 0; n < 4; ++n) qv[n] = As[e * AP + wr0 + n * 16 + li];
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int n = 0; n < 4; ++n) acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[m], qv[n], acc[m][n], 0, 0, 0);
     }
   }
 
-  float* out = a.lg + ((int64_t)bg * Rall + row0 + tr * 8) * a.ncs + col0 + tc * 8;
+  // acc[m][n][u]: block col0 + 16 m + 4 kk + u of row row0 + wr0 + 16 n + li
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if (row0 + tr * 8 + i < Rall) {
-      float* o = out + (int64_t)i * a.ncs;
-      *reinterpret_cast<float4*>(o) = make_float4(acc[i][0] * a.scale, acc[i][1] * a.scale, acc[i][2] * a.scale,
-                                                  acc[i][3] * a.scale);
-      *reinterpret_cast<float4*>(o + 4) = make_float4(acc[i][4] * a.scale, acc[i][5] * a.scale,
-                                                      acc[i][6] * a.scale, acc[i][7] * a.scale);
+  for (int n = 0; n < 4; ++n) {
+    const int r = row0 + wr0 + n * 16 + li;
+    if (r < Rall) {
+      float* o = a.lg + ((int64_t)bg * Rall + r) * a.ncs + col0 + kk * 4;
+#pragma unroll
+      for (int m = 0; m < 4; ++m)
+        *reinterpret_cast<float4*>(o + m * 16) =
+            make_float4(acc[m][n][0] * a.scale, acc[m][n][1] * a.scale, acc[m][n][2] * a.scale,
+                        acc[m][n][3] * a.scale);
     }
   }
 }
