@@ -538,7 +538,10 @@ int launch_score_topn(int dtype, ScoreArgs a, hipStream_t st) {
   }
   const int nq = score_rows_nq(a.ncs);
   const bool fast9 = a.a == 2 && a.s == 4;
-  int nw = kRowsWaves;  // fewer waves per workgroup when the generic remap's LDS rows do not fit
+  // fewer waves per workgroup when the generic remap's LDS rows do not fit, and 4 when the
+  // row registers allow at most 3 waves per SIMD (a workgroup of 4 puts one on each SIMD,
+  // so three workgroups share a CU where one of 8 waves would leave a third slot empty)
+  int nw = nq >= 8 ? 4 : kRowsWaves;
   while (nw > 1 && score_rows_lds(nq, fast9, nw, a.nsel) > 80 * 1024) nw /= 2;
   const size_t lds = score_rows_lds(nq, fast9, nw, a.nsel);
   if (lds > 156 * 1024) return 1;
