@@ -272,4 +272,52 @@ struct IntDiv {
   __device__ __forceinline__ int mod(int n) const { return n - div(n) * d; }
 };
 
+// Value of lane L ^ OFF of a wave64 (OFF a power of two below 64) without the LDS
+// crossbar: v_permlane32_swap / v_permlane16_swap for 32 and 16 (each swap returns the
+// other half's values in the result the lane's own half does not keep), DPP row_ror:8
+// for 8, row_ror:4 or :12 by lane for 4, quad_perm for 2 and 1.  Equal to
+// __shfl_xor(x, OFF) on every lane.
+template <int OFF>
+__device__ __forceinline__ uint32_t lane_xor_u32(uint32_t x) {
+  static_assert(OFF == 1 || OFF == 2 || OFF == 4 || OFF == 8 || OFF == 16 || OFF == 32, "lane offset");
+  const int lane = threadIdx.x & 63;
+  if constexpr (OFF == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  } else if constexpr (OFF == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else if constexpr (OFF == 8) {
+    return __builtin_amdgcn_update_dpp(0u, x, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (OFF == 4) {
+    const uint32_t lo = __builtin_amdgcn_update_dpp(0u, x, 0x124, 0xF, 0xF, false);  // row_ror:4
+    const uint32_t hi = __builtin_amdgcn_update_dpp(0u, x, 0x12C, 0xF, 0xF, false);  // row_ror:12
+    return (lane & 4) ? lo : hi;
+  } else if constexpr (OFF == 2) {
+    return __builtin_amdgcn_update_dpp(0u, x, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  } else {
+    return __builtin_amdgcn_update_dpp(0u, x, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  }
+}
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float x) {
+  return __uint_as_float(lane_xor_u32<OFF>(__float_as_uint(x)));
+}
+template <int OFF>
+__device__ __forceinline__ int lane_xor(int x) {
+  return (int)lane_xor_u32<OFF>((uint32_t)x);
+}
+// xor butterfly over 32, 16, 8, 4, 2, 1: every lane ends with op folded over the wave,
+// pairs combined in exactly the order of the __shfl_xor loop over the same offsets
+template <typename T, typename F>
+__device__ __forceinline__ T wave_butterfly(T x, F op) {
+  x = op(x, lane_xor<32>(x));
+  x = op(x, lane_xor<16>(x));
+  x = op(x, lane_xor<8>(x));
+  x = op(x, lane_xor<4>(x));
+  x = op(x, lane_xor<2>(x));
+  x = op(x, lane_xor<1>(x));
+  return x;
+}
+
 }  // namespace nsa

@@ -256,7 +256,7 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
 constexpr int kRowsWaves = 8;
 
 template <int NQ, bool FAST9>
-__global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a) {
+__global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu(NQ == 8 ? 4 : 1))) void score_rows_kernel(ScoreArgs a) {
   // LDS: sbe [NQ * 256] block ends (INT_MAX past NB); generic remap only, per wave:
   // row copy [NQ * 256] + Eq. 10 sums [nsel rounded up to 4]
   extern __shared__ float lds[];
@@ -286,8 +286,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
     if (be.z <= ta) vis_hi = i + 3;
     if (be.w <= ta) vis_hi = i + 4;
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) vis_hi = max(vis_hi, __shfl_xor(vis_hi, off));
+  vis_hi = wave_butterfly(vis_hi, [](int x, int y) { return max(x, y); });
   vis_hi = __builtin_amdgcn_readfirstlane(vis_hi);  // uniform: branches on it stay scalar
   // columns read (block 0 always: the no-visible-block rule scores it)
   const int ncol = max(64, ((vis_hi + 63) >> 6) * 64);
@@ -335,8 +334,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
       mx = __shfl(cur[0].x, 0);
       if (lane == 0) v[0][0] = mx;
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    mx = wave_butterfly(mx, [](float x, float y) { return fmaxf(x, y); });
     float part = 0.0f;
 #pragma unroll
     for (int s = 0; s < NQ; ++s)
@@ -346,8 +344,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
           v[s][u] = exp32(v[s][u] - mx);
           part += v[s][u];
         }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) part = part + __shfl_xor(part, off);
+    part = wave_butterfly(part, [](float x, float y) { return x + y; });
     const float rs = 1.0f / part;
 #pragma unroll
     for (int s = 0; s < NQ; ++s)
@@ -438,15 +435,18 @@ __global__ __launch_bounds__(64 * kRowsWaves) void score_rows_kernel(ScoreArgs a
         }
       }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float ov = __shfl_xor(bv, off);
-      const int oi = __shfl_xor(bi, off);
+    auto take = [&](float ov, int oi) __attribute__((always_inline)) {
       if (ov > bv || (ov == bv && oi < bi)) {
         bv = ov;
         bi = oi;
       }
-    }
+    };
+    take(lane_xor<32>(bv), lane_xor<32>(bi));
+    take(lane_xor<16>(bv), lane_xor<16>(bi));
+    take(lane_xor<8>(bv), lane_xor<8>(bi));
+    take(lane_xor<4>(bv), lane_xor<4>(bi));
+    take(lane_xor<2>(bv), lane_xor<2>(bi));
+    take(lane_xor<1>(bv), lane_xor<1>(bi));
     // bi is wave-uniform: its owner marks it taken
     if constexpr (FAST9) {
 #pragma unroll
