@@ -34,15 +34,17 @@
 
 namespace nsa {
 
+// exp32 of a softmax argument x = s - max <= 0 (or -inf): k = rint(x log2 e), r by a
+// two-constant Cody-Waite reduction, the polynomial by fma, p * 2^k; 0 below -64.  Only
+// arguments <= 0 occur, so there is no input clamp (an input below -64, -inf included,
+// may give a non-finite intermediate that the final select replaces by 0), and p * 2^k
+// is one ldexp (k >= -93 and p in [0.7, 1.5] keep it normal: exact, as the multiply by
+// the constructed power of two the oracle performs).
 __device__ __forceinline__ float exp32(float x) {
   const float kL2e = 1.44269504088896341f;
   const float kLn2Hi = 0.693145751953125f;
   const float kLn2Lo = 1.42860682030941723212e-6f;
-  // branch-free: out-of-range inputs (below -64, -inf, NaN) run the polynomial on 0
-  // and are replaced by 0 at the end; inputs above 0 are clamped to 0
   const bool ok = x >= -64.0f;
-  x = x > 0.0f ? 0.0f : x;
-  x = ok ? x : 0.0f;
   const float k = rintf(x * kL2e);
   float r = fmaf(-k, kLn2Hi, x);
   r = fmaf(-k, kLn2Lo, r);
@@ -54,7 +56,7 @@ __device__ __forceinline__ float exp32(float x) {
   p = fmaf(p, r, 0.5f);
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
-  const float v = p * __uint_as_float((uint32_t)((int)k + 127) << 23);
+  const float v = __builtin_amdgcn_ldexpf(p, (int)k);
   return ok ? v : 0.0f;
 }
 
