@@ -137,6 +137,26 @@ def test_score_topn_full_size_sampled(dev, cfgname):
     assert not ((srt[..., 1:] == srt[..., :-1]) & (srt[..., 1:] >= 0)).any()
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_score_topn_4096_columns_sampled(dev, dtype):
+    """More than 2048 compressed blocks (T = 40000: 2499 blocks, rows of 2560 logits held
+    as 16 pieces per lane).  Sampled rows, indices and scores bit-exact."""
+    B, H, G, T, dk, l, d, lp, n = 1, 4, 2, 40000, 32, 32, 16, 64, 16
+    g = torch.Generator(device=dev).manual_seed(11)
+    q = (torch.randn(B, H, T, dk, device=dev, generator=g) / math.sqrt(dk)).to(dtype)
+    be = _block_ends(T, l, d)
+    kc = torch.randn(B, G, dk, be.shape[0], device=dev, generator=g).to(dtype)
+    cfg = NSAConfig(head_dim_qk=dk, n_heads=H, n_kv_groups=G, l=l, d=d, l_prime=lp, n=n)
+    idx, pc, ps = score_and_select(q, kc, torch.tensor(be).to(dev), 1 / math.sqrt(dk), cfg, return_scores=True)
+    rows = np.unique(np.concatenate([np.arange(0, 20), np.linspace(0, T - 1, 30).astype(int), [T - 1]]))
+    ridx, rpc, rps = oracle.score_topn(q.float().cpu().numpy()[:, :, rows], kc.float().cpu().numpy(), be,
+                                       np.float32(1 / math.sqrt(dk)), l=l, d=d, lprime=lp, n=n, want_scores=True,
+                                       positions=rows)
+    np.testing.assert_array_equal(idx.cpu().numpy()[:, :, rows], ridx)
+    np.testing.assert_array_equal(pc.cpu().numpy()[:, :, rows], rpc)
+    np.testing.assert_array_equal(ps.cpu().numpy()[:, :, rows], rps)
+
+
 @pytest.mark.parametrize("H,G,T,dk,dtype", [(64, 1, 9000, 32, torch.float32), (48, 2, 4500, 64, torch.bfloat16)])
 def test_score_topn_multipass_sampled(dev, H, G, T, dk, dtype):
     """Many heads per group with many compressed blocks: a timestep's rows are scored
