@@ -1,6 +1,7 @@
 // Fused selection scoring on gfx950: Eq. 8 (compressed-attention probabilities),
 // Eq. 9 (triangular remap to selection blocks), Eq. 10 (GQA head sum) and the top-n
-// with fixed blocks, in two kernels:
+// with fixed blocks, in two kernels after a small pre-kernel (score_tile_ncomp_kernel,
+// the visible block count of each logits row tile):
 //   score_logits_kernel  the Eq. 8 logits of every (row, visible compressed block) as an
 //                        fp32 MFMA GEMM into the caller's workspace;
 //   score_rows_kernel    softmax, Eq. 9, Eq. 10 and the top-n, one wave per
@@ -118,7 +119,8 @@ __device__ __forceinline__ int score_ncomp(const ScoreArgs& a, int t_last, int* 
 // lg[r][i] = scale * (sum over e = 0..dk-1 of q[r][e] k[i][e]), each element one
 // sequential fma chain in e order (the accumulation order the indices are defined by).
 // v_mfma_f32_16x16x4_f32 computes D = C + sum_k A[m][k] B[k][n] as four IEEE fp32
-// fmas in k order 0..3, each rounded (subnormals kept), so the chain of MFMAs over the
+// fmas in k order 0..3, each rounded (subnormals kept; measured on gfx950 against an
+// emulated fma chain over millions of random operands), so the chain of MFMAs over the
 // feature steps e = 4j..4j+3 (slot k = e - 4j) is exactly that fma chain.
 // Workgroup = 256 query rows x 64 compressed blocks, 4 waves of 64 rows x 64 blocks
 // (4 x 4 MFMA tiles, blocks as the M operand so a lane holds 4 consecutive blocks of
