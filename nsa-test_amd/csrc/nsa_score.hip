@@ -281,6 +281,7 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
   float* wag = wb + NQ * 256;
 
   int vis_hi = 0;  // 1 + the largest block index visible at t (0: none)
+  int nfull = NQ;  // leading pieces whose 256 blocks are all visible (no mask needed)
 #pragma unroll
   for (int s = 0; s < NQ; ++s) {
     const int4 be = *reinterpret_cast<const int4*>(sbe + 256 * s + 4 * lane);
@@ -289,6 +290,8 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
     if (be.y <= ta) vis_hi = i + 2;
     if (be.z <= ta) vis_hi = i + 3;
     if (be.w <= ta) vis_hi = i + 4;
+    const bool all4 = be.x <= ta && be.y <= ta && be.z <= ta && be.w <= ta;
+    if (nfull == NQ && __ballot(!all4)) nfull = s;  // wave-uniform
   }
   vis_hi = wave_butterfly(vis_hi, [](int x, int y) { return max(x, y); });
   vis_hi = __builtin_amdgcn_readfirstlane(vis_hi);  // uniform: branches on it stay scalar
@@ -327,11 +330,18 @@ __global__ __launch_bounds__(64 * kRowsWaves) __attribute__((amdgpu_waves_per_eu
         v[s][0] = v[s][1] = v[s][2] = v[s][3] = 0.0f;
         continue;
       }
-      const int4 be = *reinterpret_cast<const int4*>(sbe + 256 * s + 4 * lane);
-      v[s][0] = be.x <= ta ? cur[s].x : -INFINITY;
-      v[s][1] = be.y <= ta ? cur[s].y : -INFINITY;
-      v[s][2] = be.z <= ta ? cur[s].z : -INFINITY;
-      v[s][3] = be.w <= ta ? cur[s].w : -INFINITY;
+      if (s < nfull) {  // every block of the piece visible
+        v[s][0] = cur[s].x;
+        v[s][1] = cur[s].y;
+        v[s][2] = cur[s].z;
+        v[s][3] = cur[s].w;
+      } else {
+        const int4 be = *reinterpret_cast<const int4*>(sbe + 256 * s + 4 * lane);
+        v[s][0] = be.x <= ta ? cur[s].x : -INFINITY;
+        v[s][1] = be.y <= ta ? cur[s].y : -INFINITY;
+        v[s][2] = be.z <= ta ? cur[s].z : -INFINITY;
+        v[s][3] = be.w <= ta ? cur[s].w : -INFINITY;
+      }
       mx = fmaxf(mx, fmaxf(fmaxf(v[s][0], v[s][1]), fmaxf(v[s][2], v[s][3])));
     }
     if (vis_hi == 0) {  // no visible block (wave-uniform): block 0 is scored
