@@ -286,7 +286,7 @@ int nsa_timing_end(double* total_ms, int* launches);
  * skip).  fp32 arithmetic in a fixed order: indices are reproducible bit for bit.
  * include_fixed && n_fixed > 0 merges the blocks [0, max(0,(t-l')/l'), t/l'] first.
  * workspace: device memory, 16-byte aligned, of nsa_score_topn_workspace_size() bytes
- * (the fp32 logits of every row and block, then one int per 256-row logits tile);
+ * (the fp32 logits of every row and block, then one int per 128-row logits tile);
  * NSA_ERR_WORKSPACE when smaller. */
 size_t nsa_score_topn_workspace_size(int Z, int H, int n_kv_groups, int n_ctx, int head_dim_qk, int n_blocks, int n);
 int nsa_score_topn(const void* q, const void* k_cmp, const int32_t* Block_ends, int64_t* out_idx, float* p_cmp,

@@ -122,13 +122,13 @@ __device__ __forceinline__ int score_ncomp(const ScoreArgs& a, int t_last, int* 
 // fmas in k order 0..3, each rounded (subnormals kept; measured on gfx950 against an
 // emulated fma chain over millions of random operands), so the chain of MFMAs over the
 // feature steps e = 4j..4j+3 (slot k = e - 4j) is exactly that fma chain.
-// Workgroup = 256 query rows x 64 compressed blocks, 4 waves of 64 rows x 64 blocks
-// (4 x 4 MFMA tiles, blocks as the M operand so a lane holds 4 consecutive blocks of
+// Workgroup = 128 query rows x 64 compressed blocks, 4 waves of 32 rows x 64 blocks
+// (4 x 2 MFMA tiles, blocks as the M operand so a lane holds 4 consecutive blocks of
 // one row); the operands are staged through LDS as fp32 in EK-feature chunks (the next
 // chunk is loaded into registers while the current one is used).  Column tiles past
 // the last block visible to the tile's last timestep exit at once (the causal
 // triangle is never computed).
-constexpr int kLgTM = 256, kLgTN = 64, kLgEK = 32;
+constexpr int kLgTM = 128, kLgTN = 64, kLgEK = 32;
 
 // Per kLgTM-row tile of the logits (rows r = t * hpg + head, the same for every batch
 // and group): the number of compressed blocks holding every block visible to the tile's
@@ -144,7 +144,8 @@ __global__ __launch_bounds__(256) void score_tile_ncomp_kernel(ScoreArgs a) {
 template <typename S>
 __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
   constexpr int EPL = 16 / sizeof(S);           // elements per 16-byte piece
-  constexpr int APT = kLgEK / EPL;              // A pieces per thread (its row's chunk)
+  constexpr int TPR = 256 / kLgTM;              // threads staging one A row
+  constexpr int APT = kLgEK / EPL / TPR;        // A pieces per thread (part of its row's chunk)
   constexpr int BPT = kLgTN * (kLgEK / EPL) / 256;  // B pieces per thread
   constexpr int AP = kLgTM + 16, BP = kLgTN + 16;  // padded LDS rows: the 4 k slots of a read hit distinct banks
   __shared__ __attribute__((aligned(16))) float As[kLgEK * AP];  // [e][row]
@@ -158,7 +159,7 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
   if (col0 >= a.tile_nc[blockIdx.x]) return;  // workgroup-uniform: past the visible frontier
 
   // the thread's staging row (A) and column (B)
-  const int arow = min(row0 + tid, Rall - 1);
+  const int arow = min(row0 + tid % kLgTM, Rall - 1), apart = tid / kLgTM;
   const S* qrow = reinterpret_cast<const S*>(a.q) + b * a.sq_b + (int64_t)(g * hpg + arow % hpg) * a.sq_h +
                   (int64_t)(arow / hpg) * a.sq_t;
   const int bcol = tid % kLgTN, bpart0 = tid / kLgTN;
@@ -169,7 +170,8 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
   auto load = [&](int e0) {
 #pragma unroll
     for (int j = 0; j < APT; ++j)
-      pa[j] = e0 + j * EPL < dk ? *reinterpret_cast<const uint4*>(qrow + e0 + j * EPL) : make_uint4(0, 0, 0, 0);
+      pa[j] = e0 + (apart + j * TPR) * EPL < dk ? *reinterpret_cast<const uint4*>(qrow + e0 + (apart + j * TPR) * EPL)
+                                               : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int j = 0; j < BPT; ++j) {
       const int e = e0 + (bpart0 + j * (256 / kLgTN)) * EPL;
@@ -182,7 +184,7 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
       float v[EPL];
       unpack16<S>(pa[j], v);
 #pragma unroll
-      for (int u = 0; u < EPL; ++u) As[(j * EPL + u) * AP + tid] = v[u];
+      for (int u = 0; u < EPL; ++u) As[((apart + j * TPR) * EPL + u) * AP + tid % kLgTM] = v[u];
     }
 #pragma unroll
     for (int j = 0; j < BPT; ++j) {
@@ -194,12 +196,13 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
   };
 
   const int lane = tid & 63, li = lane & 15, kk = lane >> 4;
-  const int wr0 = (tid >> 6) * 64;  // the wave's first row in the tile
-  f32x4 acc[4][4];                  // [block tile mt][row tile nt]
+  constexpr int NT = kLgTM / 64;    // 16-row MFMA tiles per wave
+  const int wr0 = (tid >> 6) * (kLgTM / 4);  // the wave's first row in the tile
+  f32x4 acc[4][NT];                 // [block tile mt][row tile nt]
 #pragma unroll
   for (int m = 0; m < 4; ++m)
 #pragma unroll
-    for (int n = 0; n < 4; ++n) acc[m][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int n = 0; n < NT; ++n) acc[m][n] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
   // a chunk past dk holds zeros: fma(0, 0, acc) == acc (acc is never -0), so the
   // padded steps leave every chain exactly as the dk-step one
@@ -212,21 +215,21 @@ __global__ __launch_bounds__(256) void score_logits_kernel(ScoreArgs a) {
 #pragma unroll
     for (int j4 = 0; j4 < kLgEK; j4 += 4) {
       const int e = j4 + kk;  // this lane's k slot
-      float kv[4], qv[4];
+      float kv[4], qv[NT];
 #pragma unroll
       for (int m = 0; m < 4; ++m) kv[m] = Bs[e * BP + m * 16 + li];
 #pragma unroll
-      for (int n = 0; n < 4; ++n) qv[n] = As[e * AP + wr0 + n * 16 + li];
+      for (int n = 0; n < NT; ++n) qv[n] = As[e * AP + wr0 + n * 16 + li];
 #pragma unroll
       for (int m = 0; m < 4; ++m)
 #pragma unroll
-        for (int n = 0; n < 4; ++n) acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[m], qv[n], acc[m][n], 0, 0, 0);
+        for (int n = 0; n < NT; ++n) acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[m], qv[n], acc[m][n], 0, 0, 0);
     }
   }
 
   // acc[m][n][u]: block col0 + 16 m + 4 kk + u of row row0 + wr0 + 16 n + li
 #pragma unroll
-  for (int n = 0; n < 4; ++n) {
+  for (int n = 0; n < NT; ++n) {
     const int r = row0 + wr0 + n * 16 + li;
     if (r < Rall) {
       float* o = a.lg + ((int64_t)bg * Rall + r) * a.ncs + col0 + kk * 4;

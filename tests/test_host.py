@@ -113,10 +113,10 @@ def test_workspace_sizes():
     assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 8192) > b
     s = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 16, 64, 1)
     assert s > f
-    # scoring: fp32 logits [Z*H][T][N rounded up to 64], then one int per 256-row tile of
+    # scoring: fp32 logits [Z*H][T][N rounded up to 64], then one int per 128-row tile of
     # a group's (timestep, head) rows, padded to 256 bytes
     sc = _lib.load().nsa_score_topn_workspace_size
-    assert sc(1, 64, 4, 8192, 192, 511, 16) == 64 * 8192 * 512 * 4 + 2048
+    assert sc(1, 64, 4, 8192, 192, 511, 16) == 64 * 8192 * 512 * 4 + 4096
     assert sc(2, 8, 2, 100, 64, 5, 4) == 2 * 8 * 100 * 64 * 4 + 256
     assert sc(1, 8, 3, 100, 64, 5, 4) == 0  # H not a multiple of the groups
 
