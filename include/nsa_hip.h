@@ -275,6 +275,12 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
 int nsa_timing_begin(int kernel_id);
 int nsa_timing_end(double* total_ms, int* launches);
 
+/* ---- dK/dV schedule query (no reference counterpart: introspection for tests) --
+ * The number of dK/dV work items per (batch, KV group) and the query-segment length
+ * (128 or 256 entries) the backward entry points launch with for this shape. */
+int nsa_bwd_dkdv_plan(int branch, int Z, int H, int n_kv_groups, int n_ctx_q, int n_ctx_kv, int n_slots,
+                      int block_size_selection, int window_size, int* items_per_bg, int* segment);
+
 /* ---- selection scoring: Eq. 8 -> 9 -> 10 -> top-n, fused -------------------
  * Replaces the module's inline Eq. 8 (nsa/kernels.py:2316-2343),
  * derive_selection_from_compression_per_timestep (nsa/kernels.py:1920-1962) and

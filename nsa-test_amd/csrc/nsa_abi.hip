@@ -348,6 +348,15 @@ size_t nsa_bwd_workspace_size(int branch, int dtype, int Z, int H, int G, int Tq
   return make_layout(s, true).total;
 }
 
+int nsa_bwd_dkdv_plan(int branch, int Z, int H, int G, int Tq, int Tkv, int nslots, int lprime, int window_size,
+                      int* items_per_bg, int* segment) {
+  Shape s{branch, NSA_BF16, Z, H, G, Tq, Tkv, 64, 64, nslots, lprime > 0 ? lprime : 64, window_size > 0 ? window_size : 1};
+  if (Z <= 0 || G <= 0 || H % G || Tq < 0 || Tkv < 0) return fail(NSA_ERR_INVALID, "bad shape");
+  if (items_per_bg) *items_per_bg = s.items_per_bg();
+  if (segment) *segment = s.seg();
+  return NSA_OK;
+}
+
 #define NSA_FWD_IO                                                                                    \
   FwdIO io{Q, K, V, Out, L, M,                                                                        \
            {stride_qz, stride_qh, stride_qm, stride_qk}, {stride_kz, stride_kg, stride_kn, stride_kk}, \

@@ -65,6 +65,7 @@ SIGNATURES.update({
     "nsa_gate_mix_bwd": (_I, [_P] + [_L] * 3 + [_P] * 3 + [_L] * 3 + [_P] + [_L] * 4 + [_P] * 5 + [_I] * 6 + [_P]),
     "nsa_compress_pool_fwd": (_I, [_P] * 5 + [_I] * 9 + [_P]),
     "nsa_compress_pool_bwd": (_I, [_P] * 7 + [_I] * 9 + [_P]),
+    "nsa_bwd_dkdv_plan": (_I, [_I] * 9 + [_P, _P]),
 })
 
 _lock = threading.Lock()
@@ -121,6 +122,16 @@ def call(name: str, *args) -> None:
 
 def size(name: str, *args) -> int:
     return int(getattr(load(), name)(*args))
+
+
+def dkdv_plan(branch: int, Z: int, H: int, G: int, Tq: int, Tkv: int, n_slots: int, lprime: int,
+              window: int) -> dict:
+    """The dK/dV schedule of a backward launch: work items per (batch, group) and the
+    query-segment length."""
+    items, seg = ctypes.c_int(0), ctypes.c_int(0)
+    call("nsa_bwd_dkdv_plan", branch, Z, H, G, Tq, Tkv, n_slots, lprime, window,
+         ctypes.cast(ctypes.pointer(items), c_void_p), ctypes.cast(ctypes.pointer(seg), c_void_p))
+    return {"items_per_bg": items.value, "segment": seg.value}
 
 
 # kernel ids of nsa_timing_begin

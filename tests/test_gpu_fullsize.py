@@ -1,0 +1,206 @@
+"""Full-size parity of the three attention branches, forward and backward, at the shapes
+bench.py times: the paper configuration (B=1, H=64, G=4, T=8192, dk=192, dv=128), the
+long configuration (B=1, H=32, G=2, T=32768, dk=dv=128, peaked low-rank q/k) and the
+sliding-only configuration (B=2, H=8, G=2, T=4096, dk=dv=64, w=512), all bf16.
+
+The GPU runs every kernel at its full-size schedule (grid, dK/dV work items, 256-entry
+query segments where the launch picks them, the selection union bitmap over up to 512
+blocks).  The float64 C oracle evaluates a sample of query rows (`positions=`):
+* out, L, M and dQ are compared on the sampled rows;
+* dO is zero outside the sampled rows, so the GPU's dK / dV are exactly the sampled
+  rows' contributions, which the oracle computes from the same rows.
+The sample holds the boundary rows (0, l'-1, l', w-1, w, the last row, ...) and random
+rows spread over the whole sequence, so every 256-entry dK/dV segment holds some.
+
+Tolerance: bf16 2e-2 norm-relative (outputs and gradients), the oracle fed the
+bf16-rounded inputs; L + M within 5e-3 absolute where finite, -inf exactly where the
+oracle row is empty.  Reference call sites: nsa/kernels.py:2401-2426 (the module's
+three branch calls); reference tests/test_large_scale.py:17-302 exercises these sizes.
+
+Also here: cases that cross the 4096-work-item threshold at small T through a large
+batch (the 256-entry segment path of the dK/dV kernels, nsa_abi.hip `Shape::seg`),
+compared on every row.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from conftest import rel_err
+from nsa import _ops
+from nsa.kernels import NSAConfig, score_and_select
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+FULL = {
+    "paper": dict(B=1, H=64, G=4, T=8192, dk=192, dv=128, w=512, lowrank=False),
+    "long": dict(B=1, H=32, G=2, T=32768, dk=128, dv=128, w=512, lowrank=True),
+}
+
+
+def _np64(t):
+    return t.detach().float().cpu().double().numpy()
+
+
+def _rows(T, seed, n_random=48, lp=64, w=512):
+    base = {0, 1, 15, 16, 31, 32, 47, lp - 1, lp, lp + 1, 2 * lp - 1, 2 * lp, w - 1, w, w + 1, T // 2, T - 2, T - 1}
+    rng = np.random.default_rng(seed)
+    rows = set(int(x) for x in rng.choice(T, size=n_random, replace=False)) | {r for r in base if 0 <= r < T}
+    return np.array(sorted(rows), dtype=np.int64)
+
+
+def _inputs(c, seed, dev):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    B, H, G, T, dk, dv = c["B"], c["H"], c["G"], c["T"], c["dk"], c["dv"]
+    if c.get("lowrank"):
+        basis = torch.randn(T, 8, device=dev, generator=g)
+        pq = torch.randn(8, dk, device=dev, generator=g)
+        pk = torch.randn(8, dk, device=dev, generator=g)
+        q = (torch.randn(B, H, T, dk, device=dev, generator=g) + basis @ pq) / math.sqrt(dk)
+        k = (torch.randn(B, G, T, dk, device=dev, generator=g) + basis @ pk) / math.sqrt(dk)
+    else:
+        q = torch.randn(B, H, T, dk, device=dev, generator=g)
+        k = torch.randn(B, G, T, dk, device=dev, generator=g)
+    v = torch.randn(B, G, T, dv, device=dev, generator=g)
+    do = torch.randn(B, H, T, dv, device=dev, generator=g)
+    bf = torch.bfloat16
+    # K is held in the reference layout [B,G,dk,T]; the kernels get its (b,g,time,dk) view
+    kp = k.to(bf).transpose(-1, -2).contiguous()
+    return q.to(bf), kp, v.to(bf), do.to(bf)
+
+
+def _sampled_check(kind, q, kp, v, do, rows, scale, **kw):
+    """Full-size GPU forward + backward (dO zero off the sampled rows) against the oracle
+    on the sampled rows."""
+    k = kp.transpose(-1, -2)
+    mask = torch.zeros(q.shape[2], dtype=torch.bool, device=q.device)
+    mask[torch.as_tensor(rows, device=q.device)] = True
+    do_s = torch.where(mask.view(1, 1, -1, 1), do, torch.zeros_like(do))
+    out, L, M = _ops.attn_fwd(kind, q, k, v, scale, **kw)
+    dq, dk, dv = _ops.attn_bwd(kind, q, k, v, out, do_s, L, M, scale, **kw)
+    torch.cuda.synchronize()
+    r = torch.as_tensor(rows, device=q.device)
+    okw = dict(kw)
+    if "indices" in okw:
+        okw["indices"] = okw["indices"][:, :, r].cpu().numpy()
+    if "block_ends" in okw:
+        okw["block_ends"] = okw["block_ends"].cpu().numpy()
+    qs, dos = _np64(q[:, :, r]), _np64(do[:, :, r])
+    kn, vn = _np64(k), _np64(v)
+    pos = rows.astype(np.int32)
+    ro, rL, rM = oracle.attn_fwd(kind, qs, kn, vn, scale, positions=pos, **okw)
+    rq, rk, rv = oracle.attn_bwd(kind, qs, kn, vn, dos, scale, positions=pos, **okw)
+    errs = {"out": rel_err(_np64(out[:, :, r]), ro), "dq": rel_err(_np64(dq[:, :, r]), rq),
+            "dk": rel_err(_np64(dk), rk), "dv": rel_err(_np64(dv), rv)}
+    print("[fullsize] errors", {k_: f"{e_:.2e}" for k_, e_ in errs.items()}, flush=True)
+    assert max(errs.values()) < TOL, errs
+    Ln, Mn = L[:, :, r].cpu().numpy(), M[:, :, r].cpu().numpy()
+    assert np.array_equal(np.isneginf(Ln), np.isneginf(rL))
+    fin = np.isfinite(rL)
+    np.testing.assert_allclose(Ln[fin] + Mn[fin], rL[fin] + rM[fin], rtol=0, atol=5e-3)
+    # no gradient leaks from the zero-dO rows into dQ
+    assert torch.count_nonzero(dq[:, :, ~mask]).item() == 0
+    return errs
+
+
+def _compressed(c, seed, dev, l=32, d=16):
+    T, B, G, dk, dv = c["T"], c["B"], c["G"], c["dk"], c["dv"]
+    n_act = (T - l) // d + 1
+    n_pad = 1 << (n_act - 1).bit_length()
+    be = torch.full((n_pad,), 999999, dtype=torch.int32)
+    be[:n_act] = torch.arange(n_act, dtype=torch.int32) * d + l - 1
+    g = torch.Generator(device=dev).manual_seed(seed)
+    kc = torch.randn(B, G, dk, n_pad, device=dev, generator=g).to(torch.bfloat16)
+    vc = torch.randn(B, G, n_pad, dv, device=dev, generator=g).to(torch.bfloat16)
+    return kc, vc, be.to(dev)
+
+
+@pytest.mark.parametrize("name", ["paper", "long"])
+def test_fullsize_sliding(dev, name):
+    c = FULL[name]
+    q, kp, v, do = _inputs(c, 100, dev)
+    rows = _rows(c["T"], 1, w=c["w"])
+    print(f"[fullsize] sliding {name} rows={len(rows)}", flush=True)
+    _sampled_check(_ops.SLIDING, q, kp, v, do, rows, 1 / math.sqrt(c["dk"]), window=c["w"])
+
+
+@pytest.mark.parametrize("name", ["paper", "long"])
+def test_fullsize_compression(dev, name):
+    c = FULL[name]
+    q, _, _, do = _inputs(c, 200, dev)
+    kc, vc, be = _compressed(c, 201, dev)
+    rows = _rows(c["T"], 2)
+    print(f"[fullsize] compression {name} rows={len(rows)} blocks={be.numel()}", flush=True)
+    _sampled_check(_ops.COMPRESSION, q, kc, vc, do, rows, 1 / math.sqrt(c["dk"]), block_ends=be)
+
+
+@pytest.mark.parametrize("name", ["paper", "long"])
+def test_fullsize_selection(dev, name):
+    """Indices from the fused scoring kernel over the full sequence (checked bit-exact
+    against the oracle on the sampled rows), then the selection branch."""
+    c = FULL[name]
+    q, kp, v, do = _inputs(c, 300, dev)
+    kc, _, be = _compressed(c, 301, dev)
+    if c["lowrank"]:  # peaked scores: compressed keys that share the queries' low-rank part
+        kc = (kc.float() * 0.2 + kp[..., 15::16][..., :kc.shape[-1]].float()).to(torch.bfloat16)
+        kc[..., (c["T"] - 32) // 16 + 1:] = 0
+    cfg = NSAConfig(head_dim_qk=c["dk"], head_dim_v=c["dv"], n_heads=c["H"], n_kv_groups=c["G"], l=32, d=16,
+                    l_prime=64, n=16, w=c["w"])
+    scale = 1 / math.sqrt(c["dk"])
+    idx = score_and_select(q, kc, be, scale, cfg)
+    rows = _rows(c["T"], 3)
+    ridx = oracle.score_topn(q[:, :, torch.as_tensor(rows, device=dev)].float().cpu().numpy(),
+                             kc.float().cpu().numpy(), be.cpu().numpy(), np.float32(scale), l=32, d=16, lprime=64,
+                             n=16, positions=rows.astype(np.int32))
+    np.testing.assert_array_equal(idx[:, :, torch.as_tensor(rows, device=dev)].cpu().numpy(), ridx)
+    print(f"[fullsize] selection {name} rows={len(rows)}", flush=True)
+    _sampled_check(_ops.SELECTION, q, kp, v, do, rows, scale, indices=idx, lprime=64)
+
+
+def test_config2_sliding(dev):
+    """Benchmark config 2: sliding window alone, B=2, H=8,
+    G=2, T=4096, dk=dv=64, w=512, bf16; 320 sampled rows per batch entry."""
+    c = dict(B=2, H=8, G=2, T=4096, dk=64, dv=64)
+    q, kp, v, do = _inputs(c, 400, dev)
+    rows = _rows(c["T"], 4, n_random=300)
+    _sampled_check(_ops.SLIDING, q, kp, v, do, rows, 1 / math.sqrt(64), window=512)
+
+
+# ------------------------------------------- 256-entry dK/dV query segments at small T
+SEG_CASES = [
+    # kind, B, H, G, T, dk, dv, extra
+    (_ops.SLIDING, 43, 8, 4, 1024, 32, 32, dict(window=512)),
+    (_ops.COMPRESSION, 18, 16, 4, 5000, 32, 32, {}),
+    (_ops.SELECTION, 26, 8, 4, 512, 64, 64, dict(lprime=64, n=16)),
+]
+
+
+@pytest.mark.parametrize("kind,B,H,G,T,dk,dv,extra", SEG_CASES)
+def test_dkdv_256_segments(dev, kind, B, H, G, T, dk, dv, extra):
+    """B*G large enough that the dK/dV launch has >= 4096 work items with 256-entry
+    query segments (the path the long configuration takes); 96+ sampled rows, so every
+    segment of every key tile holds sampled rows."""
+    from nsa import _lib
+    extra = dict(extra)
+    n = extra.pop("n", 0)
+    Tkv = T if kind != _ops.COMPRESSION else 1 << (((T - 32) // 16 + 1) - 1).bit_length()
+    lp = extra.get("lprime", 64)
+    plan = _lib.dkdv_plan(kind, B, H, G, T, Tkv, n, lp, extra.get("window", 1))
+    assert plan["segment"] == 256 and plan["items_per_bg"] * B * G >= 4096, plan
+    c = dict(B=B, H=H, G=G, T=T, dk=dk, dv=dv)
+    q, kp, v, do = _inputs(c, 500 + kind, dev)
+    kw = dict(extra)
+    if kind == _ops.COMPRESSION:
+        kp, v, kw["block_ends"] = _compressed(c, 510, dev)
+    if kind == _ops.SELECTION:
+        rng = np.random.default_rng(7)
+        idx = rng.integers(0, (T + lp - 1) // lp, size=(B, G, T, n))
+        idx[rng.random(idx.shape) < 0.1] = -1
+        kw["indices"] = torch.tensor(idx, device=dev)
+    rows = _rows(T, 9, n_random=96, w=extra.get("window", 512))
+    print(f"[fullsize] 256-segment kind={kind} B={B} T={T} plan={plan}", flush=True)
+    _sampled_check(kind, q, kp, v, do, rows, 1 / math.sqrt(dk), **kw)
