@@ -275,6 +275,25 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
 int nsa_timing_begin(int kernel_id);
 int nsa_timing_end(double* total_ms, int* launches);
 
+/* ---- allocation-free sliding-window forward ---------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc):
+ * nsa_sliding_window_fwd with the same arguments and meaning, minus the workspace.  The
+ * K/V re-pack goes to a static 32 MiB scratch array in the library (one copy per GPU,
+ * held until the process ends); a shape whose nsa_fwd_workspace_size exceeds 32 MiB
+ * returns NSA_ERR_WORKSPACE before anything is launched.  Nothing is allocated and no
+ * allocating routine is called.  Every call on one GPU shares that GPU's scratch:
+ * calls that overlap on one GPU (two streams, two threads) race; serialise them. */
+int nsa_sliding_window_fwd_noalloc(const void* Q, const void* K, const void* V, void* Out, float sm_scale, float* L,
+                                   float* M, int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                                   int64_t stride_qk, int64_t stride_kz, int64_t stride_kg, int64_t stride_kn,
+                                   int64_t stride_kk, int64_t stride_vz, int64_t stride_vg, int64_t stride_vn,
+                                   int64_t stride_vk, int64_t stride_oz, int64_t stride_oh, int64_t stride_om,
+                                   int64_t stride_ok, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm,
+                                   int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, int Z, int H,
+                                   int n_kv_groups, int n_ctx, int window_size, int head_dim_qk, int head_dim_v,
+                                   int dtype, nsa_stream_t stream);
+
 /* ---- dK/dV schedule query (no reference counterpart: introspection for tests) --
  * The number of dK/dV work items per (batch, KV group) and the query-segment length
  * (128 or 256 entries) the backward entry points launch with for this shape. */

@@ -4,6 +4,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/nsa_hip.h"
 #include "nsa_attn.h"
 #include "nsa_attn_bwd_dkdv.h"
@@ -323,6 +325,35 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   return NSA_OK;
 }
 
+// Scratch memory of the allocation-free entry point (nsa_sliding_window_fwd_noalloc):
+// a fixed device array that every GPU the library runs on holds until the process ends.
+// Host code never uses the array's name as an address: each device's copy is looked up
+// once with hipGetSymbolAddress and that pointer is passed to the kernels.
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's copy of `scratch` (looked up on the first call per device, with that
+// device current).
+int scratch_ptr(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(NSA_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(NSA_ERR_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) return fail(NSA_ERR_HIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return NSA_OK;
+}
+
 }  // namespace
 
 int nsa::set_error(int code, const char* msg) { return fail(code, "%s", msg); }
@@ -382,6 +413,31 @@ int nsa_sliding_window_fwd(const void* Q, const void* K, const void* V, void* Ou
   NSA_FWD_IO
   Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64, window_size};
   return run_fwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
+                 (hipStream_t)stream);
+}
+
+int nsa_sliding_window_fwd_noalloc(const void* Q, const void* K, const void* V, void* Out, float sm_scale, float* L,
+                                   float* M, int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                                   int64_t stride_qk, int64_t stride_kz, int64_t stride_kg, int64_t stride_kn,
+                                   int64_t stride_kk, int64_t stride_vz, int64_t stride_vg, int64_t stride_vn,
+                                   int64_t stride_vk, int64_t stride_oz, int64_t stride_oh, int64_t stride_om,
+                                   int64_t stride_ok, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm,
+                                   int64_t stride_mz, int64_t stride_mh, int64_t stride_mm, int Z, int H,
+                                   int n_kv_groups, int n_ctx, int window_size, int head_dim_qk, int head_dim_v,
+                                   int dtype, nsa_stream_t stream) {
+  NSA_FWD_IO
+  Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64, window_size};
+  int rc = validate(s);
+  if (rc) return rc;
+  const size_t need = make_layout(s, false).total;
+  if (need > kNoAllocScratchBytes)
+    return fail(NSA_ERR_WORKSPACE,
+                "nsa_sliding_window_fwd_noalloc: this shape needs %zu bytes of scratch, more than the %zu-byte "
+                "static scratch; use nsa_sliding_window_fwd with a workspace",
+                need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if ((rc = scratch_ptr(&ws))) return rc;
+  return run_fwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, ws, kNoAllocScratchBytes,
                  (hipStream_t)stream);
 }
 

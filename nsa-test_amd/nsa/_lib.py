@@ -46,6 +46,8 @@ SIGNATURES = {
     "nsa_sparse_selection_bwd": (
         _I, [_P, _P, _P, _P, _P, _P, _F, _P, _P, *_S26, _P, _P, _P, *_S12, *[_I] * 12, _I, _P, _Z, _P]),
 }
+# the allocation-free sliding-window forward: no workspace arguments
+SIGNATURES["nsa_sliding_window_fwd_noalloc"] = (_I, SIGNATURES["nsa_sliding_window_fwd"][1][:-3] + [_P])
 # the backward extensions: dq_accumulate (int) and delta_in (pointer) before the workspace
 for _n in ("nsa_sliding_window_bwd", "nsa_compression_bwd", "nsa_sparse_selection_bwd"):
     _r, _a = SIGNATURES[_n]
