@@ -64,7 +64,7 @@ struct Shape {
 
 struct Layout {
   size_t krf = 0, kcf = 0, vrf = 0, vcf = 0, lse2 = 0, delta = 0, clean = 0, chunk = 0, csr_off = 0, csr_t = 0,
-         seg_off = 0, partial = 0, total = 0;
+         seg_off = 0, perm = 0, partial = 0, total = 0;
 };
 
 // Offsets into the caller's workspace (every buffer 256-byte aligned).
@@ -98,6 +98,7 @@ Layout make_layout(const Shape& s, bool bwd) {
       L.csr_off = take(BG * (s.nblk() + 1) * 4);
       L.seg_off = take(BG * (s.nblk() + 1) * 4);
       L.csr_t = take(BG * s.Tq * s.nslots * 4);
+      L.perm = take(BG * s.items_per_bg() * 4);
     }
   }
   if (bwd) L.partial = take(BG * s.items_per_bg() * dkdv_keys(s.br) * (size_t)(s.dk + s.dv) * 4);
@@ -301,6 +302,9 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
                      s.Tkv, fallback, causal, at<int>(ws, L.clean), at<int>(ws, L.chunk), s.nblk(), 0, st);
     launch_sel_csr(at<int>(ws, L.clean), at<int>(ws, L.chunk), s.Z, s.G, s.Tq, s.nslots, s.nblk(),
                    at<int>(ws, L.csr_off), at<int>(ws, L.csr_t), at<int>(ws, L.seg_off), s.seg(), st);
+    launch_sel_item_order(at<int>(ws, L.csr_off), at<int>(ws, L.csr_t), at<int>(ws, L.seg_off), s.Z * s.G, s.Tq,
+                          s.nslots, s.items_per_bg(), s.nblk(), s.lprime, s.seg(), at<int>(ws, L.perm), st);
+    a.item_perm = at<int>(ws, L.perm);
     a.sel = at<int>(ws, L.clean);
     a.csr_off = at<int>(ws, L.csr_off);
     a.csr_t = at<int>(ws, L.csr_t);

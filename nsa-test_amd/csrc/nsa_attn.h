@@ -74,6 +74,7 @@ struct AttnArgs {
   const int* csr_off;     // [B,G,nblk+1]
   const int* csr_t;       // [B,G,Tq*nslots] query timesteps per block, ascending
   const int* seg_off;     // [B,G,nblk+1] work-item prefix per block
+  const int* item_perm;   // [B*G*items_per_bg]: the dK/dV work item (bg * items_per_bg + item) of each workgroup
 };
 
 template <typename T, int DK, int DV, int BR>

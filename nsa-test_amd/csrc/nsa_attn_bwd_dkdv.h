@@ -112,13 +112,15 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   const int wave = tid >> 6;
   const int g4 = lane >> 4;
   const int c16 = lane & 15;
-  const int bg = blockIdx.y;
+  // selection: workgroups take the items in the order of their first query timestep
+  const int lin = BR == kSelection ? a.item_perm[blockIdx.y * gridDim.x + blockIdx.x] : 0;
+  const int bg = BR == kSelection ? lin / a.items_per_bg : blockIdx.y;
   const int b = bg / a.G;
   const int grp = bg % a.G;
   const int hpg = a.hpg;
   const IntDiv hdiv = IntDiv::make(hpg);
   const float scale2 = a.scale * kLog2e;
-  const int item = blockIdx.x;
+  const int item = BR == kSelection ? lin % a.items_per_bg : blockIdx.x;
 
   // ---- decode the work item: key tile + segment of rows ----
   int key0, blk_hi = a.Tkv;

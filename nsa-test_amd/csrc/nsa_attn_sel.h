@@ -265,6 +265,8 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
   constexpr int CT = CK / 16;
   __shared__ int s_lst[4][kSelMaxT * 64];
   __shared__ uint32_t s_bits[4][kSelMaxBlocks / 32];
+  // bf16: each wave's staged K rows of one 64-key tile (rowfrag order)
+  __shared__ __attribute__((aligned(16))) uint4 s_kt[4][sizeof(S) == 2 ? 4 * NKC * 64 : 1];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform control below
@@ -342,21 +344,77 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
     c_key0 = lo & ~31;
     return true;
   };
-  // K and V rowfrags of a tile feed S^T = K Q^T and dP^T = V dO^T; the K colfrags feed
-  // dQ^T += K^T dS^T.  The colfrags are requested once S^T / dP^T are issued and the
-  // next tile's rowfrags once this tile's are consumed, so loads overlap the softmax.
+  // K and V rowfrags of a tile feed S^T = K Q^T and dP^T = V dO^T; K^T fragments feed
+  // dQ^T += K^T dS^T.
+  //  bf16: the K rows of a tile go to the wave's own LDS region by direct-to-LDS loads
+  //    (24 KB at dk = 192); the rowfrags are read back as they are and the K^T fragments
+  //    with the LDS transpose load, so each (timestep, block) pair gathers K once (40
+  //    instead of 64 KB from L2 with V).  All of them are read into registers when the
+  //    tile starts, which frees the region for the next tile's copy at once.
+  //  fp32: K colfrags are read from the re-packed K^T (kcf) once S^T / dP^T are issued.
+  // The next tile's loads are issued once this tile's S^T and dP^T are, so they overlap
+  // the softmax and the dQ products.
+  constexpr bool kLdsK = sizeof(S) == 2;
+  constexpr int NVL = 4 * NVC;  // V fragment loads per tile
   uint4 kf[4][NKC], vf[4][NVC], knf[64 / CK][DK / 16];
-  auto load_rows = [&](int key0) {
+  uint4* kst = s_kt[wave];
+  auto load_k = [&](int key0) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int kc = 0; kc < NKC; ++kc) kf[ks][kc] = ld_rowfrag<T>(krf, (key0 >> 4) + ks, kc, DK, lane);
+      for (int kc = 0; kc < NKC; ++kc) {
+        if constexpr (kLdsK)
+          copy16_to_lds(krf + ((((int64_t)(key0 >> 4) + ks) * NKC + kc) * 64 + lane) * EPF, kst + (ks * NKC + kc) * 64);
+        else
+          kf[ks][kc] = ld_rowfrag<T>(krf, (key0 >> 4) + ks, kc, DK, lane);
+      }
+  };
+  auto load_v = [&](int key0) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int kc = 0; kc < NVC; ++kc) vf[ks][kc] = ld_rowfrag<T>(vrf, (key0 >> 4) + ks, kc, DV, lane);
+  };
+  // K^T fragment (32-key chunk kc2, features 16j..16j+15) from the staged rowfrags:
+  // lane (g4, f) needs K[key][16j + f] for keys 4g4..4g4+3 and 16+4g4..16+4g4+3 of the
+  // chunk (the C-permuted order); the transpose load gives each 16-lane group a 4-key x
+  // 16-feature block whose row rho is key 4g4+rho, lanes 4rho+q reading its features
+  // 4q..4q+3: in rowfrag (16-key group ks, chunk kc) feature e of key r sits at lane
+  // ((e % 32) / 8) * 16 + r, element e % 8.
+  auto knf_lds = [&](int kc2, int j) -> uint4 {
+    const int rho = c16 >> 2, q = c16 & 3;
+    const int e = 16 * j + 4 * q;  // first of the lane's four features
+    const int kc = e / KC, gp = (e % KC) / EPF, el = e % EPF;
+    const uint16_t* base = reinterpret_cast<const uint16_t*>(kst);
+    const int r = 4 * g4 + rho;
+    const uint16_t* p0 = base + (((2 * kc2) * NKC + kc) * 64 + gp * 16 + r) * EPF + el;
+    return ld_tr_pair(p0, NKC * 64 * EPF);  // second half: the next 16-key group
+  };
+  // bf16: the tile's K copy (issued before its V loads) has landed once at most NVL
+  // vector-memory operations are outstanding; read every K and K^T fragment of the tile
+  // into registers, then the region is free for the next tile's copy.
+  auto fetch_k = [&]() {
+    if constexpr (kLdsK) {
+      wait_vmcnt<NVL>();
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int kc = 0; kc < NKC; ++kc) kf[ks][kc] = kst[(ks * NKC + kc) * 64 + lane];
+#pragma unroll
+      for (int kc2 = 0; kc2 < 64 / CK; ++kc2)
+#pragma unroll
+        for (int j = 0; j < DK / 16; ++j) knf[kc2][j] = knf_lds(kc2, j);
+      wave_lds_sync();
+      asm volatile("" ::: "memory");
     }
   };
   bool have = advance();
-  if (have) load_rows(c_key0);
+  if (have) {
+    load_k(c_key0);
+    load_v(c_key0);
+  }
   // row statistics after the first tile's loads are issued (their O loads overlap them)
   float l2, dl;
   dq_row_stats<T, NVC>(a, b, colh, colt, colv, dof, g4, srow, l2, dl);
@@ -364,22 +422,36 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
     const int key0 = c_key0, blk = c_blk;
     const int blk_lo = blk * a.lprime;
     const int blk_hi = c_hi;
+    fetch_k();
+    const bool have_next = advance();
+    // the next tile's loads are unconditional (the last tile re-reads its own keys):
+    // a branch around them would make the compiler wait for every outstanding load at
+    // the join.  bf16: the K copy goes out now, a whole tile ahead of its use.
+    const int next_key0 = have_next ? c_key0 : key0;
+    if (kLdsK) load_k(next_key0);
     f32x4 st[4], dp[4];
+    // S^T first (its operands are in registers), then dP^T, whose V rows may still be
+    // arriving
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       st[ks] = zero4();
-      dp[ks] = zero4();
 #pragma unroll
       for (int kc = 0; kc < NKC; ++kc) st[ks] = Mma<T>::run(st[ks], kf[ks][kc], qf[kc]);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      dp[ks] = zero4();
 #pragma unroll
       for (int kc = 0; kc < NVC; ++kc) dp[ks] = Mma<T>::run(dp[ks], vf[ks][kc], dof[kc]);
     }
+    if constexpr (!kLdsK) {
 #pragma unroll
-    for (int kc2 = 0; kc2 < 64 / CK; ++kc2)
+      for (int kc2 = 0; kc2 < 64 / CK; ++kc2)
 #pragma unroll
-      for (int j = 0; j < DK / 16; ++j) knf[kc2][j] = ld_colfrag<T>(kcf, key0 / CK + kc2, j, DK, lane);
-    const bool have_next = advance();
-    if (have_next) load_rows(c_key0);
+        for (int j = 0; j < DK / 16; ++j) knf[kc2][j] = ld_colfrag<T>(kcf, key0 / CK + kc2, j, DK, lane);
+      load_k(next_key0);
+    }
+    load_v(next_key0);
 
     const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
     // end of the keys of this block the lane's column sees (blk_lo when none)

@@ -206,6 +206,15 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_wave_barrier();
 }
 
+// Waits until at most N of the wave's vector-memory operations are outstanding (they
+// complete in issue order for loads), leaving lgkmcnt / expcnt unconstrained; gfx9
+// s_waitcnt encoding: vmcnt bits [3:0] and [15:14], expcnt [6:4], lgkmcnt [11:8].
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // Store 4 consecutive values (one C-tile column slice) as T.
 template <typename T> __device__ __forceinline__ void store4(typename Store<T>::type* p, f32x4 v);
 template <> __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
