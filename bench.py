@@ -81,7 +81,9 @@ def make_workload(name, dev, seed=0):
         "k_sel": kk[1].requires_grad_(), "v_sel": vv[1].requires_grad_(),
         "k_win": kk[2].requires_grad_(), "v_win": vv[2].requires_grad_(),
         "gate_logits": rnd(B, H, T, 3).requires_grad_(),
-        "dO": rnd(B, H, T, dv, scale=1 / math.sqrt(dv)),
+        # the output gradient in the layout NSAAttention's o_proj backward hands over:
+        # a [B,H,T,dv] view of [B,T,H,dv] storage
+        "dO": rnd(B, T, H, dv, scale=1 / math.sqrt(dv)).permute(0, 2, 1, 3),
     }
     return cfg, mod, w
 

@@ -162,8 +162,13 @@ int nsa_sparse_selection_bwd(const void* Q, const void* K, const void* V, const 
  * position q_offset + r; masks, fixed blocks and the all-invalid fallback use positions).
  * For single-token decode over a cache: n_ctx_q = 1, q_offset = cache length - 1.
  * The sliding-window form also takes the key length n_ctx_kv (the reference kernel
- * assumes n_ctx_kv = n_ctx).  With q_offset = 0 (and n_ctx_kv = n_ctx) each behaves
- * exactly as the entry point it extends. */
+ * assumes n_ctx_kv = n_ctx) and, for the NSA module's forward (nsa/kernels.py:2429-2463),
+ * a gated-mix epilogue: with mix_out not null it also writes
+ *   mix_out[z,h,t,:] = g0 mix_o0[z,h,t,:] + g1 mix_o1[z,h,t,:] + g2 Out[z,h,t,:]
+ * (fp32 sum of the stored values, rounded once), g_k = mix_gates[k,z,h,t] (contiguous
+ * fp32 [3,Z,H,n_ctx]); mix_o0 / mix_o1 (the other two branch outputs) share Out's
+ * strides, mix_out has its own (stride_x*, unit feature stride).  With q_offset = 0,
+ * n_ctx_kv = n_ctx and mix_out null each behaves exactly as the entry point it extends. */
 int nsa_sliding_window_fwd_ex(const void* Q, const void* K, const void* V, void* Out, float sm_scale, float* L, float* M,
                            int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_qk,
                            int64_t stride_kz, int64_t stride_kg, int64_t stride_kn, int64_t stride_kk,
@@ -172,8 +177,9 @@ int nsa_sliding_window_fwd_ex(const void* Q, const void* K, const void* V, void*
                            int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t stride_mz,
                            int64_t stride_mh, int64_t stride_mm, int Z, int H, int n_kv_groups, int n_ctx,
                            int window_size, int head_dim_qk, int head_dim_v, int dtype,
-                           int n_ctx_kv, int q_offset, void* workspace,
-                           size_t workspace_bytes, nsa_stream_t stream);
+                           int n_ctx_kv, int q_offset, const void* mix_o0, const void* mix_o1,
+                           const float* mix_gates, void* mix_out, int64_t stride_xz, int64_t stride_xh,
+                           int64_t stride_xm, void* workspace, size_t workspace_bytes, nsa_stream_t stream);
 
 int nsa_compression_fwd_ex(const void* Q, const void* K_compressed, const void* V_compressed, const int32_t* Block_ends,
                         void* Out, float sm_scale, float* L, float* M, int64_t stride_qz, int64_t stride_qh,
@@ -216,8 +222,14 @@ int nsa_score_topn_ex(const void* q, const void* k_cmp, const int32_t* Block_end
  *   delta_in       null: as the entry point extended; otherwise the row sums
  *                  D = sum_d Out * dOut per (z, h, t) row, fp32, contiguous [Z, H, n_ctx_q],
  *                  which the backward then uses instead of reading Out.
- * With dq_accumulate = 0 and delta_in = null each behaves exactly as the entry point
- * it extends. */
+ *   row_gate       null: as the entry point extended; otherwise a per-row gate
+ *                  (fp32, contiguous [Z, H, n_ctx_q]): the branch's output gradient is
+ *                  row_gate[z,h,t] * dOut (the gated mix of the NSA module,
+ *                  nsa/kernels.py:2446-2463), so callers pass the mix's dOut unscaled.
+ *   row_dot        null, or fp32 contiguous [Z, H, n_ctx_q] receiving sum_d dOut * Out
+ *                  per row (the gradient of the row's gate); needs delta_in null.
+ * With dq_accumulate = 0 and the three pointers null each behaves exactly as the entry
+ * point it extends. */
 int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const void* Out, const void* dOut,
                            float sm_scale, const float* L, const float* M, int64_t stride_qz, int64_t stride_qh,
                            int64_t stride_qm, int64_t stride_qk, int64_t stride_kz, int64_t stride_kg,
@@ -230,7 +242,7 @@ int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const
                            int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg, int64_t stride_dvn,
                            int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx, int window_size,
                            int head_dim_qk, int head_dim_v, int dtype,
-                           int dq_accumulate, const float* delta_in, void* workspace, size_t workspace_bytes,
+                           int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace, size_t workspace_bytes,
                            nsa_stream_t stream);
 
 int nsa_compression_bwd_ex(const void* Q, const void* K_blocks, const void* V_blocks, const int32_t* Block_ends,
@@ -245,7 +257,7 @@ int nsa_compression_bwd_ex(const void* Q, const void* K_blocks, const void* V_bl
                         int64_t stride_dkg, int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz,
                         int64_t stride_dvg, int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups,
                         int n_ctx_q, int n_blocks, int head_dim_qk, int head_dim_v, int dtype,
-                        int dq_accumulate, const float* delta_in, void* workspace,
+                        int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
                         size_t workspace_bytes, nsa_stream_t stream);
 
 int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, const void* Block_indices, const void* Out,
@@ -262,7 +274,7 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
                              int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
                              int n_ctx_kv, int n_slots, int block_size_selection, int is_causal, int index_is_int64,
                              int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype,
-                             int dq_accumulate, const float* delta_in, void* workspace,
+                             int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream);
 
 

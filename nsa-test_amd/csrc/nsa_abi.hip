@@ -64,7 +64,7 @@ struct Shape {
 
 struct Layout {
   size_t krf = 0, kcf = 0, vrf = 0, vcf = 0, lse2 = 0, delta = 0, clean = 0, chunk = 0, csr_off = 0, csr_t = 0,
-         seg_off = 0, perm = 0, partial = 0, total = 0;
+         seg_off = 0, partial = 0, total = 0;
 };
 
 // Offsets into the caller's workspace (every buffer 256-byte aligned).
@@ -98,7 +98,6 @@ Layout make_layout(const Shape& s, bool bwd) {
       L.csr_off = take(BG * (s.nblk() + 1) * 4);
       L.seg_off = take(BG * (s.nblk() + 1) * 4);
       L.csr_t = take(BG * s.Tq * s.nslots * 4);
-      L.perm = take(BG * s.items_per_bg() * 4);
     }
   }
   if (bwd) L.partial = take(BG * s.items_per_bg() * dkdv_keys(s.br) * (size_t)(s.dk + s.dv) * 4);
@@ -159,6 +158,12 @@ struct FwdIO {
   void* Out;
   float *L, *M;
   int64_t sq[4], sk[4], sv[4], so[4], sl[3], sm[3];
+  // sliding extension only: gated mix epilogue (null mix_out: none)
+  const void* mix_o0 = nullptr;
+  const void* mix_o1 = nullptr;
+  const float* mix_gates = nullptr;
+  void* mix_out = nullptr;
+  int64_t sx[3] = {0, 0, 0};
 };
 
 int run_fwd(const Shape& s, const FwdIO& io, float scale, int window, const int32_t* block_ends, const void* idx,
@@ -170,6 +175,13 @@ int run_fwd(const Shape& s, const FwdIO& io, float scale, int window, const int3
   if (!row_ok(io.Out, io.so[3], io.so[0], io.so[1], io.so[2], s.esz(), s.Z, s.H, s.Tq))
     return fail(NSA_ERR_LAYOUT, "Out needs unit feature stride and 16-byte aligned rows");
   if (s.br == kSliding && window <= 0) return fail(NSA_ERR_INVALID, "window_size=%d must be positive", window);
+  if (io.mix_out) {
+    if (!io.mix_o0 || !io.mix_o1 || !io.mix_gates) return fail(NSA_ERR_INVALID, "mix needs mix_o0, mix_o1 and mix_gates");
+    if (!row_ok(io.mix_out, 1, io.sx[0], io.sx[1], io.sx[2], s.esz(), s.Z, s.H, s.Tq) ||
+        !row_ok(io.mix_o0, io.so[3], io.so[0], io.so[1], io.so[2], s.esz(), s.Z, s.H, s.Tq) ||
+        !row_ok(io.mix_o1, io.so[3], io.so[0], io.so[1], io.so[2], s.esz(), s.Z, s.H, s.Tq))
+      return fail(NSA_ERR_LAYOUT, "mix outputs need 16-byte aligned unit-stride rows");
+  }
   const Layout L = make_layout(s, false);
   if (ws_bytes < L.total) return fail(NSA_ERR_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, L.total);
   if (s.Tq == 0) return NSA_OK;
@@ -194,8 +206,13 @@ int run_fwd(const Shape& s, const FwdIO& io, float scale, int window, const int3
   a.window = window;
   a.block_ends = block_ends;
   a.causal = causal;
-  const bool sel = s.br == kSelection;
-  auto opt = [&](size_t off, bool use) -> void* { return use ? at<char>(ws, off) : nullptr; };
+  a.mix_out = io.mix_out;
+  a.smx_b = io.sx[0];
+  a.smx_h = io.sx[1];
+  a.smx_t = io.sx[2];
+  a.mix_o0 = io.mix_o0;
+  a.mix_o1 = io.mix_o1;
+  a.mix_gates = io.mix_gates;
   a.krf = at<char>(ws, L.krf);
   a.vcf = at<char>(ws, L.vcf);
 
@@ -223,6 +240,8 @@ struct BwdIO {
   int64_t sq[4], sk[4], sv[4], so[4], sl[3], sm[3], sdq[4], sdk[4], sdv[4];
   int dq_acc = 0;                   // extension entry points only: add into dQ
   const float* delta_in = nullptr;  // extension entry points only: precomputed row sums
+  const float* row_gate = nullptr;  // extension entry points only: per-row gate of dOut
+  float* row_dot = nullptr;         // extension entry points only: receives sum_d dOut * Out
 };
 
 int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int32_t* block_ends, const void* idx,
@@ -236,6 +255,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   if (!row_ok(io.dQ, io.sdq[3], io.sdq[0], io.sdq[1], io.sdq[2], s.esz(), s.Z, s.H, s.Tq))
     return fail(NSA_ERR_LAYOUT, "dQ needs unit feature stride and 16-byte aligned rows");
   if (s.br == kSliding && window <= 0) return fail(NSA_ERR_INVALID, "window_size=%d must be positive", window);
+  if (io.row_dot && io.delta_in) return fail(NSA_ERR_INVALID, "row_dot needs delta_in = null (it is computed from Out)");
   const Layout L = make_layout(s, true);
   if (ws_bytes < L.total) return fail(NSA_ERR_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, L.total);
   if (s.Tq == 0) return NSA_OK;
@@ -268,6 +288,8 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.sdq_t = io.sdq[2];
   a.dq_acc = io.dq_acc;
   a.delta_in = io.delta_in;
+  a.row_gate = io.row_gate;
+  a.row_dot = io.row_dot;
   a.dk = io.dK;
   a.sdk_b = io.sdk[0];
   a.sdk_g = io.sdk[1];
@@ -302,9 +324,6 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
                      s.Tkv, fallback, causal, at<int>(ws, L.clean), at<int>(ws, L.chunk), s.nblk(), 0, st);
     launch_sel_csr(at<int>(ws, L.clean), at<int>(ws, L.chunk), s.Z, s.G, s.Tq, s.nslots, s.nblk(),
                    at<int>(ws, L.csr_off), at<int>(ws, L.csr_t), at<int>(ws, L.seg_off), s.seg(), st);
-    launch_sel_item_order(at<int>(ws, L.csr_off), at<int>(ws, L.csr_t), at<int>(ws, L.seg_off), s.Z * s.G, s.Tq,
-                          s.nslots, s.items_per_bg(), s.nblk(), s.lprime, s.seg(), at<int>(ws, L.perm), st);
-    a.item_perm = at<int>(ws, L.perm);
     a.sel = at<int>(ws, L.clean);
     a.csr_off = at<int>(ws, L.csr_off);
     a.csr_t = at<int>(ws, L.csr_t);
@@ -364,7 +383,7 @@ int nsa::set_error(int code, const char* msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 
-int nsa_abi_version(void) { return 1; }
+int nsa_abi_version(void) { return 2; }
 const char* nsa_last_error(void) { return g_err; }
 int nsa_head_dims_supported(int dtype, int dk, int dv) {
   return (dtype == NSA_F32 || dtype == NSA_BF16) && dims_supported(dk, dv);
@@ -557,11 +576,13 @@ int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const
                            int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg, int64_t stride_dvn,
                            int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx, int window_size,
                            int head_dim_qk, int head_dim_v, int dtype,
-                           int dq_accumulate, const float* delta_in, void* workspace, size_t workspace_bytes,
+                           int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace, size_t workspace_bytes,
                            nsa_stream_t stream) {
   NSA_BWD_IO
   io.dq_acc = dq_accumulate ? 1 : 0;
   io.delta_in = delta_in;
+  io.row_gate = row_gate;
+  io.row_dot = row_dot;
   Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64, window_size};
   return run_bwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
                  (hipStream_t)stream);
@@ -579,11 +600,13 @@ int nsa_compression_bwd_ex(const void* Q, const void* K, const void* V, const in
                         int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
                         int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
                         int n_blocks, int head_dim_qk, int head_dim_v, int dtype,
-                        int dq_accumulate, const float* delta_in, void* workspace,
+                        int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
                         size_t workspace_bytes, nsa_stream_t stream) {
   NSA_BWD_IO
   io.dq_acc = dq_accumulate ? 1 : 0;
   io.delta_in = delta_in;
+  io.row_gate = row_gate;
+  io.row_dot = row_dot;
   Shape s{kCompression, dtype, Z, H, n_kv_groups, n_ctx_q, n_blocks, head_dim_qk, head_dim_v, 0, 64};
   if (n_blocks > 0 && !Block_ends) return fail(NSA_ERR_INVALID, "Block_ends is null");
   return run_bwd(s, io, sm_scale, 0, Block_ends, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
@@ -604,11 +627,13 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
                              int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
                              int n_ctx_kv, int n_slots, int block_size_selection, int is_causal, int index_is_int64,
                              int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype,
-                             int dq_accumulate, const float* delta_in, void* workspace,
+                             int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream) {
   NSA_BWD_IO
   io.dq_acc = dq_accumulate ? 1 : 0;
   io.delta_in = delta_in;
+  io.row_gate = row_gate;
+  io.row_dot = row_dot;
   Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
           block_size_selection};
   if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
@@ -626,9 +651,17 @@ float* M,
                            int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t stride_mz,
                            int64_t stride_mh, int64_t stride_mm, int Z, int H, int n_kv_groups, int n_ctx,
                            int window_size, int head_dim_qk, int head_dim_v, int dtype, int n_ctx_kv, int q_offset,
-                           void* workspace,
+                           const void* mix_o0, const void* mix_o1, const float* mix_gates, void* mix_out,
+                           int64_t stride_xz, int64_t stride_xh, int64_t stride_xm, void* workspace,
                            size_t workspace_bytes, nsa_stream_t stream) {
   NSA_FWD_IO
+  io.mix_o0 = mix_o0;
+  io.mix_o1 = mix_o1;
+  io.mix_gates = mix_gates;
+  io.mix_out = mix_out;
+  io.sx[0] = stride_xz;
+  io.sx[1] = stride_xh;
+  io.sx[2] = stride_xm;
   Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx_kv, head_dim_qk, head_dim_v, 0, 64, window_size};
   s.q0 = q_offset;
   return run_fwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,

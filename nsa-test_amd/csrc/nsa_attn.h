@@ -48,6 +48,15 @@ struct AttnArgs {
   int64_t sdq_b, sdq_h, sdq_t;
   int dq_acc;  // 1: dQ is added to the destination's values instead of overwriting them
   const float* delta_in;  // null, or the caller's rowsum(O*dO) [B,H,Tq] compact (O is then not read)
+  // gated mix (the NSA module): this branch's output gradient is row_gate[row] * dOut
+  const float* row_gate;  // [B,H,Tq] compact fp32 activated gate of this branch, or null (1)
+  float* row_dot;         // [B,H,Tq] compact fp32: receives sum_d dOut * Out per row, or null
+  // forward mix epilogue (sliding / compression kernel): mix_out = g0 mix_o0 + g1 mix_o1 + g2 Out
+  void* mix_out;
+  int64_t smx_b, smx_h, smx_t;
+  const void* mix_o0;  // the other two branch outputs, with Out's strides
+  const void* mix_o1;
+  const float* mix_gates;  // [3,B,H,Tq] compact fp32 activated gates (0, 1: mix_o0 / mix_o1, 2: Out)
   const float* lse2;   // [B,H,Tq] compact: (M+L)*log2(e), +inf for empty rows
   const float* delta;  // [B,H,Tq] compact: rowsum(O*dO)
   // dK/dV destination (accumulated into, any strides) or fp32 partials
@@ -74,7 +83,6 @@ struct AttnArgs {
   const int* csr_off;     // [B,G,nblk+1]
   const int* csr_t;       // [B,G,Tq*nslots] query timesteps per block, ascending
   const int* seg_off;     // [B,G,nblk+1] work-item prefix per block
-  const int* item_perm;   // [B*G*items_per_bg]: the dK/dV work item (bg * items_per_bg + item) of each workgroup
 };
 
 template <typename T, int DK, int DV, int BR>

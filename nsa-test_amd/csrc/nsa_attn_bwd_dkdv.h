@@ -104,6 +104,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   __shared__ int s_t[NB][RC];
   __shared__ float s_l2[NB][RC];
   __shared__ float s_dl[NB][RC];
+  __shared__ float s_g[NB][RC];  // the rows' gates (1 without a row gate)
   __shared__ int s_be[KEYS];
   __shared__ int s_tl[kSegTMax];  // selection: the item's query timesteps
 
@@ -112,15 +113,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   const int wave = tid >> 6;
   const int g4 = lane >> 4;
   const int c16 = lane & 15;
-  // selection: workgroups take the items in the order of their first query timestep
-  const int lin = BR == kSelection ? a.item_perm[blockIdx.y * gridDim.x + blockIdx.x] : 0;
-  const int bg = BR == kSelection ? lin / a.items_per_bg : blockIdx.y;
+  const int bg = blockIdx.y;
   const int b = bg / a.G;
   const int grp = bg % a.G;
   const int hpg = a.hpg;
   const IntDiv hdiv = IntDiv::make(hpg);
   const float scale2 = a.scale * kLog2e;
-  const int item = BR == kSelection ? lin % a.items_per_bg : blockIdx.x;
+  const int item = blockIdx.x;
 
   // ---- decode the work item: key tile + segment of rows ----
   int key0, blk_hi = a.Tkv;
@@ -223,7 +222,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   // ---- register prefetch of one chunk (pairs of adjacent rows) ----
   uint4 pq[NQ][2], po[NO][2];
   int pr_t = -1;
-  float pr_l2 = INFINITY, pr_dl = 0.f;
+  float pr_l2 = INFINITY, pr_dl = 0.f, pr_g = 1.f;
   // Rows past the item's end re-read its last row (finite data); they are masked
   // (p = 0) through s_t = -1, so every load is unconditional and the loads of a chunk
   // issue back to back.
@@ -280,6 +279,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
       const int64_t srow = ((int64_t)b * a.H + h) * a.Tq + t;
       pr_l2 = a.lse2[srow];
       pr_dl = a.delta[srow];
+      pr_g = a.row_gate ? a.row_gate[srow] : 1.f;
       pr_t = f < f_hi ? t : -1;
     }
   };
@@ -328,6 +328,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
       s_t[buf][tid] = pr_t;
       s_l2[buf][tid] = pr_l2;
       s_dl[buf][tid] = pr_dl;
+      s_g[buf][tid] = pr_g;
     }
   };
 
@@ -386,6 +387,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
             else ok = t >= 0 && (!a.causal || mykey <= t) && mykey < blk_hi;
             p = ok ? fast_exp2(sacc[i] * scale2 - s_l2[buf][r]) : 0.f;
           }
+          p *= s_g[buf][r];  // gated: the rows' output gradient is g dO
           pt[rs][i] = p;
           dst[rs][i] = p * (pacc[i] - s_dl[buf][r]);
         }

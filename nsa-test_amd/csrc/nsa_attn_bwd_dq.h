@@ -148,8 +148,8 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
     load_be(tile_key0(0));
   }
   // row statistics after the first tile's copies are issued (their O loads overlap them)
-  float l2, dl;
-  dq_row_stats<T, NVC>(a, b, colh, colt, colv, dof, g4, srow, l2, dl);
+  float l2, dl, rgate;
+  dq_row_stats<T, NVC>(a, b, colh, colt, colv, dof, g4, srow, l2, dl, rgate);
 
   for (int it = 0; it < ntiles; ++it) {
     const int key0 = tile_key0(it);
@@ -231,9 +231,10 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
 #pragma unroll
       for (int j = 0; j < DK / 16; ++j) dq_prev[j] = load4_raw<T>(dqp + j * 16 + 4 * g4);
     }
+    const float sg = a.scale * rgate;
 #pragma unroll
     for (int j = 0; j < DK / 16; ++j) {
-      f32x4 v = dqa[j] * a.scale;
+      f32x4 v = dqa[j] * sg;
       if (a.dq_acc) v += raw4_f32(dq_prev[j]);
       store4<T>(dqp + j * 16 + 4 * g4, v);
     }

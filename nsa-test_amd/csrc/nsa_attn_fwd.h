@@ -19,6 +19,7 @@
 //   selection   key j visible iff j <= t and j lies in one of the row's selected
 //               blocks [idx*l', idx*l'+l') (union, so a repeated index counts once)
 #pragma once
+#include <algorithm>
 #include "nsa_attn.h"
 #include "nsa_device.h"
 #include "nsa_attn_sel.h"
@@ -285,22 +286,92 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   }
 
   // ---- epilogue: normalise, store O, L = log(l), M = max s -----------------------
+  // bf16: the workgroup's output rows are staged in LDS (free once every wave is past the
+  // tile loop) and stored as 16-byte row pieces, 16 lanes per 256-byte row, together with
+  // the gated mix when asked; fp32 stores from the accumulator lanes.
+  constexpr bool kStage = sizeof(S) == 2;
+  constexpr int DVP = DV + 8;  // staged row pitch (elements): 16-byte pad against bank conflicts
   S* obase = reinterpret_cast<S*>(a.o);
+  S* stage = reinterpret_cast<S*>(fwd_lds);
+  if constexpr (kStage) __syncthreads();
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) {
     if (!colv[s]) continue;
     const float inv = lsum[s] > 0.f ? 1.f / lsum[s] : 0.f;
     // the sum relative to the true maximum (m2 <= mtrue, equal when both are -inf)
     if (lsum[s] > 0.f) lsum[s] *= fast_exp2(m2[s] - mtrue[s]);
-    S* op = obase + b * a.so_b + (int64_t)colh[s] * a.so_h + (int64_t)colt[s] * a.so_t;
+    if constexpr (kStage) {
+      S* row = stage + ((wave * NSUB + s) * 16 + c16) * DVP;
 #pragma unroll
-    for (int j = 0; j < DV / 16; ++j) store4<T>(op + j * 16 + 4 * g4, oacc[s][j] * inv);
+      for (int j = 0; j < DV / 16; ++j) store4<T>(row + j * 16 + 4 * g4, oacc[s][j] * inv);
+    } else {
+      const int64_t ooff = b * a.so_b + (int64_t)colh[s] * a.so_h + (int64_t)colt[s] * a.so_t;
+#pragma unroll
+      for (int j = 0; j < DV / 16; ++j) store4<T>(obase + ooff + j * 16 + 4 * g4, oacc[s][j] * inv);
+      if (a.mix_out) {
+        // gated mix of the three branch outputs as stored: g0 o_0 + g1 o_1 + g2 o,
+        // summed in fp32 and rounded once
+        const int64_t srow = ((int64_t)b * a.H + colh[s]) * a.Tq + colt[s];
+        const int64_t bht = (int64_t)a.B * a.H * a.Tq;
+        const float g0 = a.mix_gates[srow], g1 = a.mix_gates[bht + srow], g2 = a.mix_gates[2 * bht + srow];
+        const S* o0 = reinterpret_cast<const S*>(a.mix_o0) + ooff;
+        const S* o1 = reinterpret_cast<const S*>(a.mix_o1) + ooff;
+        S* xp = reinterpret_cast<S*>(a.mix_out) + b * a.smx_b + (int64_t)colh[s] * a.smx_h +
+                (int64_t)colt[s] * a.smx_t;
+#pragma unroll
+        for (int j = 0; j < DV / 16; ++j) {
+          const int e = j * 16 + 4 * g4;
+          const f32x4 own = oacc[s][j] * inv;
+          const f32x4 x0 = load4<T>(o0 + e), x1 = load4<T>(o1 + e);
+          f32x4 m;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) m[u] = g0 * x0[u] + g1 * x1[u] + g2 * own[u];
+          store4<T>(xp + e, m);
+        }
+      }
+    }
     if (g4 == 0) {
       if (a.L)
         a.L[b * a.sl_b + (int64_t)colh[s] * a.sl_h + (int64_t)colt[s] * a.sl_t] =
             lsum[s] > 0.f ? logf(lsum[s]) : -INFINITY;
       if (a.M)
         a.M[b * a.sm_b + (int64_t)colh[s] * a.sm_h + (int64_t)colt[s] * a.sm_t] = mtrue[s] * kLn2;
+    }
+  }
+  if constexpr (kStage) {
+    __syncthreads();
+    constexpr int PPR = DV / EPF;  // 16-byte pieces per row
+    const int nrow = min(kFwdCols, ncols - col_base);
+    const IntDiv hdiv = IntDiv::make(hpg);
+    const int64_t bht = (int64_t)a.B * a.H * a.Tq;
+    for (int p = tid; p < nrow * PPR; p += 64 * NW) {
+      const int cl = p / PPR, e = (p % PPR) * EPF;
+      const int f = col_base + cl;
+      const int t = hdiv.div(f), h = grp * hpg + hdiv.mod(f);
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + cl * DVP + e);
+      const int64_t ooff = b * a.so_b + (int64_t)h * a.so_h + (int64_t)t * a.so_t;
+      *reinterpret_cast<uint4*>(obase + ooff + e) = v;
+      if (a.mix_out) {
+        // gated mix of the three branch outputs as stored: g0 o_0 + g1 o_1 + g2 o,
+        // summed in fp32 and rounded once
+        const int64_t srow = ((int64_t)b * a.H + h) * a.Tq + t;
+        const float g0 = a.mix_gates[srow], g1 = a.mix_gates[bht + srow], g2 = a.mix_gates[2 * bht + srow];
+        const uint4 u0 = *reinterpret_cast<const uint4*>(reinterpret_cast<const S*>(a.mix_o0) + ooff + e);
+        const uint4 u1 = *reinterpret_cast<const uint4*>(reinterpret_cast<const S*>(a.mix_o1) + ooff + e);
+        const uint32_t w0[4] = {u0.x, u0.y, u0.z, u0.w}, w1[4] = {u1.x, u1.y, u1.z, u1.w};
+        const uint32_t w2[4] = {v.x, v.y, v.z, v.w};
+        uint32_t r[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const float lo = g0 * __uint_as_float(w0[k] << 16) + g1 * __uint_as_float(w1[k] << 16) +
+                           g2 * __uint_as_float(w2[k] << 16);
+          const float hi = g0 * __uint_as_float(w0[k] & 0xffff0000u) + g1 * __uint_as_float(w1[k] & 0xffff0000u) +
+                           g2 * __uint_as_float(w2[k] & 0xffff0000u);
+          r[k] = pack_bf16x2(lo, hi);
+        }
+        S* xp = reinterpret_cast<S*>(a.mix_out) + b * a.smx_b + (int64_t)h * a.smx_h + (int64_t)t * a.smx_t;
+        *reinterpret_cast<uint4*>(xp + e) = make_uint4(r[0], r[1], r[2], r[3]);
+      }
     }
   }
 }
@@ -311,7 +382,9 @@ void launch_attn_fwd(const AttnArgs& a, hipStream_t s) {
     launch_attn_sel_fwd<T, DK, DV>(a, s);  // per-wave selection kernel
   } else {
     using FT = FwdTile<T, DK, DV>;
-    const size_t lds = (size_t)FT::NBUF * FT::BYTES;
+    // the K/V tile stages, reused by the bf16 epilogue for the workgroup's output rows
+    const size_t stage = sizeof(typename Store<T>::type) == 2 ? (size_t)kFwdCols * (DV + 8) * 2 : 0;
+    const size_t lds = std::max((size_t)FT::NBUF * FT::BYTES, stage);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, DK, DV, BR>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     dim3 grid((a.Tq * a.hpg + kFwdCols - 1) / kFwdCols, a.B * a.G);

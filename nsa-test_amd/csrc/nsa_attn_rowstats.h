@@ -1,6 +1,11 @@
 // Backward row statistics, computed by the dQ kernels for their own query columns:
 //   delta = sum_d O[d] * dO[d]   (fp32; or the caller's precomputed sums, delta_in)
 //   lse2  = (M + L) * log2(e)    (+inf when L = -inf: the row saw no key, every p is 0)
+//   gate  = row_gate[row]        (1 without a row gate)
+// With a row gate g the branch's output gradient is g dO: dP, D and dS all scale by g,
+// so the kernels keep D = sum_d O dO unscaled, multiply dQ by g at the end and the
+// probabilities of dK / dV by g per row; row_dot (when given) receives that unscaled D,
+// the gate's own gradient.
 // The dQ kernels use them directly and store them for the dK/dV kernel, which runs
 // after dQ on the same stream (one pass over O fewer than a separate statistics
 // kernel: dO is already in the dQ kernel's registers).
@@ -16,7 +21,7 @@ namespace nsa {
 template <typename T, int NVC>
 __device__ __forceinline__ void dq_row_stats(const AttnArgs& a, int b, int colh, int colt, bool colv,
                                              const uint4 (&dof)[NVC], int g4, int64_t srow, float& l2,
-                                             float& dl) {
+                                             float& dl, float& gate) {
   using S = typename Store<T>::type;
   constexpr int EPF = Elem<T>::kPerFrag;
   constexpr int KC = Elem<T>::kKChunk;
@@ -38,6 +43,7 @@ __device__ __forceinline__ void dq_row_stats(const AttnArgs& a, int b, int colh,
     dl = colv ? acc : 0.f;
   }
   l2 = INFINITY;
+  gate = (a.row_gate && colv) ? a.row_gate[srow] : 1.f;
   if (colv) {
     const float L = a.L[b * a.sl_b + (int64_t)colh * a.sl_h + (int64_t)colt * a.sl_t];
     const float M = a.M[b * a.sm_b + (int64_t)colh * a.sm_h + (int64_t)colt * a.sm_t];
@@ -45,6 +51,7 @@ __device__ __forceinline__ void dq_row_stats(const AttnArgs& a, int b, int colh,
     if (g4 == 0) {
       const_cast<float*>(a.delta)[srow] = dl;
       const_cast<float*>(a.lse2)[srow] = l2;
+      if (a.row_dot) a.row_dot[srow] = dl;
     }
   }
 }

@@ -416,8 +416,8 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
     load_v(c_key0);
   }
   // row statistics after the first tile's loads are issued (their O loads overlap them)
-  float l2, dl;
-  dq_row_stats<T, NVC>(a, b, colh, colt, colv, dof, g4, srow, l2, dl);
+  float l2, dl, rgate;
+  dq_row_stats<T, NVC>(a, b, colh, colt, colv, dof, g4, srow, l2, dl, rgate);
   while (have) {
     const int key0 = c_key0, blk = c_blk;
     const int blk_lo = blk * a.lprime;
@@ -482,9 +482,10 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
 #pragma unroll
       for (int j = 0; j < DK / 16; ++j) dq_prev[j] = load4_raw<T>(dqp + j * 16 + 4 * g4);
     }
+    const float sg = a.scale * rgate;
 #pragma unroll
     for (int j = 0; j < DK / 16; ++j) {
-      f32x4 v = dqa[j] * a.scale;
+      f32x4 v = dqa[j] * sg;
       if (a.dq_acc) v += raw4_f32(dq_prev[j]);  // the caller's running dQ sum
       store4<T>(dqp + j * 16 + 4 * g4, v);
     }

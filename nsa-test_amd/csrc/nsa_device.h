@@ -223,6 +223,14 @@ template <> __device__ __forceinline__ void store4<float>(float* p, f32x4 v) {
 template <> __device__ __forceinline__ void store4<bf16>(uint16_t* p, f32x4 v) {
   *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
+// The values 4 consecutive T elements would hold once stored (rounded to T).
+template <typename T> __device__ __forceinline__ f32x4 round4(f32x4 v);
+template <> __device__ __forceinline__ f32x4 round4<float>(f32x4 v) { return v; }
+template <> __device__ __forceinline__ f32x4 round4<bf16>(f32x4 v) {
+  return f32x4{bf16_bits_to_f32(f32_to_bf16_bits(v[0])), bf16_bits_to_f32(f32_to_bf16_bits(v[1])),
+               bf16_bits_to_f32(f32_to_bf16_bits(v[2])), bf16_bits_to_f32(f32_to_bf16_bits(v[3]))};
+}
+
 // 4 consecutive T values in storage form (8 bytes bf16, 16 bytes fp32): loaded early,
 // converted and added later.
 template <typename T> struct Raw4 { typedef uint4 type; };

@@ -27,8 +27,6 @@ void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g,
 void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int nslots, int nblk, int* csr_off,
                     int* csr_t, int* seg_off, int seg, hipStream_t st);
 int sel_csr_chunks(int Tq);
-void launch_sel_item_order(const int* csr_off, const int* csr_t, const int* seg_off, int BG, int Tq, int nslots,
-                           int items_per_bg, int nblk, int lprime, int seg, int* perm, hipStream_t st);
 
 // record an error message for nsa_last_error(); returns `code`
 int set_error(int code, const char* msg);

@@ -166,59 +166,6 @@ __global__ __launch_bounds__(64) void sel_csr_fill_kernel(const int* clean, cons
   }
 }
 
-// One workgroup: the dK/dV work items of every (b, g), ordered by the first query
-// timestep each reads (a counting sort over timestep buckets).  The dK/dV kernel runs
-// item perm[i] as its i-th workgroup, so the items in flight at any time read the query
-// and dO rows of nearby timesteps, which then stay in the L2 / last-level cache instead
-// of being re-read from HBM by every block that selected them.  The order only decides
-// scheduling (each item writes its own partial), so the atomics' nondeterministic order
-// within a bucket does not change any result.  Items past a group's work list go last.
-constexpr int kOrderBuckets = 1024;
-__global__ __launch_bounds__(1024) void sel_item_order_kernel(const int* csr_off, const int* csr_t,
-                                                              const int* seg_off, int BG, int items_per_bg, int nblk,
-                                                              int nsubblk, int seg, int64_t csr_stride, int shift,
-                                                              int* perm) {
-  __shared__ int hist[kOrderBuckets + 1];
-  const int tid = threadIdx.x;
-  const int n = BG * items_per_bg;
-  for (int i = tid; i <= kOrderBuckets; i += 1024) hist[i] = 0;
-  __syncthreads();
-  auto bucket_of = [&](int v) -> int {
-    const int bg = v / items_per_bg, item = v % items_per_bg;
-    const int sidx = item / nsubblk;
-    const int* so = seg_off + (int64_t)bg * (nblk + 1);
-    if (sidx >= so[nblk]) return kOrderBuckets;
-    int lo = 0, hi = nblk;  // largest j with so[j] <= sidx
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (so[mid] <= sidx) lo = mid;
-      else hi = mid;
-    }
-    const int e = csr_off[(int64_t)bg * (nblk + 1) + lo] + (sidx - so[lo]) * seg;
-    return min(kOrderBuckets - 1, csr_t[(int64_t)bg * csr_stride + e] >> shift);
-  };
-  for (int v = tid; v < n; v += 1024) atomicAdd(&hist[bucket_of(v)], 1);
-  __syncthreads();
-  if (tid == 0) {  // exclusive scan (1025 entries, once)
-    int run = 0;
-    for (int i = 0; i <= kOrderBuckets; ++i) {
-      const int c = hist[i];
-      hist[i] = run;
-      run += c;
-    }
-  }
-  __syncthreads();
-  for (int v = tid; v < n; v += 1024) perm[atomicAdd(&hist[bucket_of(v)], 1)] = v;
-}
-
-void launch_sel_item_order(const int* csr_off, const int* csr_t, const int* seg_off, int BG, int Tq, int nslots,
-                           int items_per_bg, int nblk, int lprime, int seg, int* perm, hipStream_t st) {
-  int shift = 0;
-  while ((Tq >> shift) >= kOrderBuckets) ++shift;
-  hipLaunchKernelGGL(sel_item_order_kernel, dim3(1), dim3(1024), 0, st, csr_off, csr_t, seg_off, BG, items_per_bg,
-                     nblk, (lprime + 63) / 64, seg, (int64_t)Tq * nslots, shift, perm);
-}
-
 void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g, int64_t si_t, int64_t si_n, int B,
                       int G, int Tq, int n_in, int nslots, int lprime, int Tkv, int fallback, int causal, int* clean,
                       int* chunk_cnt, int nblk, int q0, hipStream_t st) {

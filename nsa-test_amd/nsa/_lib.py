@@ -12,7 +12,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libnsa_hip.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 NSA_F32 = 0
 NSA_BF16 = 1
@@ -48,12 +48,14 @@ SIGNATURES = {
 }
 # the allocation-free sliding-window forward: no workspace arguments
 SIGNATURES["nsa_sliding_window_fwd_noalloc"] = (_I, SIGNATURES["nsa_sliding_window_fwd"][1][:-3] + [_P])
-# the backward extensions: dq_accumulate (int) and delta_in (pointer) before the workspace
+# the backward extensions: dq_accumulate (int), delta_in, row_gate, row_dot (pointers)
+# before the workspace
 for _n in ("nsa_sliding_window_bwd", "nsa_compression_bwd", "nsa_sparse_selection_bwd"):
     _r, _a = SIGNATURES[_n]
-    SIGNATURES[_n + "_ex"] = (_r, [*_a[:-3], _I, _P, *_a[-3:]])
-# the forward / scoring decode extensions: q_offset (sliding also n_ctx_kv) before the workspace
-for _n, _extra in (("nsa_sliding_window_fwd", [_I, _I]), ("nsa_compression_fwd", [_I]),
+    SIGNATURES[_n + "_ex"] = (_r, [*_a[:-3], _I, _P, _P, _P, *_a[-3:]])
+# the forward / scoring decode extensions: q_offset (sliding also n_ctx_kv and the gated
+# mix: mix_o0, mix_o1, mix_gates, mix_out, three strides) before the workspace
+for _n, _extra in (("nsa_sliding_window_fwd", [_I, _I, _P, _P, _P, _P, _L, _L, _L]), ("nsa_compression_fwd", [_I]),
                    ("nsa_sparse_selection_fwd", [_I])):
     _r, _a = SIGNATURES[_n]
     SIGNATURES[_n + "_ex"] = (_r, [*_a[:-3], *_extra, *_a[-3:]])

@@ -78,11 +78,14 @@ def _branch_extra(branch, Tkv, block_ends, indices, lprime):
 
 def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=None, indices=None,
              lprime: int = 64, causal: bool = True, fallback: bool = False, out=None, L=None, M=None,
-             q_offset: int = 0):
+             q_offset: int = 0, mix=None):
     """Forward of one NSA branch.  Returns (out, L, M); `out`, `L`, `M` are written in
     place when given (with their own strides).  q_offset: absolute position of query row
     0 in the key sequence (decode past a cache; the sliding window then takes its key
-    length from k)."""
+    length from k).  mix (sliding only): (o0, o1, gates, mix_out) -- the kernel also
+    writes mix_out = gates[0] o0 + gates[1] o1 + gates[2] out, with o0 / o1 the other two
+    branch outputs (compute dtype, out's shape and strides: pass `out` too), gates fp32
+    contiguous [3, Z, H, Tq] and mix_out any [Z, H, Tq, dv] view with unit-stride rows."""
     _check_device(q, k, v, block_ends, indices, out, L, M)
     Z, H, Tq, dk = q.shape
     G, Tkv = k.shape[1], k.shape[2]
@@ -108,11 +111,21 @@ def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=
     if q_offset < 0:
         raise ValueError("q_offset must be >= 0")
     # the reference-interface entry points, or their decode extensions
-    dec = q_offset != 0 or (branch == SLIDING and Tq != Tkv)
+    dec = q_offset != 0 or (branch == SLIDING and (Tq != Tkv or mix is not None))
     sfx, tail = ("_ex", (int(q_offset), _ptr(ws), ws.numel(), st)) if dec else ("", (_ptr(ws), ws.numel(), st))
+    if mix is not None and (branch != SLIDING or not direct_out or any(
+            t.dtype != cdt or t.stride() != o.stride() for t in mix[:2])):
+        raise ValueError("mix needs the sliding branch, `out` in the compute dtype and o0 / o1 with out's strides")
     if branch == SLIDING:
         if dec:
-            tail = (Tkv, *tail)
+            if mix is not None:
+                o0, o1, gates, xo = mix
+                if gates.dtype != torch.float32 or not gates.is_contiguous() or tuple(gates.shape) != (3, Z, H, Tq):
+                    raise ValueError(f"mix gates must be contiguous fp32 [3, {Z}, {H}, {Tq}]")
+                mixargs = (_ptr(o0), _ptr(o1), _ptr(gates), _ptr(xo), *xo.stride()[:3])
+            else:
+                mixargs = (_ptr(None), _ptr(None), _ptr(None), _ptr(None), 0, 0, 0)
+            tail = (Tkv, int(q_offset), *mixargs, *tail[1:])
         _lib.call("nsa_sliding_window_fwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(o), float(scale), _ptr(Lk),
                   _ptr(Mk), *common_strides, *lm_strides, Z, H, G, Tq, int(window), DK, DV, dt, *tail)
     elif branch == COMPRESSION:
@@ -136,11 +149,13 @@ def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=
 
 def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0, block_ends=None, indices=None,
              lprime: int = 64, causal: bool = True, fallback: bool = False, dq=None, dk=None, dv=None,
-             dq_accumulate: bool = False, delta=None):
+             dq_accumulate: bool = False, delta=None, row_gate=None, row_dot=None):
     """Backward of one NSA branch.  dq is overwritten (added to when dq_accumulate, which
     needs dq), dk / dv ([Z,G,Tkv,*] logical views) are accumulated into (allocated
     zeroed when not given).  delta: optional precomputed row sums sum_d o * do [Z,H,Tq]
-    (fp32), used instead of reading o.  Returns (dq, dk, dv)."""
+    (fp32), used instead of reading o.  row_gate: optional fp32 contiguous [Z,H,Tq]; the
+    branch's output gradient is then row_gate * do.  row_dot: optional fp32 contiguous
+    [Z,H,Tq] that receives sum_d do * o per row.  Returns (dq, dk, dv)."""
     if dq_accumulate and dq is None:
         raise ValueError("dq_accumulate needs the dq tensor to add to")
     _check_device(q, k, v, o, do, L, M, block_ends, indices, dq, dk, dv)
@@ -153,9 +168,12 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     qk = _rows(_pad_last(q.to(cdt), DK))
     kk = _pad_last(k.to(cdt), DK)
     vk = _pad_last(v.to(cdt), DV)
-    # O and dO are read with one set of strides (as the reference kernels do)
-    ok = _pad_last(o.to(cdt), DV).contiguous()
-    dok = _pad_last(do.to(cdt), DV).contiguous()
+    # O and dO are read with one set of strides (as the reference kernels do): kept as
+    # they are when they already share unit-stride, aligned rows
+    ok = _pad_last(o.to(cdt), DV)
+    dok = _pad_last(do.to(cdt), DV)
+    if ok.stride() != dok.stride() or not (_rows_ok(ok) and _rows_ok(dok)):
+        ok, dok = ok.contiguous(), dok.contiguous()
     Lf = L.to(torch.float32)
     Mf = M.to(torch.float32)
     direct_dq = dq is not None and dq.dtype == cdt and dkw == DK and _rows_ok(dq)
@@ -178,8 +196,11 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     dl = None if delta is None else delta.to(torch.float32).contiguous()
     if dl is not None and tuple(dl.shape) != (Z, H, Tq):
         raise ValueError(f"delta must be [{Z}, {H}, {Tq}], got {tuple(dl.shape)}")
-    if acc or dl is not None:
-        sfx, tail = "_ex", (int(acc), _ptr(dl), _ptr(ws), ws.numel(), st)
+    for t in (row_gate, row_dot):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != (Z, H, Tq)):
+            raise ValueError(f"row_gate / row_dot must be contiguous fp32 [{Z}, {H}, {Tq}]")
+    if acc or dl is not None or row_gate is not None or row_dot is not None:
+        sfx, tail = "_ex", (int(acc), _ptr(dl), _ptr(row_gate), _ptr(row_dot), _ptr(ws), ws.numel(), st)
     else:
         sfx, tail = "", (_ptr(ws), ws.numel(), st)
     if branch == SLIDING:

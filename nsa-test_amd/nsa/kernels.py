@@ -268,47 +268,107 @@ class NSACore(torch.autograd.Function):
     """The attention core of NSAAttention over one query tensor: the three branches
     (CompressionAttention, SelectionAttention and SlidingWindowAttention, with their
     arguments and layouts), the gate activation of config.gate_mode (sigmoid, or softmax
-    over the three gates) applied to gate_logits [B,H,T,3], and the gated mix (GatedMix),
-    as one function returning the mixed output.  The activation runs inside the mix
-    kernels (the backward returns the gradient of the logits).  The backward runs the mix backward, which gives each branch's output
-    gradient g_k dO and dg_k = sum_d dO o_k; the branch backwards then take
-    D_k = g_k dg_k (= sum_d o_k (g_k dO)) as their row sums instead of reading o_k again,
-    and the second and third add their dQ into the first's (the dQ kernels' accumulate
-    mode) instead of autograd summing three dQ tensors."""
+    over the three gates) applied to gate_logits [B,H,T,3], and the gated mix (GatedMix,
+    reference nsa/kernels.py:2429-2463), as one function returning the mixed output.
+
+    The mix is fused into the branch kernels: the sliding-window forward runs last and
+    its epilogue writes g0 o_cmp + g1 o_sel + g2 o_win; the branch backwards take the mix's
+    output gradient dout unscaled with their gate as a per-row factor (the branch's
+    output gradient is g_k dout: dQ is scaled by g_k, the dK / dV probabilities by the
+    row's g_k) and write sum_d dout . o_k per row, from which the gate-logit gradient
+    follows.  No per-branch output gradient is materialised, and the second and third
+    dQ are added into the first's (the dQ kernels' accumulate mode).  Head widths
+    without a compiled kernel, or fused_mix = False, take the separate GatedMix passes."""
+
+    fused_mix = True
 
     @staticmethod
     def forward(ctx, q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win, gate_logits,
                 scale, config):
         _ops._check_device(q, gate_logits)
         lp = config.l_prime
+        act = GATE_ACT[config.gate_mode]
+        cdt = _ops.compute_dtype(q.dtype)
+        B, H, T, dk = q.shape
+        dv = v_compressed.shape[-1]
+        fused = NSACore.fused_mix and _ops.kernel_dims(dk, dv) == (dk, dv)
+        ctx.scale, ctx.lprime, ctx.window, ctx.gdtype, ctx.act, ctx.fused = (scale, lp, config.w, gate_logits.dtype,
+                                                                             act, fused)
+        if fused:
+            # branch outputs and the mix in [B,T,H,dv] storage (the module's layout)
+            def bthd():
+                return torch.empty(B, T, H, dv, device=q.device, dtype=cdt).permute(0, 2, 1, 3)
+
+            o_c, o_s, o_w, out = bthd(), bthd(), bthd(), bthd()
+            gates = _gate_activation(gate_logits.float(), act).permute(3, 0, 1, 2).contiguous()  # [3,B,H,T]
+            _, Lc, Mc = _ops.attn_fwd(COMPRESSION, q, _kt(k_compressed), v_compressed, scale, block_ends=block_ends,
+                                      out=o_c)
+            _, Ls, Ms = _ops.attn_fwd(SELECTION, q, _kt(k_sel), v_sel, scale, indices=indices, lprime=lp,
+                                      fallback=True, out=o_s)
+            _, Lw, Mw = _ops.attn_fwd(SLIDING, q, _kt(k_win), v_win, scale, window=config.w, out=o_w,
+                                      mix=(o_c, o_s, gates, out))
+            ctx.save_for_backward(q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win,
+                                  gates, o_c, o_s, o_w, Lc, Mc, Ls, Ms, Lw, Mw)
+            return out.to(q.dtype)
         o_c, Lc, Mc = _ops.attn_fwd(COMPRESSION, q, _kt(k_compressed), v_compressed, scale, block_ends=block_ends)
         o_s, Ls, Ms = _ops.attn_fwd(SELECTION, q, _kt(k_sel), v_sel, scale, indices=indices, lprime=lp,
                                     fallback=True)
         o_w, Lw, Mw = _ops.attn_fwd(SLIDING, q, _kt(k_win), v_win, scale, window=config.w)
-        cdt = _ops.compute_dtype(q.dtype)
         os_ = [t.to(cdt).contiguous() for t in (o_c, o_s, o_w)]
         g = gate_logits.to(cdt)
-        act = GATE_ACT[config.gate_mode]
         out = _mix_fwd(os_, g, act)
         ctx.save_for_backward(q, k_compressed, v_compressed, block_ends, k_sel, v_sel, indices, k_win, v_win, g,
                               *os_, Lc, Mc, Ls, Ms, Lw, Mw)
-        ctx.scale, ctx.lprime, ctx.window, ctx.gdtype, ctx.act = scale, lp, config.w, gate_logits.dtype, act
         return out.to(q.dtype)
 
     @staticmethod
     def backward(ctx, dout):
         (q, kc, vc, be, ks, vs, idx, kw, vw, g, o_c, o_s, o_w, Lc, Mc, Ls, Ms, Lw, Mw) = ctx.saved_tensors
         sc = ctx.scale
-        dos, dg, deltas = _mix_bwd(dout, [o_c, o_s, o_w], g, want_delta=True, act=ctx.act)
         dq = torch.empty(q.shape, device=q.device, dtype=_ops.compute_dtype(q.dtype))
-        _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, dos[0], Lc, Mc, sc, block_ends=be, dq=dq,
-                                    delta=deltas[0])
-        _, dks, dvs = _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, dos[1], Ls, Ms, sc, indices=idx,
-                                    lprime=ctx.lprime, fallback=True, dq=dq, dq_accumulate=True, delta=deltas[1])
-        _, dkw, dvw = _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, dos[2], Lw, Mw, sc, window=ctx.window, dq=dq,
-                                    dq_accumulate=True, delta=deltas[2])
+        if ctx.fused:
+            d = dout.to(o_c.dtype)
+            if d.stride() != o_c.stride():  # one copy into the branch outputs' layout
+                d = torch.empty_like(o_c).copy_(d)
+            rdot = torch.empty(g.shape, device=q.device, dtype=torch.float32)  # [3,B,H,T]
+            _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, d, Lc, Mc, sc, block_ends=be, dq=dq,
+                                        row_gate=g[0], row_dot=rdot[0])
+            _, dks, dvs = _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, d, Ls, Ms, sc, indices=idx,
+                                        lprime=ctx.lprime, fallback=True, dq=dq, dq_accumulate=True, row_gate=g[1],
+                                        row_dot=rdot[1])
+            _, dkw, dvw = _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, d, Lw, Mw, sc, window=ctx.window, dq=dq,
+                                        dq_accumulate=True, row_gate=g[2], row_dot=rdot[2])
+            dg = _gate_activation_grad(g, rdot, ctx.act).permute(1, 2, 3, 0)
+        else:
+            dos, dg, deltas = _mix_bwd(dout, [o_c, o_s, o_w], g, want_delta=True, act=ctx.act)
+            _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, dos[0], Lc, Mc, sc, block_ends=be, dq=dq,
+                                        delta=deltas[0])
+            _, dks, dvs = _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, dos[1], Ls, Ms, sc, indices=idx,
+                                        lprime=ctx.lprime, fallback=True, dq=dq, dq_accumulate=True, delta=deltas[1])
+            _, dkw, dvw = _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, dos[2], Lw, Mw, sc, window=ctx.window, dq=dq,
+                                        dq_accumulate=True, delta=deltas[2])
         return (dq.to(q.dtype), dkc.transpose(-1, -2), dvc, None, dks.transpose(-1, -2), dvs, None,
                 dkw.transpose(-1, -2), dvw, dg.to(ctx.gdtype), None, None)
+
+
+def _gate_activation(z, act):
+    """Gates from the gate input z [..., 3] (fp32): z itself, sigmoid(z) or softmax over
+    the three (reference nsa/kernels.py:2436-2440)."""
+    if act == 1:
+        return torch.sigmoid(z)
+    if act == 2:
+        return torch.softmax(z, dim=-1)
+    return z
+
+
+def _gate_activation_grad(a, r, act):
+    """Gradient of the gate input from the gates a and r_k = sum_d dout . o_k (both
+    [3, ...] fp32): r (identity), r a (1 - a) (sigmoid), a (r - sum_j a_j r_j) (softmax)."""
+    if act == 1:
+        return r * a * (1 - a)
+    if act == 2:
+        return a * (r - (a * r).sum(0, keepdim=True))
+    return r
 
 
 class _LinearSplitK(torch.autograd.Function):
