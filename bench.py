@@ -11,8 +11,9 @@ weights) are synthetic and resident in HBM before the timed region.
 
 The JSON line also carries the long-context configuration (T=32768, configs[3]) as
 `secondary`, a per-kernel breakdown, the roofline of the dominant kernel (timed with
-HIP events inside the timed region) and a CPU baseline (the C oracle, one core, on a
-sample of query rows, extrapolated linearly: each row's work is independent).
+HIP events inside the timed region) and a CPU baseline (the C oracle on all host cores,
+one thread each, on a sample of query rows, extrapolated linearly: each row's work is
+independent).
 """
 import argparse
 import json
@@ -167,11 +168,23 @@ def kernel_breakdown(cfg, mod, w):
     return res
 
 
-def cpu_baseline(name, samples, seed=0):
-    """The C oracle (one core) on `samples` query timesteps of one KV group plus
-    compress_tokens of that group; extrapolated to the whole workload."""
+def cpu_threads():
+    """Host cores this process may use (its affinity set), at most 16 (the GPU box's share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def cpu_baseline(name, rows_per_thread, seed=0):
+    """The C oracle on all host cores: compress_tokens of one KV group, then the scoring
+    and the three branches fwd+bwd for a sample of that group's query timesteps, split
+    over one thread per core (every row's work is independent; the oracle's C calls
+    release the GIL).  Extrapolated linearly to every row and group of the workload."""
+    import concurrent.futures as cf
+
     import numpy as np
-    import torch
 
     import oracle
     from nsa import NSAConfig
@@ -179,6 +192,8 @@ def cpu_baseline(name, samples, seed=0):
     c = CONFIGS[name]
     B, H, G, T, dk, dv = c["B"], c["H"], c["G"], c["T"], c["dk"], c["dv"]
     hpg = H // G
+    nthreads = cpu_threads()
+    samples = min(T, rows_per_thread * nthreads)
     rng = np.random.default_rng(seed)
     cfg = NSAConfig(head_dim_qk=dk, head_dim_v=dv, n_heads=hpg, n_kv_groups=1, n=c["n"], w=c["w"])
     scale = 1 / math.sqrt(dk)
@@ -193,23 +208,35 @@ def cpu_baseline(name, samples, seed=0):
     t0 = time.perf_counter()
     kc, vc, be, _ = oracle.compress_tokens(k[0], v[0], w1, np.zeros(2 * dk), w2, np.zeros(dk), pe, cfg.l, cfg.d)
     t_group = time.perf_counter() - t0
+    kct = np.ascontiguousarray(kc.transpose(0, 1, 3, 2))
+    kc32 = kc.astype(np.float32)
+    # float64 once, so the per-thread oracle calls convert nothing
+    k = [np.ascontiguousarray(x, dtype=np.float64) for x in k]
+    v = [np.ascontiguousarray(x, dtype=np.float64) for x in v]
+    vc = np.ascontiguousarray(vc, dtype=np.float64)
+
+    def run(sl):
+        r, qs, ds = rows[sl], q[:, :, sl], do[:, :, sl]
+        idx = oracle.score_topn(qs, kc32, be, np.float32(scale), l=cfg.l, d=cfg.d, lprime=cfg.l_prime, n=cfg.n,
+                                positions=r)
+        oracle.attn_fwd(oracle.COMPRESSION, qs, kct, vc, scale, block_ends=be, positions=r)
+        oracle.attn_bwd(oracle.COMPRESSION, qs, kct, vc, ds, scale, block_ends=be, positions=r)
+        oracle.attn_fwd(oracle.SELECTION, qs, k[1], v[1], scale, indices=idx, lprime=cfg.l_prime, positions=r)
+        oracle.attn_bwd(oracle.SELECTION, qs, k[1], v[1], ds, scale, indices=idx, lprime=cfg.l_prime, positions=r)
+        oracle.attn_fwd(oracle.SLIDING, qs, k[2], v[2], scale, window=cfg.w, positions=r)
+        oracle.attn_bwd(oracle.SLIDING, qs, k[2], v[2], ds, scale, window=cfg.w, positions=r)
+
+    bounds = np.linspace(0, samples, nthreads + 1).astype(int)
     t0 = time.perf_counter()
-    idx = oracle.score_topn(q, kc.astype(np.float32), be, np.float32(scale), l=cfg.l, d=cfg.d, lprime=cfg.l_prime,
-                            n=cfg.n, positions=rows)
-    kct = kc.transpose(0, 1, 3, 2)
-    oracle.attn_fwd(oracle.COMPRESSION, q, kct, vc, scale, block_ends=be, positions=rows)
-    oracle.attn_bwd(oracle.COMPRESSION, q, kct, vc, do, scale, block_ends=be, positions=rows)
-    oracle.attn_fwd(oracle.SELECTION, q, k[1], v[1], scale, indices=idx, lprime=cfg.l_prime, positions=rows)
-    oracle.attn_bwd(oracle.SELECTION, q, k[1], v[1], do, scale, indices=idx, lprime=cfg.l_prime, positions=rows)
-    oracle.attn_fwd(oracle.SLIDING, q, k[2], v[2], scale, window=cfg.w, positions=rows)
-    oracle.attn_bwd(oracle.SLIDING, q, k[2], v[2], do, scale, window=cfg.w, positions=rows)
+    with cf.ThreadPoolExecutor(nthreads) as ex:
+        list(ex.map(run, [slice(bounds[i], bounds[i + 1]) for i in range(nthreads)]))
     t_rows = time.perf_counter() - t0
     total = B * G * (t_group + t_rows * T / samples)
-    del torch
-    return {"value": round(B * T / total, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"C oracle (float64 branches, fp32 scoring), 1 thread: {samples} of {T} query timesteps x "
-                      f"{hpg} heads of 1 of {G} KV groups fwd+bwd ({t_rows:.1f}s) + compress_tokens of that group "
-                      f"({t_group:.1f}s), extrapolated x{T / samples:.0f} rows x{G} groups"}
+    return {"value": round(B * T / total, 2), "unit": "tokens/s", "cores": nthreads, "kind": "port",
+            "sample": f"C oracle (float64 branches, fp32 scoring), {nthreads} threads: {samples} of {T} query "
+                      f"timesteps x {hpg} heads of 1 of {G} KV groups fwd+bwd ({t_rows:.1f}s wall) + "
+                      f"compress_tokens of that group ({t_group:.1f}s), extrapolated x{T / samples:.1f} rows "
+                      f"x{G} groups"}
 
 
 def measured_traffic(config, kernel):
@@ -231,7 +258,7 @@ def main():
     ap.add_argument("--config", default="paper", choices=sorted(CONFIGS))
     ap.add_argument("--no-secondary", action="store_true", help="skip the T=32K configuration")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-samples", type=int, default=1024)
+    ap.add_argument("--cpu-rows-per-thread", type=int, default=256)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build targets single-GPU "
@@ -318,7 +345,7 @@ def main():
         del mod2, w2
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_samples)
+        result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_rows_per_thread)
     print(json.dumps(result), flush=True)
 
 

@@ -52,6 +52,29 @@ def module_case(name, seed, B, T, **cfg_kw):
     print("wrote", name, {k: v.shape for k, v in arrs.items() if not k.startswith(("param/", "cfg/"))})
 
 
+def heads_case(name, seed, B, T, **cfg_kw):
+    """Selection at the paper's head shapes (dk = 192, 16 query heads per group): only
+    what the Eq. 8 -> top-n pipeline reads and writes is kept (q, K_cmp, block_ends,
+    selection scores and indices), not the module's parameters."""
+    torch.manual_seed(seed)
+    cfg = NSAConfig(**cfg_kw)
+    m = NSAAttention(cfg).eval()
+    x = torch.randn(B, T, cfg.d_model)
+    with torch.no_grad():
+        _, info = m(x, output_attentions=True)
+        q = m.q_proj(x).view(B, T, cfg.n_heads, cfg.head_dim_qk).transpose(1, 2)
+        kcomp = m.k_compress(x).view(B, T, cfg.n_kv_groups, cfg.head_dim_qk).transpose(1, 2)
+        vcomp = m.v_compress(x).view(B, T, cfg.n_kv_groups, cfg.head_dim_v).transpose(1, 2)
+        kc, _, be, _ = m.compress_tokens(kcomp, vcomp)
+    arrs = {"q": q.contiguous().numpy(), "k_cmp": kc.numpy(), "block_ends": be.numpy(),
+            "selection_scores": info["selection_scores"].numpy(), "selected_indices": info["selected_indices"].numpy()}
+    for k in ("d_model", "head_dim_qk", "head_dim_v", "l", "d", "l_prime", "n", "include_fixed_in_selection",
+              "n_fixed", "w", "n_heads", "n_kv_groups"):
+        arrs[f"cfg/{k}"] = np.asarray(getattr(cfg, k))
+    np.savez_compressed(OUT / f"{name}.npz", **arrs)
+    print("wrote", name, {k: v.shape for k, v in arrs.items() if not k.startswith("cfg/")})
+
+
 def topn_case(name, seed, B, H, G, T, nblk, n, l_prime, include_fixed, n_fixed, kind):
     g = torch.Generator().manual_seed(seed)
     if kind == "ties":
@@ -93,6 +116,9 @@ if __name__ == "__main__":
     # T shorter than one compression block: fallback paths
     module_case("module_short", 2, B=1, T=24, d_model=64, head_dim_qk=32, head_dim_v=32, n_heads=4, n_kv_groups=1,
                 l=32, d=16, l_prime=64, n=4, w=16)
+    # the paper's head shapes: dk = 192, dv = 128, 16 query heads per KV group
+    heads_case("heads_paper", 7, B=1, T=512, d_model=64, head_dim_qk=192, head_dim_v=128, n_heads=16,
+               n_kv_groups=1, l=32, d=16, l_prime=64, n=5, w=128)
     topn_case("topn_ties_fixed", 3, B=2, H=8, G=2, T=256, nblk=8, n=5, l_prime=32, include_fixed=True, n_fixed=3,
               kind="ties")
     topn_case("topn_ties_nofixed", 4, B=1, H=4, G=4, T=64, nblk=16, n=6, l_prime=16, include_fixed=False, n_fixed=0,

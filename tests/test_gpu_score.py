@@ -74,7 +74,7 @@ def test_score_topn_bit_exact(dev, B, H, G, T, dk, l, d, lp, n, fixed, dtype):
     np.testing.assert_array_equal(ps, rps)
 
 
-@pytest.mark.parametrize("name", ["module_cfg1", "module_odd_softmax", "module_short"])
+@pytest.mark.parametrize("name", ["module_cfg1", "module_odd_softmax", "module_short", "heads_paper"])
 def test_score_topn_golden(dev, name):
     """Indices of the reference module (eval mode) from its own q and K_cmp."""
     f = load_fixture(name)

@@ -236,6 +236,20 @@ def test_score_pipeline_golden(name):
     np.testing.assert_array_equal(idx, f["selected_indices"])
 
 
+def test_score_pipeline_golden_paper_heads():
+    """The reference module's selection at the paper's head shapes (dk = 192, 16 query
+    heads per group, fp32): the oracle's fixed-order fp32 pipeline gives the same indices,
+    and Eq. 9 scores within a few ulp of torch's matmul / softmax order."""
+    f = load_fixture("heads_paper")
+    cfg = _Cfg(f)
+    idx, _, ps = oracle.score_topn(f["q"], f["k_cmp"], f["block_ends"], np.float32(1 / math.sqrt(cfg.head_dim_qk)),
+                                   l=cfg.l, d=cfg.d, lprime=cfg.l_prime, n=cfg.n,
+                                   include_fixed=cfg.include_fixed_in_selection, n_fixed=cfg.n_fixed,
+                                   want_scores=True)
+    np.testing.assert_allclose(ps, f["selection_scores"], rtol=4e-6, atol=0)
+    np.testing.assert_array_equal(idx, f["selected_indices"])
+
+
 @pytest.mark.parametrize("name", MODULE_CASES)
 def test_compress_tokens_golden(name):
     f = load_fixture(name)
