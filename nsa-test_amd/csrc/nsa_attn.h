@@ -10,7 +10,7 @@ enum DType : int { kF32 = 0, kBF16 = 1 };
 
 // Columns handled by one forward / dQ workgroup (4 waves x NSUB x 16).
 constexpr int kFwdNSub = 1;
-constexpr int kFwdWaves = 16;
+constexpr int kFwdWaves = 8;
 constexpr int kFwdCols = kFwdWaves * kFwdNSub * 16;
 constexpr int kDqWaves = 12;
 constexpr int kDqCols = kDqWaves * 16;

@@ -41,9 +41,10 @@ struct FwdTile {
   static constexpr int NKF = 4 * (DK / KC);          // K fragments (ks, kc)
   static constexpr int NVF = (64 / CK) * (DV / 16);  // V^T fragments (kc2, j)
   static constexpr int BYTES = (NKF + NVF) * 1024;
-  // a double buffer (one WG of 16 waves per CU, four waves per SIMD); one stage when
-  // two do not fit
-  static constexpr int NBUF = 2 * BYTES <= 96 * 1024 ? 2 : 1;
+  // two 8-wave workgroups per CU (four waves per SIMD), so one workgroup's prologue and
+  // epilogue overlap the other's tile loop: a double buffer when two workgroups' stages
+  // fit the 160 KB of LDS, else one stage (the other workgroup covers the refill)
+  static constexpr int NBUF = 2 * BYTES <= 76 * 1024 ? 2 : 1;
 };
 
 template <typename T, int DK, int DV, int BR>

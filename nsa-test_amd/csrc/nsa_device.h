@@ -175,16 +175,6 @@ __device__ __forceinline__ uint4 frag_std(const typename Store<T>::type* row, in
   return *reinterpret_cast<const uint4*>(row + g * Elem<T>::kPerFrag);
 }
 
-__device__ __forceinline__ float wave_max16(float v) {  // over lanes sharing (l & 15)
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
-}
-__device__ __forceinline__ float wave_sum16(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
-}
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
@@ -324,6 +314,19 @@ template <int OFF>
 __device__ __forceinline__ int lane_xor(int x) {
   return (int)lane_xor_u32<OFF>((uint32_t)x);
 }
+// max / sum over the four lanes sharing (l & 15), lane swaps instead of LDS-crossbar
+// shuffles (same pairing order as __shfl_xor with 16, then 32)
+__device__ __forceinline__ float wave_max16(float v) {
+  v = fmaxf(v, lane_xor<16>(v));
+  v = fmaxf(v, lane_xor<32>(v));
+  return v;
+}
+__device__ __forceinline__ float wave_sum16(float v) {
+  v += lane_xor<16>(v);
+  v += lane_xor<32>(v);
+  return v;
+}
+
 // xor butterfly over 32, 16, 8, 4, 2, 1: every lane ends with op folded over the wave,
 // pairs combined in exactly the order of the __shfl_xor loop over the same offsets
 template <typename T, typename F>

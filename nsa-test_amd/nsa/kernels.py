@@ -693,17 +693,20 @@ class NSAAttention(torch.nn.Module):
 
     def _add_blocks(self, cache: NSAKVCache) -> None:
         """Compress every block the cache's tokens complete (block i covers tokens
-        i*d .. i*d+l-1), with compress_tokens on the block's own l tokens."""
+        i*d .. i*d+l-1): one compress_tokens call over the tokens of all new blocks."""
         c = self.config
-        while cache.n_act * c.d + c.l <= cache.length:
-            i = cache.n_act
-            lo = i * c.d
-            kc, vc, _, n1 = self.compress_tokens(cache.k_cmp_in[:, :, lo:lo + c.l], cache.v_cmp_in[:, :, lo:lo + c.l])
-            assert n1 == 1
-            cache.K_cmp[..., i] = kc[..., 0]
-            cache.V_cmp[:, :, i] = vc[:, :, 0]
-            cache.block_ends[i] = lo + c.l - 1
-            cache.n_act += 1
+        n_new = (cache.length - c.l) // c.d + 1 if cache.length >= c.l else 0
+        i0 = cache.n_act
+        if n_new <= i0:
+            return
+        lo, hi = i0 * c.d, (n_new - 1) * c.d + c.l
+        kc, vc, _, n1 = self.compress_tokens(cache.k_cmp_in[:, :, lo:hi], cache.v_cmp_in[:, :, lo:hi])
+        assert n1 == n_new - i0
+        cache.K_cmp[..., i0:n_new] = kc[..., :n1]
+        cache.V_cmp[:, :, i0:n_new] = vc[:, :, :n1]
+        cache.block_ends[i0:n_new] = torch.arange(i0, n_new, device=cache.block_ends.device,
+                                                  dtype=torch.int32) * c.d + (c.l - 1)
+        cache.n_act = n_new
 
     @torch.no_grad()
     def prefill(self, hidden_states: torch.Tensor, cache: NSAKVCache) -> None:
@@ -751,7 +754,7 @@ class NSAAttention(torch.nn.Module):
         cdt = _ops.compute_dtype(q.dtype)
         os_ = [o.to(cdt).contiguous() for o in (o_c, o_s, o_w)]
         o = _mix_fwd(os_, gate_logits.to(cdt), GATE_ACT[c.gate_mode]).to(q.dtype)
-        out = self.o_proj(o.transpose(1, 2).reshape(B, 1, H * dv))
+        out = self.dropout(self.o_proj(o.transpose(1, 2).reshape(B, 1, H * dv)))  # as forward does
         info = None
         if output_attentions:
             gates = torch.softmax(gate_logits, dim=-1) if c.gate_mode == "softmax" else torch.sigmoid(gate_logits)
