@@ -101,10 +101,12 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) S QTs[NB][kTr ? 8 : DK * RP];
   __shared__ __attribute__((aligned(16))) S Os[NB][RC * OP];
   __shared__ __attribute__((aligned(16))) S OTs[NB][kTr ? 8 : DV * RP];
-  __shared__ int s_t[NB][RC];
-  __shared__ float s_l2[NB][RC];
-  __shared__ float s_dl[NB][RC];
-  __shared__ float s_g[NB][RC];  // the rows' gates (1 without a row gate)
+  // per staged row: timestep (-1 past the item's end), lse2, delta, gate (1 without a row
+  // gate); 16-byte aligned so a lane reads its four consecutive rows at once
+  __shared__ __attribute__((aligned(16))) int s_t[NB][RC];
+  __shared__ __attribute__((aligned(16))) float s_l2[NB][RC];
+  __shared__ __attribute__((aligned(16))) float s_dl[NB][RC];
+  __shared__ __attribute__((aligned(16))) float s_g[NB][RC];
   __shared__ int s_be[KEYS];
   __shared__ int s_tl[kSegTMax];  // selection: the item's query timesteps
 
@@ -373,23 +375,29 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
         for (int kc = 0; kc < NKC; ++kc) sacc = Mma<T>::run(sacc, frag_std<T>(qrow + kc * KC, g4), kf[kc]);
 #pragma unroll
         for (int kc = 0; kc < NVC; ++kc) pacc = Mma<T>::run(pacc, frag_std<T>(orow + kc * KC, g4), vf[kc]);
+        // the lane's four rows rs*16 + 4*g4 + i: their statistics as one 16-byte read each,
+        // the mask applied to the exponent argument (no divergent branch)
+        const int r4 = rs * 16 + 4 * g4;
+        const float4 l2v = *reinterpret_cast<const float4*>(&s_l2[buf][r4]);
+        const float4 dlv = *reinterpret_cast<const float4*>(&s_dl[buf][r4]);
+        const float4 gv = *reinterpret_cast<const float4*>(&s_g[buf][r4]);
+        const int4 tv = *reinterpret_cast<const int4*>(&s_t[buf][r4]);
+        const float l2a[4] = {l2v.x, l2v.y, l2v.z, l2v.w}, dla[4] = {dlv.x, dlv.y, dlv.z, dlv.w};
+        const float ga[4] = {gv.x, gv.y, gv.z, gv.w};
+        const int ta[4] = {tv.x, tv.y, tv.z, tv.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int r = rs * 16 + 4 * g4 + i;
-          float p;
-          if (all_visible) {
-            p = fast_exp2(sacc[i] * scale2 - s_l2[buf][r]);
-          } else {
-            const int t = s_t[buf][r];
-            bool ok;
+          bool ok = true;
+          if (!all_visible) {
+            const int t = ta[i];
             if (BR == kSliding) ok = t >= 0 && mykey <= t && mykey > t - a.window && mykey < a.Tkv;
             else if (BR == kCompression) ok = t >= 0 && mybe <= t;
             else ok = t >= 0 && (!a.causal || mykey <= t) && mykey < blk_hi;
-            p = ok ? fast_exp2(sacc[i] * scale2 - s_l2[buf][r]) : 0.f;
           }
-          p *= s_g[buf][r];  // gated: the rows' output gradient is g dO
+          // lse2 is +inf for rows that saw no key: p = 0 there
+          const float p = fast_exp2(ok ? sacc[i] * scale2 - l2a[i] : -INFINITY) * ga[i];  // gated: g dO
           pt[rs][i] = p;
-          dst[rs][i] = p * (pacc[i] - s_dl[buf][r]);
+          dst[rs][i] = p * (pacc[i] - dla[i]);
         }
       }
 #pragma unroll
