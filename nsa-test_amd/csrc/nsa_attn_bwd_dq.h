@@ -168,9 +168,7 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
 
     int be_max = 0;
     if (BR == kCompression) {
-      be_max = sbe[lane];
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) be_max = max(be_max, __shfl_xor(be_max, o));
+      be_max = wave_butterfly(sbe[lane], [](int x, int y) { return max(x, y); });
     }
 
     // Every (subtile, tile) pair runs the products, fully masked when no key is
@@ -196,16 +194,14 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float p;
-        if (all_visible) {
-          p = fast_exp2(st[ks][i] * scale2 - l2);
-        } else {
+        bool ok = true;
+        if (!all_visible) {
           const int key = key0 + ks * 16 + 4 * g4 + i;
-          bool ok;
           if (BR == kSliding) ok = (uint32_t)(key - kmin_s) < kspan_s;
           else ok = colv & (sbe[ks * 16 + 4 * g4 + i] <= colt);
-          p = ok ? fast_exp2(st[ks][i] * scale2 - l2) : 0.f;
         }
+        // the mask on the exponent argument: no divergent branch around the exp
+        const float p = fast_exp2(ok ? st[ks][i] * scale2 - l2 : -INFINITY);
         st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
       }
     }

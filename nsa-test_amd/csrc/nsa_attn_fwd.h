@@ -180,9 +180,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
     const uint4* vb = fwd_lds + buf * (FT::NKF + FT::NVF) * 64 + FT::NKF * 64;
     int be_max = 0;
     if (BR == kCompression) {
-      be_max = sbe[lane];
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) be_max = max(be_max, __shfl_xor(be_max, o));
+      be_max = wave_butterfly(sbe[lane], [](int x, int y) { return max(x, y); });
     }
     uint4 pf[NSUB][64 / CK];
 #pragma unroll

@@ -465,7 +465,7 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const bool ok = (uint32_t)(kb + ks * 16 + i) < span;
-        const float p = ok ? fast_exp2(st[ks][i] * scale2 - l2) : 0.f;
+        const float p = fast_exp2(ok ? st[ks][i] * scale2 - l2 : -INFINITY);
         st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
       }
 #pragma unroll
