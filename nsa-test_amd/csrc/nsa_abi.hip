@@ -55,10 +55,19 @@ struct Shape {
     if (br == kSelection) return nsubblk() * (nblk() + (int)(((int64_t)Tq * nslots + sg - 1) / sg));
     return ((Tkv + dkdv_keys(br) - 1) / dkdv_keys(br)) * dkdv_nseg(br, Tq, window, sg);
   }
-  // segment length: 128 entries when 256-entry segments leave fewer than 4096 work
-  // items in all (shorter segments then raise the parallelism by more than their extra
-  // partials cost), else 256
-  int seg() const { return (int64_t)Z * G * items_for(kSegTMax) < 4096 ? kSegTMax / 2 : kSegTMax; }
+  // sliding window with at least one 128-key tile per CU: a work item owns a key tile
+  // with all its query rows and accumulates into dK / dV itself (no partials, no
+  // reduce pass)
+  bool direct() const {
+    return br == kSliding && (int64_t)Z * G * ((Tkv + dkdv_keys(br) - 1) / dkdv_keys(br)) >= kDkdvDirectItems;
+  }
+  // segment length: the whole query span in direct mode; else 128 entries when
+  // 256-entry segments leave fewer than 4096 work items in all (shorter segments then
+  // raise the parallelism by more than their extra partials cost), else 256
+  int seg() const {
+    if (direct()) return min(window + dkdv_keys(br) - 1, Tq + dkdv_keys(br) - 1);
+    return (int64_t)Z * G * items_for(kSegTMax) < 4096 ? kSegTMax / 2 : kSegTMax;
+  }
   int items_per_bg() const { return items_for(seg()); }
 };
 
@@ -100,7 +109,7 @@ Layout make_layout(const Shape& s, bool bwd) {
       L.csr_t = take(BG * s.Tq * s.nslots * 4);
     }
   }
-  if (bwd) L.partial = take(BG * s.items_per_bg() * dkdv_keys(s.br) * (size_t)(s.dk + s.dv) * 4);
+  if (bwd && !s.direct()) L.partial = take(BG * s.items_per_bg() * dkdv_keys(s.br) * (size_t)(s.dk + s.dv) * 4);
   L.total = off;
   return L;
 }
@@ -312,6 +321,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.delta = at<float>(ws, L.delta);
   a.items_per_bg = s.items_per_bg();
   a.seg = s.seg();
+  a.direct = s.direct() ? 1 : 0;
   a.partial = at<float>(ws, L.partial);
 
   launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp,
@@ -342,7 +352,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   if ((rc = check_hip("dK/dV kernel"))) return rc;
   {
     TimingScope ts(kIdReduce, st);
-    launch_partial_reduce(s.dtype, s.dk, s.dv, s.br, a, st);
+    if (!a.direct) launch_partial_reduce(s.dtype, s.dk, s.dv, s.br, a, st);
   }
   if ((rc = check_hip("dK/dV reduce"))) return rc;
   return NSA_OK;

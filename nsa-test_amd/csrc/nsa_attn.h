@@ -21,6 +21,9 @@ constexpr int kRowChunk = 32;
 // Query entries (timesteps; selection: CSR entries) per dK/dV work item: 128 or 256,
 // chosen per launch (dkdv_seg_len), at most kSegTMax.
 constexpr int kSegTMax = 256;
+// dK/dV key tiles (all batches and groups) from which the sliding-window backward gives
+// each tile all its query rows in one work item (one item per CU or more)
+constexpr int kDkdvDirectItems = 256;
 
 struct AttnArgs {
   // queries [B,H,Tq,DK], unit stride on the feature axis
@@ -68,6 +71,7 @@ struct AttnArgs {
   int items_per_bg;
   int q0;  // absolute position of query row 0 (0 unless a caller decodes past a cache)
   int seg;  // query entries per dK/dV work item
+  int direct;  // dK/dV items accumulate into dk / dv themselves (one item per key tile)
   // shapes
   int B, H, G, hpg, Tq, Tkv;
   float scale;

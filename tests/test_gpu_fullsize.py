@@ -170,10 +170,22 @@ def test_config2_sliding(dev):
     _sampled_check(_ops.SLIDING, q, kp, v, do, rows, 1 / math.sqrt(64), window=512)
 
 
+def test_dkdv_direct_mode(dev):
+    """Sliding window with at least 256 key tiles over all batches and groups: each dK/dV
+    work item owns one 128-key tile with all its query rows and adds into dK / dV
+    itself (no partials, no reduce pass); every row of every head checked."""
+    from nsa import _lib
+    B, H, G, T, d, w = 64, 8, 4, 256, 64, 100
+    plan = _lib.dkdv_plan(_ops.SLIDING, B, H, G, T, T, 0, 64, w)
+    assert plan["items_per_bg"] == 2 and plan["segment"] >= w + 127, plan
+    q, kp, v, do = _inputs(dict(B=B, H=H, G=G, T=T, dk=d, dv=d), 600, dev)
+    _sampled_check(_ops.SLIDING, q, kp, v, do, np.arange(T), 1 / math.sqrt(d), window=w)
+
+
 # ------------------------------------------- 256-entry dK/dV query segments at small T
 SEG_CASES = [
     # kind, B, H, G, T, dk, dv, extra
-    (_ops.SLIDING, 43, 8, 4, 1024, 32, 32, dict(window=512)),
+    (_ops.SLIDING, 1, 6, 3, 8192, 32, 32, dict(window=8192)),
     (_ops.COMPRESSION, 18, 16, 4, 5000, 32, 32, {}),
     (_ops.SELECTION, 26, 8, 4, 512, 64, 64, dict(lprime=64, n=16)),
 ]
