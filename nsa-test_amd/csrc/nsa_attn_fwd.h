@@ -110,11 +110,19 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
 
   f32x4 oacc[NSUB][DV / 16];
   float m2[NSUB], mtrue[NSUB], lsum[NSUB];  // exponent reference, true maximum, sum
+  // bf16: the column sums of P come from the matrix cores (the packed P fragment times an
+  // all-ones A operand: every row of the 16x16 result holds the column's sum of the bf16
+  // probabilities, the same rounded values the P.V product uses) instead of per-element
+  // adds and lane reductions; the exponent argument is a single fma
+  constexpr bool kMmaSum = sizeof(S) == 2;
+  f32x4 lacc[NSUB];
+  const uint4 ones = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) {
     m2[s] = -INFINITY;
     mtrue[s] = -INFINITY;
     lsum[s] = 0.f;
+    lacc[s] = zero4();
 #pragma unroll
     for (int j = 0; j < DV / 16; ++j) oacc[s][j] = zero4();
   }
@@ -228,23 +236,31 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
         const float mnew = fmaxf(m2[s], mtrue[s]);
         const float alpha = m2[s] == -INFINITY ? 0.f : fast_exp2(m2[s] - mnew);
         lsum[s] *= alpha;
+        lacc[s] *= alpha;
 #pragma unroll
         for (int j = 0; j < DV / 16; ++j) oacc[s][j] *= alpha;
         m2[s] = mnew;
       }
       const float nref = m2[s] == -INFINITY ? 0.f : -m2[s];
-      float rs = 0.f;
+      if constexpr (kMmaSum) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+        for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = fast_exp2(mul_add_rounded(st[s][ks][i], scale2, nref));
-          st[s][ks][i] = p;
-          rs += p;
+          for (int i = 0; i < 4; ++i) st[s][ks][i] = fast_exp2(fmaf(st[s][ks][i], scale2, nref));
+      } else {
+        float rs = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = fast_exp2(mul_add_rounded(st[s][ks][i], scale2, nref));
+            st[s][ks][i] = p;
+            rs += p;
+          }
         }
+        rs = wave_sum16(rs);
+        lsum[s] += rs;
       }
-      rs = wave_sum16(rs);
-      lsum[s] += rs;
 #pragma unroll
       for (int kc2 = 0; kc2 < 64 / CK; ++kc2) pf[s][kc2] = CFrag<T>::pack(st[s][kc2 * CT], st[s][kc2 * CT + CT - 1]);
     }
@@ -257,6 +273,10 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
         const uint4 vf = vb[(kc2 * (DV / 16) + j) * 64 + lane];
 #pragma unroll
         for (int s = 0; s < NSUB; ++s) oacc[s][j] = Mma<T>::run(oacc[s][j], vf, pf[s][kc2]);
+      }
+      if constexpr (kMmaSum) {
+#pragma unroll
+        for (int s = 0; s < NSUB; ++s) lacc[s] = Mma<T>::run(lacc[s], ones, pf[s][kc2]);
       }
     }
   };
@@ -296,6 +316,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) {
     if (!colv[s]) continue;
+    if constexpr (kMmaSum) lsum[s] = lacc[s][0];
     const float inv = lsum[s] > 0.f ? 1.f / lsum[s] : 0.f;
     // the sum relative to the true maximum (m2 <= mtrue, equal when both are -inf)
     if (lsum[s] > 0.f) lsum[s] *= fast_exp2(m2[s] - mtrue[s]);

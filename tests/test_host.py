@@ -109,8 +109,12 @@ def test_workspace_sizes():
     f = _lib.size("nsa_fwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64)
     b = _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 512)
     assert 0 < f < b
-    # a wider window spreads each key tile over more query segments
-    assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 8192) > b
+    # with >= 256 key tiles (Z*G*tiles) the sliding dK/dV adds straight into dK/dV:
+    # a wider window needs no partials then
+    assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 8192) == b
+    # with fewer tiles a wider window spreads each key tile over more query segments
+    b1 = _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 16, 1, 8192, 8192, 192, 128, 0, 64, 512)
+    assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 16, 1, 8192, 8192, 192, 128, 0, 64, 8192) > b1
     s = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 16, 64, 1)
     assert s > f
     # scoring: fp32 logits [Z*H][T][N rounded up to 64], then one int per 128-row tile of
