@@ -8,7 +8,8 @@ namespace nsa {
 enum Branch : int { kSliding = 0, kCompression = 1, kSelection = 2 };
 enum DType : int { kF32 = 0, kBF16 = 1 };
 
-// Columns handled by one forward / dQ workgroup (4 waves x NSUB x 16).
+// Columns handled by one dense forward workgroup (kFwdWaves waves x NSUB x 16) and one
+// dense dQ workgroup (kDqWaves waves x 16).
 constexpr int kFwdNSub = 1;
 constexpr int kFwdWaves = 8;
 constexpr int kFwdCols = kFwdWaves * kFwdNSub * 16;

@@ -15,7 +15,10 @@
 //
 // Every item writes its fp32 dK/dV partial for its keys; a reduce kernel sums the
 // segments of each key tile in a fixed order and accumulates into the caller's dK/dV.
-// No floating-point atomics: the result is bit-reproducible.
+// Direct mode (sliding window with at least kDkdvDirectItems key tiles over all batches
+// and groups, so one item per tile still fills the machine): the item's segment is the
+// tile's whole query span and it adds its sums into dK/dV itself, with no partials and
+// no reduce.  No floating-point atomics: the result is bit-reproducible.
 //
 // Backward algebra (reference nsa/kernels.py:1303-1530): with s = scale q.k,
 //   p = exp(s - M - L),  dS = p (dO.v - D),  dK = scale dS^T Q,  dV = p^T dO.
