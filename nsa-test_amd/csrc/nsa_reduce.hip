@@ -4,6 +4,7 @@
 // each item wrote fp32 partials [keys][DK + DV].  One workgroup per key tile
 // sums them in item order (fixed, so the result is reproducible) and accumulates
 // into the caller's dK / dV with their strides.
+#include <algorithm>
 #include "nsa_attn.h"
 #include "nsa_attn_bwd_dkdv.h"
 #include "nsa_device.h"
@@ -32,7 +33,7 @@ bool dispatch_attn_bwd_dkdv(int dtype, int dk, int dv, int br, const AttnArgs& a
 }
 
 template <typename T>
-__global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK, int DV, int br) {
+__global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK, int DV, int br, int split) {
   using S = typename Store<T>::type;
   const int bg = blockIdx.y;
   const int b = bg / a.G, grp = bg % a.G;
@@ -58,25 +59,17 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
   }
   if (count == 0 || key0 >= key_hi) return;
   const float* base = a.partial + (int64_t)bg * a.items_per_bg * keys * width;
+  const int64_t istride = (int64_t)step * keys * width;  // floats between consecutive items
   // blockIdx.z splits the tile's keys x width elements (in groups of four: DK and DV are
-  // multiples of four, so a group never straddles dK / dV) over kReduceSplit workgroups
+  // multiples of four, so a group never straddles dK / dV) over `split` workgroups
   const int n4 = keys * width / 4;
-  const int per = (n4 + kReduceSplit - 1) / kReduceSplit;
+  const int per = (n4 + split - 1) / split;
   const int e_end = min(n4, (int)(blockIdx.z + 1) * per);
   for (int e4 = blockIdx.z * per + threadIdx.x; e4 < e_end; e4 += 256) {
     const int e = 4 * e4;
     const int kl = e / width, col = e % width;
     const int key = key0 + kl;
     if (key >= key_hi) continue;
-    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int k = 0; k < count; ++k) {
-      const float4 v = *reinterpret_cast<const float4*>(base + (int64_t)(first + k * step) * keys * width + e);
-      sum.x += v.x;
-      sum.y += v.y;
-      sum.z += v.z;
-      sum.w += v.w;
-    }
-    const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
     S* p;
     int64_t sd;
     if (col < DK) {
@@ -87,24 +80,39 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
           (int64_t)(col - DK) * a.sdv_d;
       sd = a.sdv_d;
     }
-    if (sd == 1 && (reinterpret_cast<uintptr_t>(p) % (4 * sizeof(S))) == 0) {  // one vector read-modify-write
-      if constexpr (sizeof(S) == 2) {
-        uint2 w = *reinterpret_cast<const uint2*>(p);
-        const float x0 = bf16_bits_to_f32((uint16_t)(w.x & 0xffffu)) + sv[0];
-        const float x1 = bf16_bits_to_f32((uint16_t)(w.x >> 16)) + sv[1];
-        const float x2 = bf16_bits_to_f32((uint16_t)(w.y & 0xffffu)) + sv[2];
-        const float x3 = bf16_bits_to_f32((uint16_t)(w.y >> 16)) + sv[3];
-        w.x = (uint32_t)f32_to_bf16_bits(x0) | ((uint32_t)f32_to_bf16_bits(x1) << 16);
-        w.y = (uint32_t)f32_to_bf16_bits(x2) | ((uint32_t)f32_to_bf16_bits(x3) << 16);
-        *reinterpret_cast<uint2*>(p) = w;
-      } else {
-        float4 w = *reinterpret_cast<const float4*>(p);
-        w.x += sv[0];
-        w.y += sv[1];
-        w.z += sv[2];
-        w.w += sv[3];
-        *reinterpret_cast<float4*>(p) = w;
+    const bool vec = sd == 1 && (reinterpret_cast<uintptr_t>(p) % (4 * sizeof(S))) == 0;
+    // the destination's current values are requested first (independent of the sum)
+    typename Raw4<T>::type old{};
+    if (vec) old = load4_raw<T>(p);
+    // the items' partials in item order (fixed: reproducible), four loads in flight
+    const float* src = base + (int64_t)first * keys * width + e;
+    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    int k = 0;
+    for (; k + 4 <= count; k += 4) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4*>(src + (k + u) * istride);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        sum.x += v[u].x;
+        sum.y += v[u].y;
+        sum.z += v[u].z;
+        sum.w += v[u].w;
       }
+    }
+    for (; k < count; ++k) {
+      const float4 v = *reinterpret_cast<const float4*>(src + k * istride);
+      sum.x += v.x;
+      sum.y += v.y;
+      sum.z += v.z;
+      sum.w += v.w;
+    }
+    const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
+    if (vec) {  // one vector read-modify-write
+      f32x4 w = raw4_f32(old);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) w[u] += sv[u];
+      store4<T>(p, w);
     } else {
 #pragma unroll
       for (int u = 0; u < 4; ++u) p[u * sd] = Elem<T>::from_f32(Elem<T>::to_f32(p[u * sd]) + sv[u]);
@@ -117,11 +125,17 @@ void launch_partial_reduce(int dtype, int dk, int dv, int br, const AttnArgs& a,
   if (br != kSelection) tiles = (a.Tkv + dkdv_keys(br) - 1) / dkdv_keys(br);
   else tiles = a.nblk * ((a.lprime + 63) / 64);
   if (tiles <= 0) return;
-  dim3 grid(tiles, a.B * a.G, kReduceSplit);
+  // at least ~2048 workgroups (few key tiles: compression), each with one or more float4
+  // groups per thread
+  const int n4 = dkdv_keys(br) * (dk + dv) / 4;
+  const int64_t tb = (int64_t)tiles * a.B * a.G;
+  int split = (int)std::min<int64_t>(std::max<int64_t>(kReduceSplit, (2048 + tb - 1) / tb), (n4 + 255) / 256);
+  split = std::max(split, 1);
+  dim3 grid(tiles, a.B * a.G, split);
   if (dtype == kF32)
-    hipLaunchKernelGGL(partial_reduce_kernel<float>, grid, dim3(256), 0, st, a, dk, dv, br);
+    hipLaunchKernelGGL(partial_reduce_kernel<float>, grid, dim3(256), 0, st, a, dk, dv, br, split);
   else
-    hipLaunchKernelGGL(partial_reduce_kernel<bf16>, grid, dim3(256), 0, st, a, dk, dv, br);
+    hipLaunchKernelGGL(partial_reduce_kernel<bf16>, grid, dim3(256), 0, st, a, dk, dv, br, split);
 }
 
 }  // namespace nsa
