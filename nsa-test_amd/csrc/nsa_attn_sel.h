@@ -69,18 +69,38 @@ __device__ __forceinline__ bool sel_has(const int* l, int nslots, int blk) {
 }
 
 // ============================================================== forward
+// Two phases.  (1) bf16: the blocks every wave of the workgroup selected (at 16 heads per
+// group: the four timesteps' common blocks -- block 0 and the local ones at least) are
+// walked by the whole workgroup: each tile's K / V^T fragments are copied direct-to-LDS
+// once and all four waves compute from them.  (2) Every wave walks the rest of its
+// union on its own, fragments straight from L2 into registers one tile ahead.  Both
+// phases feed the same online softmax; every column applies its own selection mask in
+// both.
+template <typename T, int DK, int DV>
+struct SelFwdShared {
+  static constexpr int KC = Elem<T>::kKChunk;
+  static constexpr int CK = CFrag<T>::kKeys;
+  static constexpr int NKF = 4 * (DK / KC);          // K rowfrags of a 64-key tile
+  static constexpr int NVF = (64 / CK) * (DV / 16);  // V^T colfrags
+  static constexpr bool kOn = sizeof(typename Store<T>::type) == 2;
+  static constexpr int kLdsBytes = kOn ? (NKF + NVF) * 1024 : 0;
+};
+
 template <typename T, int DK, int DV>
 // Two waves per SIMD (256 registers): the second wave covers the latency of the first
 // one's fragment loads and softmax, which bound this kernel with one wave per SIMD.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_sel_fwd_kernel(AttnArgs a, int ncoltiles) {
   using S = typename Store<T>::type;
+  using SH = SelFwdShared<T, DK, DV>;
   constexpr int EPF = Elem<T>::kPerFrag;
   constexpr int KC = Elem<T>::kKChunk;
   constexpr int NKC = DK / KC;
   constexpr int CK = CFrag<T>::kKeys;
   constexpr int CT = CK / 16;
+  constexpr int NWD = kSelMaxBlocks / 32;
   __shared__ int s_lst[4][kSelMaxT * 64];
-  __shared__ uint32_t s_bits[4][kSelMaxBlocks / 32];
+  __shared__ uint32_t s_bits[4][NWD];
+  extern __shared__ __attribute__((aligned(16))) uint4 sel_tile[];  // [NKF + NVF][64] (phase 1)
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform control below
@@ -91,16 +111,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   const int hpg = a.hpg;
   const int ncols = a.Tq * hpg;
   const int f0 = (L % ncoltiles) * 64 + wave * kSelWaveCols;
-  if (f0 >= ncols) return;  // whole wave idle (no barriers below)
+  const bool active = f0 < ncols;  // idle waves still meet the phase-1 barriers
   const float scale2 = a.scale * kLog2e;
+  const int nwords = (a.nblk + 31) / 32;
 
-  SelWave w;
+  SelWave w{0, 0};
   int* lst = s_lst[wave];
   uint32_t* bits = s_bits[wave];
-  sel_wave_setup<T, false>(a, bg, f0, lst, bits, w, lane);
+  if (active) {
+    sel_wave_setup<T, false>(a, bg, f0, lst, bits, w, lane);
+  } else if (SH::kOn) {
+    for (int i = lane; i < nwords; i += 64) bits[i] = 0;
+  }
 
   const int f = f0 + c16;
-  const bool colv = f < ncols;
+  const bool colv = active && f < ncols;
   const int colt = colv ? f / hpg : w.t_first;
   const int colh = colv ? grp * hpg + f % hpg : grp * hpg;
   const int t_last = w.t_first + w.nt - 1 + a.q0;  // absolute positions: row r is at a.q0 + r
@@ -118,9 +143,112 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 #pragma unroll
   for (int j = 0; j < DV / 16; ++j) oacc[j] = zero4();
   float m2 = -INFINITY, mtrue = -INFINITY, lsum = 0.f;  // exponent reference, true maximum, sum
-  const int nwords = (a.nblk + 31) / 32;
   const bool one_t = w.nt == 1;
 
+  // masking and the online softmax of one tile's S^T (keys key0 .. key0 + 63 of block blk
+  // [blk_lo, blk_hi)); returns the packed P^T fragments
+  auto softmax_tile = [&](f32x4 (&st)[4], int key0, int blk, int blk_hi, uint4 (&pf)[64 / CK])
+                          __attribute__((always_inline)) {
+    const int blk_lo = blk * a.lprime;
+    const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
+    // end of the keys of this block the lane's column sees (blk_lo when none)
+    const int kend = colsel ? max(blk_lo, a.causal ? min(blk_hi, colt + a.q0 + 1) : blk_hi) : blk_lo;
+    const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first + a.q0) && key0 >= blk_lo &&
+                             key0 + 63 < blk_hi && f0 + kSelWaveCols <= ncols;
+    float mx = -INFINITY;
+    // lane-visible keys of this block: [blk_lo, kend); branch-free test per element
+    const uint32_t span = all_visible ? 0xffffffffu : (uint32_t)(kend - blk_lo);
+    const int kb = key0 + 4 * g4 - blk_lo;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = (uint32_t)(kb + ks * 16 + i) < span;
+        const float v = ok ? st[ks][i] : -INFINITY;
+        st[ks][i] = v;
+        mx = fmaxf(mx, v);
+      }
+    // maximum over the raw products (scale2 > 0; the exponent argument is the rounded
+    // product minus the reference, so the maximum maps to exp2(0) = 1 exactly); lazy
+    // rescale of the exponent reference m2 (moves only when a column maximum exceeds it
+    // by kLazyRescale), the true maximum mtrue kept for M and the epilogue
+    mx = wave_max16(mx) * scale2;
+    mtrue = fmaxf(mtrue, mx);
+    if (__ballot(mx > m2 + kLazyRescale) != 0ull) {
+      const float mnew = fmaxf(m2, mtrue);
+      const float alpha = m2 == -INFINITY ? 0.f : fast_exp2(m2 - mnew);
+      lsum *= alpha;
+#pragma unroll
+      for (int j = 0; j < DV / 16; ++j) oacc[j] *= alpha;
+      m2 = mnew;
+    }
+    const float nref = m2 == -INFINITY ? 0.f : -m2;
+    float rs = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = fast_exp2(mul_add_rounded(st[ks][i], scale2, nref));
+        st[ks][i] = p;
+        rs += p;
+      }
+    lsum += wave_sum16(rs);
+#pragma unroll
+    for (int kc2 = 0; kc2 < 64 / CK; ++kc2) pf[kc2] = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
+  };
+
+  // ---- phase 1: the workgroup's common blocks, one LDS copy per tile -----------------
+  __shared__ uint32_t s_common[SH::kOn ? NWD : 1];
+  if constexpr (SH::kOn) {
+    __syncthreads();  // every wave's bitmap is written
+    for (int i = threadIdx.x; i < nwords; i += 256) s_common[i] = s_bits[0][i] & s_bits[1][i] & s_bits[2][i] & s_bits[3][i];
+    __syncthreads();
+    const int t_max = (min((L % ncoltiles) * 64 + 64, ncols) - 1) / hpg + a.q0;  // the workgroup's last position
+    for (int wd = 0; wd < nwords; ++wd) {
+      uint32_t word = s_common[wd];  // uniform across the workgroup
+      while (word) {
+        const int blk = wd * 32 + __builtin_ctz(word);
+        word &= word - 1;
+        const int lo = blk * a.lprime;
+        const int blk_hi = min(lo + a.lprime, a.Tkv);
+        for (int key0 = lo & ~31; key0 < blk_hi && !(a.causal && key0 > t_max); key0 += 64) {
+          for (int fr = wave; fr < SH::NKF + SH::NVF; fr += 4) {
+            const S* src;
+            if (fr < SH::NKF) {
+              const int ks = fr / NKC, kc = fr % NKC;
+              src = krf + ((((int64_t)(key0 >> 4) + ks) * NKC + kc) * 64 + lane) * EPF;
+            } else {
+              const int v = fr - SH::NKF, kc2 = v / (DV / 16), j = v % (DV / 16);
+              src = vcf + ((((int64_t)(key0 / CK) + kc2) * (DV / 16) + j) * 64 + lane) * EPF;
+            }
+            copy16_to_lds(src, sel_tile + fr * 64);
+          }
+          __builtin_amdgcn_s_waitcnt(0);
+          __syncthreads();
+          if (active) {
+            f32x4 st[4];
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+              st[ks] = zero4();
+#pragma unroll
+              for (int kc = 0; kc < NKC; ++kc) st[ks] = Mma<T>::run(st[ks], sel_tile[(ks * NKC + kc) * 64 + lane], qf[kc]);
+            }
+            uint4 pf[64 / CK];
+            softmax_tile(st, key0, blk, blk_hi, pf);
+#pragma unroll
+            for (int kc2 = 0; kc2 < 64 / CK; ++kc2)
+#pragma unroll
+              for (int j = 0; j < DV / 16; ++j)
+                oacc[j] = Mma<T>::run(oacc[j], sel_tile[(SH::NKF + kc2 * (DV / 16) + j) * 64 + lane], pf[kc2]);
+          }
+          __syncthreads();  // the tile is read before the next copy
+        }
+      }
+    }
+  }
+  if (!active) return;
+
+  // ---- phase 2: the rest of the wave's union, straight from L2 --------------------------
   // Tile cursor over the union bitmap (wave-uniform scalar state).  Tiles start on a
   // 32-key boundary (the C-permuted chunks of vt / kn) and cover 64 keys.
   int c_wd = -1, c_blk = -1, c_key0 = 0, c_hi = 0;
@@ -132,7 +260,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     }
     while (c_word == 0) {
       if (++c_wd >= nwords) return false;
-      c_word = __builtin_amdgcn_readfirstlane(bits[c_wd]);
+      uint32_t wd = bits[c_wd];
+      if constexpr (SH::kOn) wd &= ~s_common[c_wd];
+      c_word = __builtin_amdgcn_readfirstlane(wd);
     }
     c_blk = c_wd * 32 + __builtin_ctz(c_word);
     c_word &= c_word - 1;
@@ -167,7 +297,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
   }
   while (have) {
     const int key0 = c_key0, blk = c_blk;
-    const int blk_lo = blk * a.lprime;
     const int blk_hi = c_hi;
     // S^T[key, col] for the 64 keys of this tile
     f32x4 st[4];
@@ -179,55 +308,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
     }
     const bool have_next = advance();
     if (have_next) load_k(c_key0);
-
-    const bool colsel = colv && (one_t || sel_has(mylst, a.nslots, blk));
-    // end of the keys of this block the lane's column sees (blk_lo when none)
-    const int kend = colsel ? max(blk_lo, a.causal ? min(blk_hi, colt + a.q0 + 1) : blk_hi) : blk_lo;
-    const bool all_visible = one_t && colv && (!a.causal || key0 + 63 <= w.t_first + a.q0) && key0 >= blk_lo &&
-                             key0 + 63 < blk_hi && f0 + kSelWaveCols <= ncols;
-    float mx = -INFINITY;
-    // lane-visible keys of this block: [blk_lo, kend); branch-free test per element
-    const uint32_t span = all_visible ? 0xffffffffu : (uint32_t)(kend - blk_lo);
-    const int kb = key0 + 4 * g4 - blk_lo;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool ok = (uint32_t)(kb + ks * 16 + i) < span;
-        const float v = ok ? st[ks][i] : -INFINITY;
-        st[ks][i] = v;
-        mx = fmaxf(mx, v);
-      }
-    // maximum over the raw products (scale2 > 0; the exponent argument is the rounded
-    // product minus the reference, so the maximum maps to exp2(0) = 1 exactly); lazy rescale of the exponent
-    // reference m2 (moves only when a column maximum exceeds it by kLazyRescale), the
-    // true maximum mtrue kept for M and the epilogue
-    mx = wave_max16(mx) * scale2;
-    mtrue = fmaxf(mtrue, mx);
-    if (__ballot(mx > m2 + kLazyRescale) != 0ull) {
-      const float mnew = fmaxf(m2, mtrue);
-      const float alpha = m2 == -INFINITY ? 0.f : fast_exp2(m2 - mnew);
-      lsum *= alpha;
-#pragma unroll
-      for (int j = 0; j < DV / 16; ++j) oacc[j] *= alpha;
-      m2 = mnew;
-    }
-    const float nref = m2 == -INFINITY ? 0.f : -m2;
-    float rs = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = fast_exp2(mul_add_rounded(st[ks][i], scale2, nref));
-        st[ks][i] = p;
-        rs += p;
-      }
-    lsum += wave_sum16(rs);
+    uint4 pf[64 / CK];
+    softmax_tile(st, key0, blk, blk_hi, pf);
 #pragma unroll
     for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
-      const uint4 pf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
 #pragma unroll
-      for (int j = 0; j < DV / 16; ++j) oacc[j] = Mma<T>::run(oacc[j], vf[kc2][j], pf);
+      for (int j = 0; j < DV / 16; ++j) oacc[j] = Mma<T>::run(oacc[j], vf[kc2][j], pf[kc2]);
     }
     if (have_next) load_v(c_key0);
     have = have_next;
@@ -249,8 +335,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 
 template <typename T, int DK, int DV>
 void launch_attn_sel_fwd(const AttnArgs& a, hipStream_t s) {
+  using SH = SelFwdShared<T, DK, DV>;
   const int ncoltiles = (a.Tq * a.hpg + 63) / 64;
-  hipLaunchKernelGGL((attn_sel_fwd_kernel<T, DK, DV>), dim3(ncoltiles * a.B * a.G), dim3(256), 0, s, a, ncoltiles);
+  if (SH::kLdsBytes > 0)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_sel_fwd_kernel<T, DK, DV>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, SH::kLdsBytes);
+  hipLaunchKernelGGL((attn_sel_fwd_kernel<T, DK, DV>), dim3(ncoltiles * a.B * a.G), dim3(256), SH::kLdsBytes, s, a,
+                     ncoltiles);
 }
 
 // ============================================================== dQ
