@@ -14,7 +14,8 @@ constexpr int kFwdNSub = 1;
 constexpr int kFwdWaves = 8;
 constexpr int kFwdCols = kFwdWaves * kFwdNSub * 16;
 constexpr int kDqWaves = 12;
-constexpr int kDqCols = kDqWaves * 16;
+constexpr int kDqNSub = 1;
+constexpr int kDqCols = kDqWaves * kDqNSub * 16;
 // Distinct selection blocks a row's union bitmap can hold.
 constexpr int kSelMaxBlocks = 4096;
 // Query rows staged per step of the dK/dV kernels.

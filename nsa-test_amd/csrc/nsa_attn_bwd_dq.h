@@ -17,7 +17,7 @@
 namespace nsa {
 
 // ============================== dQ (query-major) ===============================
-// Workgroup = kDqWaves waves x 16 query columns.  The operands of a 64-key tile --
+// Workgroup = kDqWaves waves x kDqNSub x 16 query columns.  The operands of a 64-key tile --
 // K rowfrags (S^T = K Q^T), V rowfrags (dP^T = V dO^T) and K^T colfrags
 // (dQ^T += K^T dS^T) -- are copied global -> LDS by direct-to-LDS loads from the
 // fragment-native krf / vrf / kcf layouts, one 1 KB MFMA fragment per instruction, into a
@@ -47,6 +47,7 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
   constexpr int CK = CFrag<T>::kKeys;
   constexpr int CT = CK / 16;
   constexpr int NW = kDqWaves;
+  constexpr int NS = kDqNSub;  // 16-column subtiles per wave: each fragment read feeds NS products
   static_assert(DK % KC == 0 && DV % KC == 0, "head dims");
 
   extern __shared__ __attribute__((aligned(16))) uint4 dq_lds[];  // [NBUF][NF][64]
@@ -72,34 +73,42 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
   const S* kcf = reinterpret_cast<const S*>(a.kcf) + (int64_t)bg * DK * a.Tp;
   const S* vrf = reinterpret_cast<const S*>(a.vrf) + (int64_t)bg * a.Tp * DV;
 
-  // one 16-column subtile per wave
-  const int f0 = col_base + wave * 16;
-  const int f = f0 + c16;
-  const bool colv = f < ncols;
-  const int colt = colv ? f / hpg : 0;
-  const int colh = colv ? grp * hpg + f % hpg : 0;
-  const int sub_t0 = f0 / hpg;
-  const int sub_t1 = f0 < ncols ? min(a.Tq - 1, (f0 + 15) / hpg) : -1;
-  uint4 qf[NKC], dof[NVC];
-  {
-    const S* qp = reinterpret_cast<const S*>(a.q) + b * a.sq_b + (int64_t)colh * a.sq_h + (int64_t)colt * a.sq_t;
-    const S* dp = reinterpret_cast<const S*>(a.dout) + b * a.sdo_b + (int64_t)colh * a.sdo_h +
-                  (int64_t)colt * a.sdo_t;
+  // NS 16-column subtiles per wave
+  int colt[NS], colh[NS], sub_t0[NS], sub_t1[NS], kmin_s[NS];
+  bool colv[NS], full[NS];
+  uint32_t kspan_s[NS];
+  int64_t srow[NS];
+  uint4 qf[NS][NKC], dof[NS][NVC];
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    const int f0 = col_base + (wave * NS + s) * 16;
+    const int f = f0 + c16;
+    colv[s] = f < ncols;
+    full[s] = f0 + 16 <= ncols;
+    colt[s] = colv[s] ? f / hpg : 0;
+    colh[s] = colv[s] ? grp * hpg + f % hpg : 0;
+    sub_t0[s] = f0 / hpg;
+    sub_t1[s] = f0 < ncols ? min(a.Tq - 1, (f0 + 15) / hpg) : -1;
+    const S* qp = reinterpret_cast<const S*>(a.q) + b * a.sq_b + (int64_t)colh[s] * a.sq_h + (int64_t)colt[s] * a.sq_t;
+    const S* dp = reinterpret_cast<const S*>(a.dout) + b * a.sdo_b + (int64_t)colh[s] * a.sdo_h +
+                  (int64_t)colt[s] * a.sdo_t;
 #pragma unroll
     for (int kc = 0; kc < NKC; ++kc)
-      qf[kc] = colv ? *reinterpret_cast<const uint4*>(qp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
+      qf[s][kc] = colv[s] ? *reinterpret_cast<const uint4*>(qp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int kc = 0; kc < NVC; ++kc)
-      dof[kc] = colv ? *reinterpret_cast<const uint4*>(dp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
+      dof[s][kc] = colv[s] ? *reinterpret_cast<const uint4*>(dp + kc * KC + g4 * EPF) : make_uint4(0, 0, 0, 0);
+    srow[s] = ((int64_t)b * a.H + colh[s]) * a.Tq + colt[s];
+    // sliding: the column sees keys [kmin_s, kmin_s + kspan_s) (branch-free test)
+    kmin_s[s] = max(colt[s] - a.window + 1, 0);
+    kspan_s[s] = colv[s] ? (uint32_t)max(0, min(colt[s], a.Tkv - 1) + 1 - kmin_s[s]) : 0u;
   }
-  const int64_t srow = ((int64_t)b * a.H + colh) * a.Tq + colt;
-  // sliding: the column sees keys [kmin_s, kmin_s + kspan_s) (branch-free test)
-  const int kmin_s = max(colt - a.window + 1, 0);
-  const uint32_t kspan_s = colv ? (uint32_t)max(0, min(colt, a.Tkv - 1) + 1 - kmin_s) : 0u;
 
-  f32x4 dqa[DK / 16];
+  f32x4 dqa[NS][DK / 16];
 #pragma unroll
-  for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
+  for (int s = 0; s < NS; ++s)
+#pragma unroll
+    for (int j = 0; j < DK / 16; ++j) dqa[s][j] = zero4();
 
   int ntiles = 0, key_lo = 0;
   if (BR == kSliding) {
@@ -148,8 +157,10 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
     load_be(tile_key0(0));
   }
   // row statistics after the first tile's copies are issued (their O loads overlap them)
-  float l2, dl, rgate;
-  dq_row_stats<T, NVC>(a, b, colh, colt, colv, dof, g4, srow, l2, dl, rgate);
+  float l2[NS], dl[NS], rgate[NS];
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    dq_row_stats<T, NVC>(a, b, colh[s], colt[s], colv[s], dof[s], g4, srow[s], l2[s], dl[s], rgate[s]);
 
   for (int it = 0; it < ntiles; ++it) {
     const int key0 = tile_key0(it);
@@ -173,43 +184,63 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
 
     // Every (subtile, tile) pair runs the products, fully masked when no key is
     // visible: a branch around them would make the compiler move the accumulators
-    // between register files on every tile.
-    f32x4 st[4], dp[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      st[ks] = zero4();
-      dp[ks] = zero4();
-#pragma unroll
-      for (int kc = 0; kc < NKC; ++kc) st[ks] = Mma<T>::run(st[ks], kb[(ks * NKC + kc) * 64 + lane], qf[kc]);
-#pragma unroll
-      for (int kc = 0; kc < NVC; ++kc) dp[ks] = Mma<T>::run(dp[ks], vb[(ks * NVC + kc) * 64 + lane], dof[kc]);
-    }
-    bool all_visible = false;
-    const bool full = f0 + 16 <= ncols;
-    if (BR == kSliding)
-      all_visible = full && key0 + 63 <= sub_t0 && key0 > sub_t1 - a.window && key0 + 63 < a.Tkv;
-    else
-      all_visible = full && be_max <= sub_t0;
+    // between register files on every tile.  Each fragment read from LDS feeds the
+    // products of all NS subtiles.
+    f32x4 st[NS][4], dp[NS][4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        bool ok = true;
-        if (!all_visible) {
-          const int key = key0 + ks * 16 + 4 * g4 + i;
-          if (BR == kSliding) ok = (uint32_t)(key - kmin_s) < kspan_s;
-          else ok = colv & (sbe[ks * 16 + 4 * g4 + i] <= colt);
-        }
-        // the mask on the exponent argument: no divergent branch around the exp
-        const float p = fast_exp2(ok ? st[ks][i] * scale2 - l2 : -INFINITY);
-        st[ks][i] = p * (dp[ks][i] - dl);  // dS^T
+      for (int s = 0; s < NS; ++s) {
+        st[s][ks] = zero4();
+        dp[s][ks] = zero4();
       }
+#pragma unroll
+      for (int kc = 0; kc < NKC; ++kc) {
+        const uint4 kf = kb[(ks * NKC + kc) * 64 + lane];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) st[s][ks] = Mma<T>::run(st[s][ks], kf, qf[s][kc]);
+      }
+#pragma unroll
+      for (int kc = 0; kc < NVC; ++kc) {
+        const uint4 vf = vb[(ks * NVC + kc) * 64 + lane];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dp[s][ks] = Mma<T>::run(dp[s][ks], vf, dof[s][kc]);
+      }
+    }
+    uint4 sf[NS][64 / CK];
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      bool all_visible = false;
+      if (BR == kSliding)
+        all_visible = full[s] && key0 + 63 <= sub_t0[s] && key0 > sub_t1[s] - a.window && key0 + 63 < a.Tkv;
+      else
+        all_visible = full[s] && be_max <= sub_t0[s];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          bool ok = true;
+          if (!all_visible) {
+            const int key = key0 + ks * 16 + 4 * g4 + i;
+            if (BR == kSliding) ok = (uint32_t)(key - kmin_s[s]) < kspan_s[s];
+            else ok = colv[s] & (sbe[ks * 16 + 4 * g4 + i] <= colt[s]);
+          }
+          // the mask on the exponent argument: no divergent branch around the exp
+          const float p = fast_exp2(ok ? st[s][ks][i] * scale2 - l2[s] : -INFINITY);
+          st[s][ks][i] = p * (dp[s][ks][i] - dl[s]);  // dS^T
+        }
+      }
+#pragma unroll
+      for (int kc2 = 0; kc2 < 64 / CK; ++kc2) sf[s][kc2] = CFrag<T>::pack(st[s][kc2 * CT], st[s][kc2 * CT + CT - 1]);
     }
 #pragma unroll
     for (int kc2 = 0; kc2 < 64 / CK; ++kc2) {
-      const uint4 sf = CFrag<T>::pack(st[kc2 * CT], st[kc2 * CT + CT - 1]);
 #pragma unroll
-      for (int j = 0; j < DK / 16; ++j) dqa[j] = Mma<T>::run(dqa[j], tb[(kc2 * (DK / 16) + j) * 64 + lane], sf);
+      for (int j = 0; j < DK / 16; ++j) {
+        const uint4 tf = tb[(kc2 * (DK / 16) + j) * 64 + lane];
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dqa[s][j] = Mma<T>::run(dqa[s][j], tf, sf[s][kc2]);
+      }
     }
     if (TL::NBUF == 1 && it + 1 < ntiles) {  // single buffer: refill once every wave is done
       __syncthreads();
@@ -218,19 +249,21 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
     }
   }
 
-  if (colv) {
+#pragma unroll
+  for (int s = 0; s < NS; ++s) {
+    if (!colv[s]) continue;
     // accumulate mode: the caller's running dQ (loaded here, not at the start: the
     // registers are not spare in this kernel)
-    S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)colt * a.sdq_t;
+    S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh[s] * a.sdq_h + (int64_t)colt[s] * a.sdq_t;
     typename Raw4<T>::type dq_prev[DK / 16];
     if (a.dq_acc) {
 #pragma unroll
       for (int j = 0; j < DK / 16; ++j) dq_prev[j] = load4_raw<T>(dqp + j * 16 + 4 * g4);
     }
-    const float sg = a.scale * rgate;
+    const float sg = a.scale * rgate[s];
 #pragma unroll
     for (int j = 0; j < DK / 16; ++j) {
-      f32x4 v = dqa[j] * sg;
+      f32x4 v = dqa[s][j] * sg;
       if (a.dq_acc) v += raw4_f32(dq_prev[j]);
       store4<T>(dqp + j * 16 + 4 * g4, v);
     }
