@@ -325,7 +325,8 @@ class NSACore(torch.autograd.Function):
     def backward(ctx, dout):
         (q, kc, vc, be, ks, vs, idx, kw, vw, g, o_c, o_s, o_w, Lc, Mc, Ls, Ms, Lw, Mw) = ctx.saved_tensors
         sc = ctx.scale
-        dq = torch.empty(q.shape, device=q.device, dtype=_ops.compute_dtype(q.dtype))
+        # dQ in q's own layout (no transposing copy on the way back to the projection)
+        dq = torch.empty_like(q, dtype=_ops.compute_dtype(q.dtype))
         if ctx.fused:
             d = dout.to(o_c.dtype)
             if d.stride() != o_c.stride():  # one copy into the branch outputs' layout
@@ -786,7 +787,8 @@ class NSAAttention(torch.nn.Module):
             indices, p_cmp, p_slc = sel, None, None
 
         gate_logits = self.gate_mlp(x).view(B, T, H, 3).permute(0, 2, 1, 3)
-        qk = q.contiguous()
+        # the projection's [B,T,H,dk] storage as it is (the kernels take any row strides)
+        qk = q if _ops._rows_ok(q) else q.contiguous()
         o = NSACore.apply(qk, k_cmp, v_cmp, block_ends, k_sel.transpose(-1, -2), v_sel, indices,
                           k_win.transpose(-1, -2), v_win, gate_logits, self.scale, c)
         o = o.transpose(1, 2).reshape(B, T, H * dv)
