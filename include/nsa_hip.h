@@ -44,6 +44,9 @@ enum {
   NSA_ERR_HIP = 5
 };
 
+/* bwd_flags bits of the backward extensions (nsa_*_bwd_ex) */
+enum { NSA_BWD_DQ_ACCUMULATE = 1, NSA_BWD_DKDV_OVERWRITE = 2 };
+
 /* ABI revision of this header. */
 int nsa_abi_version(void);
 /* Text of the last error raised on the calling thread ("" if none). */
@@ -215,10 +218,14 @@ int nsa_score_topn_ex(const void* q, const void* k_cmp, const int32_t* Block_end
 /* Extensions (no counterpart in the reference): the three backward entry points above
  * with two more arguments, for callers that run the three branches over one query
  * tensor and already hold the row sums, such as the NSA module:
- *   dq_accumulate  0: dQ is overwritten, as by the entry point extended; 1: this
- *                  branch's dQ is added to the values dQ already holds (same element
- *                  type, added in fp32 and rounded once), so no separate pass sums the
- *                  branches' dQ.
+ *   bwd_flags      0: as the entry point extended; otherwise a set of bits:
+ *                  NSA_BWD_DQ_ACCUMULATE  this branch's dQ is added to the values dQ
+ *                    already holds (same element type, added in fp32 and rounded
+ *                    once), so no separate pass sums the branches' dQ;
+ *                  NSA_BWD_DKDV_OVERWRITE  dK and dV are overwritten with this
+ *                    branch's gradients (every element written, zeros where no query
+ *                    sees a key) instead of added to, so the caller needs no zero
+ *                    fill.  Other bits are rejected with NSA_ERR_INVALID.
  *   delta_in       null: as the entry point extended; otherwise the row sums
  *                  D = sum_d Out * dOut per (z, h, t) row, fp32, contiguous [Z, H, n_ctx_q],
  *                  which the backward then uses instead of reading Out.
@@ -228,7 +235,7 @@ int nsa_score_topn_ex(const void* q, const void* k_cmp, const int32_t* Block_end
  *                  nsa/kernels.py:2446-2463), so callers pass the mix's dOut unscaled.
  *   row_dot        null, or fp32 contiguous [Z, H, n_ctx_q] receiving sum_d dOut * Out
  *                  per row (the gradient of the row's gate); needs delta_in null.
- * With dq_accumulate = 0 and the three pointers null each behaves exactly as the entry
+ * With bwd_flags = 0 and the three pointers null each behaves exactly as the entry
  * point it extends. */
 int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const void* Out, const void* dOut,
                            float sm_scale, const float* L, const float* M, int64_t stride_qz, int64_t stride_qh,
@@ -242,7 +249,7 @@ int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const
                            int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg, int64_t stride_dvn,
                            int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx, int window_size,
                            int head_dim_qk, int head_dim_v, int dtype,
-                           int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace, size_t workspace_bytes,
+                           int bwd_flags, const float* delta_in, const float* row_gate, float* row_dot, void* workspace, size_t workspace_bytes,
                            nsa_stream_t stream);
 
 int nsa_compression_bwd_ex(const void* Q, const void* K_blocks, const void* V_blocks, const int32_t* Block_ends,
@@ -257,7 +264,7 @@ int nsa_compression_bwd_ex(const void* Q, const void* K_blocks, const void* V_bl
                         int64_t stride_dkg, int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz,
                         int64_t stride_dvg, int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups,
                         int n_ctx_q, int n_blocks, int head_dim_qk, int head_dim_v, int dtype,
-                        int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
+                        int bwd_flags, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
                         size_t workspace_bytes, nsa_stream_t stream);
 
 int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, const void* Block_indices, const void* Out,
@@ -274,7 +281,7 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
                              int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
                              int n_ctx_kv, int n_slots, int block_size_selection, int is_causal, int index_is_int64,
                              int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype,
-                             int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
+                             int bwd_flags, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream);
 
 

@@ -225,10 +225,8 @@ int run_fwd(const Shape& s, const FwdIO& io, float scale, int window, const int3
   a.krf = at<char>(ws, L.krf);
   a.vcf = at<char>(ws, L.vcf);
 
-  launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp, nullptr,
-                nullptr, const_cast<void*>(a.krf), nullptr, st);
-  launch_repack(s.dtype, io.V, io.sv[0], io.sv[1], io.sv[2], io.sv[3], s.Z, s.G, s.Tkv, s.dv, a.Tp, nullptr,
-                nullptr, nullptr, const_cast<void*>(a.vcf), st);
+  launch_repack_kv(s.dtype, io.K, io.sk, s.dk, const_cast<void*>(a.krf), nullptr, io.V, io.sv, s.dv, nullptr,
+                   const_cast<void*>(a.vcf), s.Z, s.G, s.Tkv, a.Tp, st);
   if (s.br == kSelection) {
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
                      s.Tkv, fallback, causal, at<int>(ws, L.clean), nullptr, s.nblk(), s.q0, st);
@@ -248,6 +246,7 @@ struct BwdIO {
   void *dQ, *dK, *dV;
   int64_t sq[4], sk[4], sv[4], so[4], sl[3], sm[3], sdq[4], sdk[4], sdv[4];
   int dq_acc = 0;                   // extension entry points only: add into dQ
+  int dkdv_ow = 0;                  // extension entry points only: overwrite dK / dV
   const float* delta_in = nullptr;  // extension entry points only: precomputed row sums
   const float* row_gate = nullptr;  // extension entry points only: per-row gate of dOut
   float* row_dot = nullptr;         // extension entry points only: receives sum_d dOut * Out
@@ -267,9 +266,24 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   if (io.row_dot && io.delta_in) return fail(NSA_ERR_INVALID, "row_dot needs delta_in = null (it is computed from Out)");
   const Layout L = make_layout(s, true);
   if (ws_bytes < L.total) return fail(NSA_ERR_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, L.total);
-  if (s.Tq == 0) return NSA_OK;
 
   AttnArgs a = base_args(s, scale);
+  a.dk = io.dK;
+  a.sdk_b = io.sdk[0];
+  a.sdk_g = io.sdk[1];
+  a.sdk_t = io.sdk[2];
+  a.sdk_d = io.sdk[3];
+  a.dv = io.dV;
+  a.sdv_b = io.sdv[0];
+  a.sdv_g = io.sdv[1];
+  a.sdv_t = io.sdv[2];
+  a.sdv_d = io.sdv[3];
+  a.dkdv_ow = io.dkdv_ow;
+  if (s.Tq == 0) {  // no query rows: dK / dV receive nothing (zeros when overwritten)
+    if (!io.dkdv_ow) return NSA_OK;
+    launch_zero_dkdv(s.dtype, s.dk, s.dv, a, st);
+    return check_hip("dK/dV zero fill");
+  }
   a.q = io.Q;
   a.sq_b = io.sq[0];
   a.sq_h = io.sq[1];
@@ -299,16 +313,6 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.delta_in = io.delta_in;
   a.row_gate = io.row_gate;
   a.row_dot = io.row_dot;
-  a.dk = io.dK;
-  a.sdk_b = io.sdk[0];
-  a.sdk_g = io.sdk[1];
-  a.sdk_t = io.sdk[2];
-  a.sdk_d = io.sdk[3];
-  a.dv = io.dV;
-  a.sdv_b = io.sdv[0];
-  a.sdv_g = io.sdv[1];
-  a.sdv_t = io.sdv[2];
-  a.sdv_d = io.sdv[3];
   a.window = window;
   a.block_ends = block_ends;
   a.causal = causal;
@@ -324,11 +328,8 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.direct = s.direct() ? 1 : 0;
   a.partial = at<float>(ws, L.partial);
 
-  launch_repack(s.dtype, io.K, io.sk[0], io.sk[1], io.sk[2], io.sk[3], s.Z, s.G, s.Tkv, s.dk, a.Tp,
-                nullptr, nullptr, const_cast<void*>(a.krf),
-                const_cast<void*>(a.kcf), st);
-  launch_repack(s.dtype, io.V, io.sv[0], io.sv[1], io.sv[2], io.sv[3], s.Z, s.G, s.Tkv, s.dv, a.Tp,
-                nullptr, nullptr, const_cast<void*>(a.vrf), nullptr, st);
+  launch_repack_kv(s.dtype, io.K, io.sk, s.dk, const_cast<void*>(a.krf), const_cast<void*>(a.kcf), io.V, io.sv,
+                   s.dv, const_cast<void*>(a.vrf), nullptr, s.Z, s.G, s.Tkv, a.Tp, st);
   if (s.br == kSelection) {
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
                      s.Tkv, fallback, causal, at<int>(ws, L.clean), at<int>(ws, L.chunk), s.nblk(), 0, st);
@@ -393,7 +394,7 @@ int nsa::set_error(int code, const char* msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 
-int nsa_abi_version(void) { return 2; }
+int nsa_abi_version(void) { return 3; }
 const char* nsa_last_error(void) { return g_err; }
 int nsa_head_dims_supported(int dtype, int dk, int dv) {
   return (dtype == NSA_F32 || dtype == NSA_BF16) && dims_supported(dk, dv);
@@ -586,10 +587,13 @@ int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const
                            int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg, int64_t stride_dvn,
                            int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx, int window_size,
                            int head_dim_qk, int head_dim_v, int dtype,
-                           int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace, size_t workspace_bytes,
+                           int bwd_flags, const float* delta_in, const float* row_gate, float* row_dot, void* workspace, size_t workspace_bytes,
                            nsa_stream_t stream) {
   NSA_BWD_IO
-  io.dq_acc = dq_accumulate ? 1 : 0;
+  if (bwd_flags & ~(NSA_BWD_DQ_ACCUMULATE | NSA_BWD_DKDV_OVERWRITE))
+    return fail(NSA_ERR_INVALID, "bwd_flags=%d has unknown bits", bwd_flags);
+  io.dq_acc = (bwd_flags & NSA_BWD_DQ_ACCUMULATE) ? 1 : 0;
+  io.dkdv_ow = (bwd_flags & NSA_BWD_DKDV_OVERWRITE) ? 1 : 0;
   io.delta_in = delta_in;
   io.row_gate = row_gate;
   io.row_dot = row_dot;
@@ -610,10 +614,13 @@ int nsa_compression_bwd_ex(const void* Q, const void* K, const void* V, const in
                         int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz, int64_t stride_dvg,
                         int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
                         int n_blocks, int head_dim_qk, int head_dim_v, int dtype,
-                        int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
+                        int bwd_flags, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
                         size_t workspace_bytes, nsa_stream_t stream) {
   NSA_BWD_IO
-  io.dq_acc = dq_accumulate ? 1 : 0;
+  if (bwd_flags & ~(NSA_BWD_DQ_ACCUMULATE | NSA_BWD_DKDV_OVERWRITE))
+    return fail(NSA_ERR_INVALID, "bwd_flags=%d has unknown bits", bwd_flags);
+  io.dq_acc = (bwd_flags & NSA_BWD_DQ_ACCUMULATE) ? 1 : 0;
+  io.dkdv_ow = (bwd_flags & NSA_BWD_DKDV_OVERWRITE) ? 1 : 0;
   io.delta_in = delta_in;
   io.row_gate = row_gate;
   io.row_dot = row_dot;
@@ -637,10 +644,13 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
                              int64_t stride_dvn, int64_t stride_dvk, int Z, int H, int n_kv_groups, int n_ctx_q,
                              int n_ctx_kv, int n_slots, int block_size_selection, int is_causal, int index_is_int64,
                              int all_invalid_fallback, int head_dim_qk, int head_dim_v, int dtype,
-                             int dq_accumulate, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
+                             int bwd_flags, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream) {
   NSA_BWD_IO
-  io.dq_acc = dq_accumulate ? 1 : 0;
+  if (bwd_flags & ~(NSA_BWD_DQ_ACCUMULATE | NSA_BWD_DKDV_OVERWRITE))
+    return fail(NSA_ERR_INVALID, "bwd_flags=%d has unknown bits", bwd_flags);
+  io.dq_acc = (bwd_flags & NSA_BWD_DQ_ACCUMULATE) ? 1 : 0;
+  io.dkdv_ow = (bwd_flags & NSA_BWD_DKDV_OVERWRITE) ? 1 : 0;
   io.delta_in = delta_in;
   io.row_gate = row_gate;
   io.row_dot = row_dot;

@@ -64,7 +64,7 @@ struct AttnArgs {
   const float* mix_gates;  // [3,B,H,Tq] compact fp32 activated gates (0, 1: mix_o0 / mix_o1, 2: Out)
   const float* lse2;   // [B,H,Tq] compact: (M+L)*log2(e), +inf for empty rows
   const float* delta;  // [B,H,Tq] compact: rowsum(O*dO)
-  // dK/dV destination (accumulated into, any strides) or fp32 partials
+  // dK/dV destination (accumulated into, or overwritten with dkdv_ow; any strides) or fp32 partials
   void* dk;
   int64_t sdk_b, sdk_g, sdk_t, sdk_d;
   void* dv;
@@ -74,6 +74,7 @@ struct AttnArgs {
   int q0;  // absolute position of query row 0 (0 unless a caller decodes past a cache)
   int seg;  // query entries per dK/dV work item
   int direct;  // dK/dV items accumulate into dk / dv themselves (one item per key tile)
+  int dkdv_ow;  // 1: dK / dV are overwritten (every element written) instead of added to
   // shapes
   int B, H, G, hpg, Tq, Tkv;
   float scale;

@@ -431,12 +431,19 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     }
   }
 
-  // ---- direct mode: add this item's dK / dV into the caller's (lane holds
+  // ---- direct mode: add this item's dK / dV into the caller's, or store them (lane holds
   // dK^T[d = 16j + 4*g4 + i][key = mykey]: four consecutive features of one key) ----
   if (a.direct) {
     if (mykey >= a.Tkv) return;
     S* kp = reinterpret_cast<S*>(a.dk) + b * a.sdk_b + grp * a.sdk_g + (int64_t)mykey * a.sdk_t;
     S* vp = reinterpret_cast<S*>(a.dv) + b * a.sdv_b + grp * a.sdv_g + (int64_t)mykey * a.sdv_t;
+    if (a.dkdv_ow) {  // the item owns its keys: store instead of read-modify-write
+#pragma unroll
+      for (int j = 0; j < DK / 16; ++j) set4<T>(kp, (int64_t)(j * 16 + 4 * g4), a.sdk_d, dka[j] * a.scale);
+#pragma unroll
+      for (int j = 0; j < DV / 16; ++j) set4<T>(vp, (int64_t)(j * 16 + 4 * g4), a.sdv_d, dva[j]);
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < DK / 16; ++j) add4<T>(kp, (int64_t)(j * 16 + 4 * g4), a.sdk_d, dka[j] * a.scale);
 #pragma unroll

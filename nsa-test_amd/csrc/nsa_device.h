@@ -264,6 +264,20 @@ __device__ __forceinline__ void add4(typename Store<T>::type* p, int64_t e, int6
   }
 }
 
+// p[(e + u) * sd] = v[u] for u < 4, rounded to T (one vector store when the four
+// elements are contiguous and aligned).
+template <typename T>
+__device__ __forceinline__ void set4(typename Store<T>::type* p, int64_t e, int64_t sd, f32x4 v) {
+  using S = typename Store<T>::type;
+  S* q = p + e * sd;
+  if (sd == 1 && (reinterpret_cast<uintptr_t>(q) % (4 * sizeof(S))) == 0) {
+    store4<T>(q, v);
+  } else {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) q[u * sd] = Elem<T>::from_f32(v[u]);
+  }
+}
+
 // 2^x on the transcendental unit (v_exp_f32); exp2(-inf) = 0.  Inputs here are <= 0,
 // results below the normal range may flush, which the softmax tolerates.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

@@ -13,12 +13,18 @@ namespace nsa {
 
 void launch_repack(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t s_r, int64_t s_c, int B, int G,
                    int R, int C, int Rp, void* rowm, void* colm, void* rowf, void* colf, hipStream_t st);
+// K and V fragment copies of one call (one launch when both suit the fragment kernel);
+// sk / sv: (b, g, row, feature) strides
+void launch_repack_kv(int dtype, const void* k, const int64_t* sk, int dk, void* krf, void* kcf, const void* v,
+                      const int64_t* sv, int dv, void* vrf, void* vcf, int B, int G, int R, int Rp, hipStream_t st);
 
 // return false when (dtype, dk, dv, branch) has no compiled kernel
 bool dispatch_attn_fwd(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
 bool dispatch_attn_bwd_dq(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
 bool dispatch_attn_bwd_dkdv(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
 void launch_partial_reduce(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
+// dK / dV [B, G, Tkv, dk | dv] (a.dk / a.dv, any strides) set to zero
+void launch_zero_dkdv(int dtype, int dk, int dv, const AttnArgs& a, hipStream_t st);
 
 // selection index cleaning and block -> query CSR
 void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g, int64_t si_t, int64_t si_n, int B,

@@ -74,25 +74,43 @@ __global__ __launch_bounds__(256) void repack_kernel(const S* __restrict__ src, 
   }
 }
 
+// One repack of a fragment-layout copy: its source (unit feature stride, 16-byte
+// aligned rows), width and the outputs it fills.
+template <typename S>
+struct RepackJob {
+  const S* src;
+  int64_t s_b, s_g, s_r;
+  int C;
+  S* rowf;
+  S* colf;
+};
+
 // Fragment layouts from a source with unit feature stride and 16-byte aligned rows:
 // a 64 x 64 tile is read as 16-byte pieces into LDS (rows >= R zero), then every
 // output 16-byte piece is written in output order -- a rowfrag piece is EPF
 // consecutive features of one row (one LDS read), a colfrag piece gathers EPF rows of
-// one feature (the C-permuted key order of CFrag for bf16).
+// one feature (the C-permuted key order of CFrag for bf16).  Two jobs share a launch
+// (K and V of one call): column tiles [0, ytiles0) of blockIdx.y are job 0's, the rest
+// job 1's.
 template <typename S>
-__global__ __launch_bounds__(256) void repack_frag_kernel(const S* __restrict__ src, int64_t s_b, int64_t s_g,
-                                                          int64_t s_r, int G, int R, int C, int Rp,
-                                                          S* __restrict__ rowf, S* __restrict__ colf) {
+__global__ __launch_bounds__(256) void repack_frag_kernel(RepackJob<S> j0, RepackJob<S> j1, int ytiles0, int G,
+                                                          int R, int Rp) {
   using T = typename std::conditional<sizeof(S) == 2, bf16, float>::type;
   constexpr int EPF = 16 / sizeof(S);
   constexpr int KC = Elem<T>::kKChunk;
   constexpr int CK = CFrag<T>::kKeys;
   constexpr int P = 64 + EPF;  // LDS row pitch (elements): 16-byte aligned rows
   __shared__ __attribute__((aligned(16))) S tile[64 * P];
+  const bool second = (int)blockIdx.y >= ytiles0;
+  const RepackJob<S>& j = second ? j1 : j0;
+  const int C = j.C;
+  S* __restrict__ rowf = j.rowf;
+  S* __restrict__ colf = j.colf;
   const int bg = blockIdx.z;
   const int b = bg / G, g = bg % G;
-  const int r0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
-  const S* base = src + b * s_b + g * s_g;
+  const int r0 = blockIdx.x * 64, c0 = (second ? blockIdx.y - ytiles0 : blockIdx.y) * 64;
+  const S* base = j.src + b * j.s_b + g * j.s_g;
+  const int64_t s_r = j.s_r;
   const int tid = threadIdx.x;
   constexpr int PPR = 64 / EPF;  // 16-byte pieces per tile row
   for (int q = tid; q < 64 * PPR; q += 256) {
@@ -139,21 +157,28 @@ __global__ __launch_bounds__(256) void repack_frag_kernel(const S* __restrict__ 
   }
 }
 
+// the fragment-only kernel applies: unit feature stride, 16-byte aligned rows
+static bool repack_vec_ok(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t s_r, int64_t s_c, int B,
+                          int G, int R, int C) {
+  const int epf = dtype == kF32 ? 4 : 8;
+  return s_c == 1 && C % epf == 0 && ((uintptr_t)src) % 16 == 0 && (B == 1 || s_b % epf == 0) &&
+         (G == 1 || s_g % epf == 0) && (R <= 1 || s_r % epf == 0);
+}
+
 void launch_repack(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t s_r, int64_t s_c, int B, int G,
                    int R, int C, int Rp, void* rowm, void* colm, void* rowf, void* colf, hipStream_t st) {
   if (!rowm && !colm && !rowf && !colf) return;
   dim3 grid((Rp + 63) / 64, (C + 63) / 64, B * G);
   {
-    const int esz = dtype == kF32 ? 4 : 2, epf = 16 / esz;
-    const bool vec = !rowm && !colm && s_c == 1 && C % epf == 0 && ((uintptr_t)src) % 16 == 0 &&
-                     (B == 1 || s_b % epf == 0) && (G == 1 || s_g % epf == 0) && (R <= 1 || s_r % epf == 0);
+    const bool vec = !rowm && !colm && repack_vec_ok(dtype, src, s_b, s_g, s_r, s_c, B, G, R, C);
     if (vec) {
-      if (dtype == kF32)
-        hipLaunchKernelGGL(repack_frag_kernel<float>, grid, dim3(256), 0, st, (const float*)src, s_b, s_g, s_r, G, R,
-                           C, Rp, (float*)rowf, (float*)colf);
-      else
-        hipLaunchKernelGGL(repack_frag_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, s_b, s_g, s_r,
-                           G, R, C, Rp, (uint16_t*)rowf, (uint16_t*)colf);
+      if (dtype == kF32) {
+        const RepackJob<float> j{(const float*)src, s_b, s_g, s_r, C, (float*)rowf, (float*)colf};
+        hipLaunchKernelGGL(repack_frag_kernel<float>, grid, dim3(256), 0, st, j, j, (int)grid.y, G, R, Rp);
+      } else {
+        const RepackJob<uint16_t> j{(const uint16_t*)src, s_b, s_g, s_r, C, (uint16_t*)rowf, (uint16_t*)colf};
+        hipLaunchKernelGGL(repack_frag_kernel<uint16_t>, grid, dim3(256), 0, st, j, j, (int)grid.y, G, R, Rp);
+      }
       return;
     }
   }
@@ -164,6 +189,30 @@ void launch_repack(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t
     hipLaunchKernelGGL(repack_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, s_b, s_g, s_r, s_c, G,
                        R, C, Rp, (uint16_t*)rowm, (uint16_t*)colm, (uint16_t*)rowf, (uint16_t*)colf);
   }
+}
+
+// The fragment copies of K and V for one call in one launch when both sources suit the
+// fragment-only kernel (column tiles of K first, then V's), else one launch each.
+void launch_repack_kv(int dtype, const void* k, const int64_t* sk, int dk, void* krf, void* kcf, const void* v,
+                      const int64_t* sv, int dv, void* vrf, void* vcf, int B, int G, int R, int Rp, hipStream_t st) {
+  const bool kany = krf || kcf, vany = vrf || vcf;
+  if (kany && vany && repack_vec_ok(dtype, k, sk[0], sk[1], sk[2], sk[3], B, G, R, dk) &&
+      repack_vec_ok(dtype, v, sv[0], sv[1], sv[2], sv[3], B, G, R, dv)) {
+    const int yk = (dk + 63) / 64;
+    const dim3 grid((Rp + 63) / 64, yk + (dv + 63) / 64, B * G);
+    if (dtype == kF32) {
+      const RepackJob<float> jk{(const float*)k, sk[0], sk[1], sk[2], dk, (float*)krf, (float*)kcf};
+      const RepackJob<float> jv{(const float*)v, sv[0], sv[1], sv[2], dv, (float*)vrf, (float*)vcf};
+      hipLaunchKernelGGL(repack_frag_kernel<float>, grid, dim3(256), 0, st, jk, jv, yk, G, R, Rp);
+    } else {
+      const RepackJob<uint16_t> jk{(const uint16_t*)k, sk[0], sk[1], sk[2], dk, (uint16_t*)krf, (uint16_t*)kcf};
+      const RepackJob<uint16_t> jv{(const uint16_t*)v, sv[0], sv[1], sv[2], dv, (uint16_t*)vrf, (uint16_t*)vcf};
+      hipLaunchKernelGGL(repack_frag_kernel<uint16_t>, grid, dim3(256), 0, st, jk, jv, yk, G, R, Rp);
+    }
+    return;
+  }
+  launch_repack(dtype, k, sk[0], sk[1], sk[2], sk[3], B, G, R, dk, Rp, nullptr, nullptr, krf, kcf, st);
+  launch_repack(dtype, v, sv[0], sv[1], sv[2], sv[3], B, G, R, dv, Rp, nullptr, nullptr, vrf, vcf, st);
 }
 
 }  // namespace nsa

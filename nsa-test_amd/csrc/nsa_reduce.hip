@@ -3,7 +3,8 @@
 // Compression and selection split a key tile's queries over several work items;
 // each item wrote fp32 partials [keys][DK + DV].  One workgroup per key tile
 // sums them in item order (fixed, so the result is reproducible) and accumulates
-// into the caller's dK / dV with their strides.
+// into the caller's dK / dV with their strides (or, in overwrite mode, stores the sum:
+// a tile without items then stores zeros).
 #include <algorithm>
 #include "nsa_attn.h"
 #include "nsa_attn_bwd_dkdv.h"
@@ -57,7 +58,7 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
     count = so[j + 1] - so[j];
     step = nsubblk;
   }
-  if (count == 0 || key0 >= key_hi) return;
+  if ((count == 0 && !a.dkdv_ow) || key0 >= key_hi) return;
   const float* base = a.partial + (int64_t)bg * a.items_per_bg * keys * width;
   const int64_t istride = (int64_t)step * keys * width;  // floats between consecutive items
   // blockIdx.z splits the tile's keys x width elements (in groups of four: DK and DV are
@@ -81,9 +82,10 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
       sd = a.sdv_d;
     }
     const bool vec = sd == 1 && (reinterpret_cast<uintptr_t>(p) % (4 * sizeof(S))) == 0;
+    const bool ow = a.dkdv_ow;
     // the destination's current values are requested first (independent of the sum)
     typename Raw4<T>::type old{};
-    if (vec) old = load4_raw<T>(p);
+    if (vec && !ow) old = load4_raw<T>(p);
     // the items' partials in item order (fixed: reproducible), four loads in flight
     const float* src = base + (int64_t)first * keys * width + e;
     float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -108,7 +110,9 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
       sum.w += v.w;
     }
     const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
-    if (vec) {  // one vector read-modify-write
+    if (ow) {
+      set4<T>(p, 0, sd, f32x4{sv[0], sv[1], sv[2], sv[3]});
+    } else if (vec) {  // one vector read-modify-write
       f32x4 w = raw4_f32(old);
 #pragma unroll
       for (int u = 0; u < 4; ++u) w[u] += sv[u];
@@ -118,6 +122,30 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
       for (int u = 0; u < 4; ++u) p[u * sd] = Elem<T>::from_f32(Elem<T>::to_f32(p[u * sd]) + sv[u]);
     }
   }
+}
+
+// Overwrite mode with no query rows: dK / dV [B, G, Tkv, dk | dv] (any strides) set to 0.
+template <typename T>
+__global__ __launch_bounds__(256) void zero_dkdv_kernel(AttnArgs a, int DK, int DV) {
+  using S = typename Store<T>::type;
+  const int bg = blockIdx.y, b = bg / a.G, grp = bg % a.G;
+  const int width = DK + DV;
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= (int64_t)a.Tkv * width) return;
+  const int key = (int)(e / width), col = (int)(e % width);
+  S* p = col < DK ? reinterpret_cast<S*>(a.dk) + b * a.sdk_b + grp * a.sdk_g + (int64_t)key * a.sdk_t +
+                        (int64_t)col * a.sdk_d
+                  : reinterpret_cast<S*>(a.dv) + b * a.sdv_b + grp * a.sdv_g + (int64_t)key * a.sdv_t +
+                        (int64_t)(col - DK) * a.sdv_d;
+  *p = Elem<T>::from_f32(0.f);
+}
+
+void launch_zero_dkdv(int dtype, int dk, int dv, const AttnArgs& a, hipStream_t st) {
+  const int64_t n = (int64_t)a.Tkv * (dk + dv);
+  if (n <= 0 || a.B * a.G <= 0) return;
+  dim3 grid((unsigned)((n + 255) / 256), a.B * a.G);
+  if (dtype == kF32) hipLaunchKernelGGL(zero_dkdv_kernel<float>, grid, dim3(256), 0, st, a, dk, dv);
+  else hipLaunchKernelGGL(zero_dkdv_kernel<bf16>, grid, dim3(256), 0, st, a, dk, dv);
 }
 
 void launch_partial_reduce(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st) {

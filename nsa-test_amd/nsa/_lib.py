@@ -12,7 +12,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libnsa_hip.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 NSA_F32 = 0
 NSA_BF16 = 1
@@ -48,7 +48,7 @@ SIGNATURES = {
 }
 # the allocation-free sliding-window forward: no workspace arguments
 SIGNATURES["nsa_sliding_window_fwd_noalloc"] = (_I, SIGNATURES["nsa_sliding_window_fwd"][1][:-3] + [_P])
-# the backward extensions: dq_accumulate (int), delta_in, row_gate, row_dot (pointers)
+# the backward extensions: bwd_flags (int), delta_in, row_gate, row_dot (pointers)
 # before the workspace
 for _n in ("nsa_sliding_window_bwd", "nsa_compression_bwd", "nsa_sparse_selection_bwd"):
     _r, _a = SIGNATURES[_n]

@@ -19,6 +19,8 @@ import torch.nn.functional as F
 from . import _lib
 
 SLIDING, COMPRESSION, SELECTION = 0, 1, 2
+# bwd_flags bits of the backward extension entry points (include/nsa_hip.h)
+BWD_DQ_ACCUMULATE, BWD_DKDV_OVERWRITE = 1, 2
 HEAD_DIM_PAIRS = ((32, 32), (64, 64), (128, 128), (192, 128))
 
 
@@ -149,10 +151,11 @@ def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=
 
 def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0, block_ends=None, indices=None,
              lprime: int = 64, causal: bool = True, fallback: bool = False, dq=None, dk=None, dv=None,
-             dq_accumulate: bool = False, delta=None, row_gate=None, row_dot=None):
+             dq_accumulate: bool = False, delta=None, row_gate=None, row_dot=None, dkdv_overwrite: bool = False):
     """Backward of one NSA branch.  dq is overwritten (added to when dq_accumulate, which
-    needs dq), dk / dv ([Z,G,Tkv,*] logical views) are accumulated into (allocated
-    zeroed when not given).  delta: optional precomputed row sums sum_d o * do [Z,H,Tq]
+    needs dq), dk / dv ([Z,G,Tkv,*] logical views) are accumulated into, or overwritten
+    when dkdv_overwrite (allocated when not given: the kernels then write every element,
+    so no zero fill is needed).  delta: optional precomputed row sums sum_d o * do [Z,H,Tq]
     (fp32), used instead of reading o.  row_gate: optional fp32 contiguous [Z,H,Tq]; the
     branch's output gradient is then row_gate * do.  row_dot: optional fp32 contiguous
     [Z,H,Tq] that receives sum_d do * o per row.  Returns (dq, dk, dv)."""
@@ -181,8 +184,11 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     dqk = dq if direct_dq else torch.empty(Z, H, Tq, DK, device=dev, dtype=cdt)
     direct_dk = dk is not None and dk.dtype == cdt and dkw == DK
     direct_dv = dv is not None and dv.dtype == cdt and dvw == DV
-    dkk = dk if direct_dk else torch.zeros(Z, G, Tkv, DK, device=dev, dtype=cdt)
-    dvk = dv if direct_dv else torch.zeros(Z, G, Tkv, DV, device=dev, dtype=cdt)
+    # overwrite mode when the caller asks for it or both buffers are this call's own
+    ow = bool(dkdv_overwrite) or (not direct_dk and not direct_dv)
+    alloc = torch.empty if ow else torch.zeros
+    dkk = dk if direct_dk else alloc(Z, G, Tkv, DK, device=dev, dtype=cdt)
+    dvk = dv if direct_dv else alloc(Z, G, Tkv, DV, device=dev, dtype=cdt)
     n_slots = indices.shape[-1] if branch == SELECTION else 0
     ws_bytes = _lib.size("nsa_bwd_workspace_size", branch, _dtype_code(cdt), Z, H, G, Tq, Tkv, DK, DV, n_slots,
                          lprime, int(window) if branch == SLIDING else 1)
@@ -199,8 +205,9 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     for t in (row_gate, row_dot):
         if t is not None and (t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != (Z, H, Tq)):
             raise ValueError(f"row_gate / row_dot must be contiguous fp32 [{Z}, {H}, {Tq}]")
-    if acc or dl is not None or row_gate is not None or row_dot is not None:
-        sfx, tail = "_ex", (int(acc), _ptr(dl), _ptr(row_gate), _ptr(row_dot), _ptr(ws), ws.numel(), st)
+    if acc or ow or dl is not None or row_gate is not None or row_dot is not None:
+        flags = (BWD_DQ_ACCUMULATE if acc else 0) | (BWD_DKDV_OVERWRITE if ow else 0)
+        sfx, tail = "_ex", (flags, _ptr(dl), _ptr(row_gate), _ptr(row_dot), _ptr(ws), ws.numel(), st)
     else:
         sfx, tail = "", (_ptr(ws), ws.numel(), st)
     if branch == SLIDING:
@@ -229,13 +236,13 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     if not direct_dk:
         r = dkk[..., :dkw]
         if dk is not None:
-            dk.add_(r.to(dk.dtype))
+            dk.copy_(r) if dkdv_overwrite else dk.add_(r.to(dk.dtype))
         else:
             dk = r if q.dtype == cdt else r.to(q.dtype)
     if not direct_dv:
         r = dvk[..., :dvw]
         if dv is not None:
-            dv.add_(r.to(dv.dtype))
+            dv.copy_(r) if dkdv_overwrite else dv.add_(r.to(dv.dtype))
         else:
             dv = r if q.dtype == cdt else r.to(q.dtype)
     return dq, dk, dv

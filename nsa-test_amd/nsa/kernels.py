@@ -352,6 +352,17 @@ class NSACore(torch.autograd.Function):
                 dkw.transpose(-1, -2), dvw, dg.to(ctx.gdtype), None, None)
 
 
+@functools.lru_cache(maxsize=32)
+def _block_ends(n_pad: int, n_act: int, d: int, l: int, device) -> torch.Tensor:
+    """block_ends [n_pad] int32: block i ends at token i*d + l - 1 for i < n_act, the
+    padding blocks at 999999 (never visible).  Built once per shape and device: the
+    per-step rebuild was five small launches."""
+    be = torch.full((n_pad,), 999999, device=device, dtype=torch.int32)
+    if n_act > 0:
+        be[:n_act] = torch.arange(n_act, device=device, dtype=torch.int32) * d + (l - 1)
+    return be
+
+
 def _gate_activation(z, act):
     """Gates from the gate input z [..., 3] (fp32): z itself, sigmoid(z) or softmax over
     the three (reference nsa/kernels.py:2436-2440)."""
@@ -655,7 +666,9 @@ class NSAAttention(torch.nn.Module):
                         ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, int]:
         """keys [B,G,T,dk], values [B,G,T,dv] -> (K_cmp [B,G,dk,Np], V_cmp [B,G,Np,dv],
         block_ends [Np] int32, n_actual) with Np the power-of-two padded block count
-        (padding: zero keys/values, block_ends 999999), as nsa/kernels.py:2119-2208."""
+        (padding: zero keys/values, block_ends 999999), as nsa/kernels.py:2119-2208.
+        block_ends depends only on (Np, n_actual, d, l) and is a shared cached tensor:
+        treat it as read-only."""
         c = self.config
         B, G, T, dk = keys.shape
         dv = values.shape[-1]
@@ -664,11 +677,10 @@ class NSAAttention(torch.nn.Module):
         while n_pad < n_act:
             n_pad *= 2
         dev, dt = keys.device, keys.dtype
-        block_ends = torch.full((n_pad,), 999999, device=dev, dtype=torch.int32)
+        block_ends = _block_ends(n_pad, n_act, c.d, c.l, dev)
         if n_act <= 0:
             return (torch.zeros(B, G, dk, n_pad, device=dev, dtype=dt), torch.zeros(B, G, n_pad, dv, device=dev, dtype=dt),
                     block_ends, n_act)
-        block_ends[:n_act] = torch.arange(n_act, device=dev, dtype=torch.int32) * c.d + (c.l - 1)
         l1, l2 = self.compress_mlp[0], self.compress_mlp[2]
         W1k, W1p = l1.weight[:, :dk], l1.weight[:, dk:]
         Y = _LinearSplitK.apply(keys, W1k.to(dt), None)                          # [B,G,T,2dk]

@@ -139,6 +139,54 @@ def test_selection_parity(dev, B, H, G, T, dk, dv, lp, n, dtype):
     _check(_ops.SELECTION, q, kp, v, do, 1 / math.sqrt(dk), dtype, indices=idx.to(dev), lprime=lp)
 
 
+OVERWRITE_CASES = [
+    # kind, B, H, G, Tq, Tkv, d, extra
+    ("sliding_direct", 64, 8, 4, 256, 256, 64, dict(window=100)),  # items store their own keys
+    ("sliding", 1, 8, 2, 700, 700, 64, dict(window=512)),          # partials + reduce
+    ("compression", 1, 8, 2, 400, 32, 64, {}),
+    ("selection", 1, 8, 2, 512, 512, 64, dict(lprime=64)),         # blocks 4.. never selected
+    ("compression_empty", 1, 4, 2, 0, 16, 64, {}),                 # no query rows
+]
+
+
+@pytest.mark.parametrize("case,B,H,G,Tq,Tkv,d,extra", OVERWRITE_CASES)
+def test_dkdv_overwrite_matches_accumulate(dev, case, B, H, G, Tq, Tkv, d, extra):
+    """The backward extensions' dK/dV overwrite bit (bwd_flags NSA_BWD_DKDV_OVERWRITE):
+    caller buffers pre-filled with garbage are overwritten with exactly the gradients of
+    the default call, and without the bit a buffer of ones receives exactly 1 + those
+    gradients (fp32: the kernels add the same fp32 sums).  Covers the sliding direct
+    mode, the reduce pass (including selection tiles no row selected, which must be
+    written as zeros) and a launch with no query rows."""
+    kind = {"sliding": _ops.SLIDING, "compression": _ops.COMPRESSION, "selection": _ops.SELECTION}[case.split("_")[0]]
+    dtype = torch.float32
+    kw = dict(extra)
+    q, kp, v, do = _make(11, B, H, G, Tq, Tkv, d, d, dtype, dev)
+    if kind == _ops.COMPRESSION:
+        be = torch.full((Tkv,), 999999, dtype=torch.int32)
+        n_act = Tkv - 4  # four padding blocks that no row sees
+        be[:n_act] = torch.arange(n_act, dtype=torch.int32) * 16 + 31
+        kw["block_ends"] = be.to(dev)
+    if kind == _ops.SELECTION:
+        kw["indices"] = _random_indices(5, B, G, Tq, 4 * 64, 64, 3, p_empty=0.0).to(dev)
+    k = kp.transpose(-1, -2)
+    print(f"[overwrite] {case} B={B} H={H} G={G} Tq={Tq} Tkv={Tkv}", flush=True)
+    out, L, M = _ops.attn_fwd(kind, q, k, v, 1 / math.sqrt(d), **kw)
+    _, gk, gv = _ops.attn_bwd(kind, q, k, v, out, do, L, M, 1 / math.sqrt(d), **kw)
+    dk1 = torch.full((B, G, Tkv, d), 7.0, device=dev)
+    dv1 = torch.full((B, G, Tkv, d), -3.0, device=dev)
+    _ops.attn_bwd(kind, q, k, v, out, do, L, M, 1 / math.sqrt(d), dk=dk1, dv=dv1, dkdv_overwrite=True, **kw)
+    dk2 = torch.ones(B, G, Tkv, d, device=dev)
+    dv2 = torch.ones(B, G, Tkv, d, device=dev)
+    _ops.attn_bwd(kind, q, k, v, out, do, L, M, 1 / math.sqrt(d), dk=dk2, dv=dv2, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(dk1, gk) and torch.equal(dv1, gv)
+    assert torch.equal(dk2, 1 + gk) and torch.equal(dv2, 1 + gv)
+    if kind == _ops.SELECTION:  # keys of blocks no row selected
+        assert torch.count_nonzero(gk[:, :, 4 * 64:]) == 0 and torch.count_nonzero(gv[:, :, 4 * 64:]) == 0
+    if Tq == 0:
+        assert torch.count_nonzero(gk) == 0 and torch.count_nonzero(gv) == 0
+
+
 def test_selection_int32_indices_and_noncausal(dev):
     B, H, G, T, d, lp = 1, 4, 2, 128, 32, 32
     q, kp, v, do = _make(5, B, H, G, T, T, d, d, torch.float32, dev)

@@ -131,6 +131,14 @@ def test_error_codes_without_gpu_work():
     rc = lib.nsa_sliding_window_fwd(*([None] * 4), 1.0, None, None, *([0] * 22), 1, 1, 1, 8, 4, 48, 48,
                                     _lib.NSA_F32, None, 0, None)
     assert rc == _lib.NSA_ERR_UNSUPPORTED and b"head dims" in lib.nsa_last_error()
+    # the backward extensions reject unknown bwd_flags bits before any other work
+    import ctypes
+    argt = _lib.SIGNATURES["nsa_sliding_window_bwd_ex"][1]
+    args = [1.0 if t is ctypes.c_float else (None if t in (ctypes.c_void_p,) or hasattr(t, "contents") else 0)
+            for t in argt]
+    args[len(argt) - 7] = _ops.BWD_DQ_ACCUMULATE | _ops.BWD_DKDV_OVERWRITE | 4
+    rc = lib.nsa_sliding_window_bwd_ex(*args)
+    assert rc == _lib.NSA_ERR_INVALID and b"bwd_flags" in lib.nsa_last_error()
     assert _ops.kernel_dims(48, 48) == (64, 64) and _ops.kernel_dims(192, 128) == (192, 128)
     with pytest.raises(ValueError):
         _ops.kernel_dims(512, 64)
