@@ -363,6 +363,18 @@ int nsa_gate_mix_bwd(const void* dout, int64_t sd_b, int64_t sd_h, int64_t sd_t,
                      void* do_sel, void* do_win, float* dgates, float* delta, int B, int H, int T, int dv,
                      int gate_act, int dtype, nsa_stream_t stream);
 
+/* The gate activation alone, for the fused path whose mix runs in the sliding-window
+ * forward's epilogue and whose branch backwards write the row dots (the reference
+ * applies it inline, nsa/kernels.py:2436-2440).  gate_act as above.  Forward: gates
+ * (contiguous fp32 [3,B,H,T]) = act(gate_in), gate_in [B,H,T,3] in dtype with strides
+ * sz_*.  Backward: from the gates and row_dots r_k = sum_d dout . o_k (both contiguous
+ * fp32 [3,B,H,T]), dgate_in (dtype, strides sz_*) receives the gradient of the gate
+ * input: r_k (0), r_k g_k (1 - g_k) (1), g_k (r_k - sum_j g_j r_j) (2). */
+int nsa_gate_act_fwd(const void* gate_in, int64_t sz_b, int64_t sz_h, int64_t sz_t, int64_t sz_k, float* gates, int B,
+                     int H, int T, int gate_act, int dtype, nsa_stream_t stream);
+int nsa_gate_act_bwd(const float* gates, const float* row_dots, void* dgate_in, int64_t sz_b, int64_t sz_h,
+                     int64_t sz_t, int64_t sz_k, int B, int H, int T, int gate_act, int dtype, nsa_stream_t stream);
+
 /* ---- compression pooling (compress_tokens, nsa/kernels.py:2119-2208) --------
  * With the first MLP layer split as W1 = [W1k | W1p]:  Y = k W1k^T  [Z,G,T,width],
  * C = E W1p^T + b1  [l,width].  Forward writes R[i] = mean_{u<l} relu(Y[d*i+u] + C[u])

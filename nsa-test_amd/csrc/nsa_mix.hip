@@ -63,6 +63,37 @@ __device__ __forceinline__ uint4 pack_piece(const float* f) {
   }
 }
 
+// the gates g_k = act(z_k) of one row: z (none), sigmoid, or softmax over the three
+__device__ __forceinline__ void gate_act3(int act, float& g0, float& g1, float& g2) {
+  if (act == 1) {
+    g0 = 1.f / (1.f + __expf(-g0));
+    g1 = 1.f / (1.f + __expf(-g1));
+    g2 = 1.f / (1.f + __expf(-g2));
+  } else if (act == 2) {
+    const float m = fmaxf(g0, fmaxf(g1, g2));
+    const float e0 = __expf(g0 - m), e1 = __expf(g1 - m), e2 = __expf(g2 - m);
+    const float inv = 1.f / (e0 + e1 + e2);
+    g0 = e0 * inv;
+    g1 = e1 * inv;
+    g2 = e2 * inv;
+  }
+}
+
+// gradient of the gate input z from the gates g and dg_k = d loss / d g_k (in place on dg)
+__device__ __forceinline__ void gate_act3_grad(int act, float g0, float g1, float g2, float& d0, float& d1,
+                                               float& d2) {
+  if (act == 1) {
+    d0 = d0 * g0 * (1.f - g0);
+    d1 = d1 * g1 * (1.f - g1);
+    d2 = d2 * g2 * (1.f - g2);
+  } else if (act == 2) {
+    const float s = g0 * d0 + g1 * d1 + g2 * d2;
+    d0 = g0 * (d0 - s);
+    d1 = g1 * (d1 - s);
+    d2 = g2 * (d2 - s);
+  }
+}
+
 template <typename S, bool BWD>
 __global__ __launch_bounds__(256) void gate_mix_kernel(MixArgs a, int lpr_log2) {
   constexpr int EPF = 16 / sizeof(S);
@@ -79,18 +110,7 @@ __global__ __launch_bounds__(256) void gate_mix_kernel(MixArgs a, int lpr_log2) 
   const int64_t xoff = b * a.sx_b + h * a.sx_h + (int64_t)t * a.sx_t;
   const S* gp = reinterpret_cast<const S*>(a.g) + b * a.sg_b + h * a.sg_h + (int64_t)t * a.sg_t;
   float g0 = ld1<S>(gp), g1 = ld1<S>(gp + a.sg_k), g2 = ld1<S>(gp + 2 * a.sg_k);
-  if (a.act == 1) {
-    g0 = 1.f / (1.f + __expf(-g0));
-    g1 = 1.f / (1.f + __expf(-g1));
-    g2 = 1.f / (1.f + __expf(-g2));
-  } else if (a.act == 2) {
-    const float m = fmaxf(g0, fmaxf(g1, g2));
-    const float e0 = __expf(g0 - m), e1 = __expf(g1 - m), e2 = __expf(g2 - m);
-    const float inv = 1.f / (e0 + e1 + e2);
-    g0 = e0 * inv;
-    g1 = e1 * inv;
-    g2 = e2 * inv;
-  }
+  gate_act3(a.act, g0, g1, g2);
   float dg0 = 0.f, dg1 = 0.f, dg2 = 0.f;
   for (int e = sub * EPF; e < a.dv; e += lpr * EPF) {
     float o0[EPF], o1[EPF], o2[EPF];
@@ -135,21 +155,69 @@ __global__ __launch_bounds__(256) void gate_mix_kernel(MixArgs a, int lpr_log2) 
         a.delta[2 * nrows + rr] = g2 * dg2;
       }
       float z0 = dg0, z1 = dg1, z2 = dg2;  // gradient of the gate input
-      if (a.act == 1) {
-        z0 = dg0 * g0 * (1.f - g0);
-        z1 = dg1 * g1 * (1.f - g1);
-        z2 = dg2 * g2 * (1.f - g2);
-      } else if (a.act == 2) {
-        const float s = g0 * dg0 + g1 * dg1 + g2 * dg2;
-        z0 = g0 * (dg0 - s);
-        z1 = g1 * (dg1 - s);
-        z2 = g2 * (dg2 - s);
-      }
+      gate_act3_grad(a.act, g0, g1, g2, z0, z1, z2);
       a.dg[rr * 3 + 0] = z0;
       a.dg[rr * 3 + 1] = z1;
       a.dg[rr * 3 + 2] = z2;
     }
   }
+}
+
+// Gate activation alone (the fused mix path, whose mix runs in the sliding-window
+// epilogue): forward z [B,H,T,3] (any strides, fp32 / bf16) -> g [3][B*H*T] fp32;
+// backward g and r_k = sum_d dout . o_k ([3][B*H*T] fp32) -> dz [B,H,T,3] (any strides,
+// fp32 / bf16).  One thread per (b, h, t) row.
+template <typename S, bool BWD>
+__global__ __launch_bounds__(256) void gate_act_kernel(const void* zin, float* g, const float* r, void* dz,
+                                                       int64_t s_b, int64_t s_h, int64_t s_t, int64_t s_k, int H,
+                                                       int T, int64_t nrows, int act) {
+  const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (row >= nrows) return;
+  const int t = row % T;
+  const int h = (row / T) % H;
+  const int64_t b = row / ((int64_t)T * H);
+  const int64_t off = b * s_b + h * s_h + (int64_t)t * s_t;
+  if constexpr (!BWD) {
+    const S* zp = reinterpret_cast<const S*>(zin) + off;
+    float g0 = ld1<S>(zp), g1 = ld1<S>(zp + s_k), g2 = ld1<S>(zp + 2 * s_k);
+    gate_act3(act, g0, g1, g2);
+    g[row] = g0;
+    g[nrows + row] = g1;
+    g[2 * nrows + row] = g2;
+  } else {
+    const float g0 = g[row], g1 = g[nrows + row], g2 = g[2 * nrows + row];
+    float d0 = r[row], d1 = r[nrows + row], d2 = r[2 * nrows + row];
+    gate_act3_grad(act, g0, g1, g2, d0, d1, d2);
+    S* zp = reinterpret_cast<S*>(dz) + off;
+    if constexpr (sizeof(S) == 4) {
+      zp[0] = d0;
+      zp[s_k] = d1;
+      zp[2 * s_k] = d2;
+    } else {
+      zp[0] = f32_to_bf16_bits(d0);
+      zp[s_k] = f32_to_bf16_bits(d1);
+      zp[2 * s_k] = f32_to_bf16_bits(d2);
+    }
+  }
+}
+
+template <bool BWD>
+static int launch_gate_act(int dtype, const void* z, float* g, const float* r, void* dz, int64_t s_b, int64_t s_h,
+                           int64_t s_t, int64_t s_k, int B, int H, int T, int act, hipStream_t st) {
+  if (dtype != NSA_F32 && dtype != NSA_BF16) return set_error(NSA_ERR_INVALID, "dtype not supported");
+  if (B < 0 || H < 0 || T < 0) return set_error(NSA_ERR_INVALID, "bad shape");
+  if (act < 0 || act > 2) return set_error(NSA_ERR_INVALID, "gate_act must be 0, 1 or 2");
+  const int64_t nrows = (int64_t)B * H * T;
+  if (nrows == 0) return NSA_OK;
+  const dim3 grid((unsigned)((nrows + 255) / 256));
+  if (dtype == NSA_F32)
+    hipLaunchKernelGGL((gate_act_kernel<float, BWD>), grid, dim3(256), 0, st, z, g, r, dz, s_b, s_h, s_t, s_k, H, T,
+                       nrows, act);
+  else
+    hipLaunchKernelGGL((gate_act_kernel<uint16_t, BWD>), grid, dim3(256), 0, st, z, g, r, dz, s_b, s_h, s_t, s_k, H,
+                       T, nrows, act);
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NSA_OK : set_error(NSA_ERR_HIP, hipGetErrorString(e));
 }
 
 template <bool BWD>
@@ -255,4 +323,17 @@ extern "C" int nsa_gate_mix_bwd(const void* dout, int64_t sd_b, int64_t sd_h, in
   a.T = T;
   a.dv = dv;
   return launch_mix<true>(dtype, a, (hipStream_t)stream);
+}
+
+extern "C" int nsa_gate_act_fwd(const void* gate_in, int64_t sz_b, int64_t sz_h, int64_t sz_t, int64_t sz_k,
+                                float* gates, int B, int H, int T, int gate_act, int dtype, nsa_stream_t stream) {
+  return nsa::launch_gate_act<false>(dtype, gate_in, gates, nullptr, nullptr, sz_b, sz_h, sz_t, sz_k, B, H, T,
+                                     gate_act, (hipStream_t)stream);
+}
+
+extern "C" int nsa_gate_act_bwd(const float* gates, const float* row_dots, void* dgate_in, int64_t sz_b, int64_t sz_h,
+                                int64_t sz_t, int64_t sz_k, int B, int H, int T, int gate_act, int dtype,
+                                nsa_stream_t stream) {
+  return nsa::launch_gate_act<true>(dtype, nullptr, const_cast<float*>(gates), row_dots, dgate_in, sz_b, sz_h, sz_t,
+                                    sz_k, B, H, T, gate_act, (hipStream_t)stream);
 }

@@ -300,7 +300,7 @@ class NSACore(torch.autograd.Function):
                 return torch.empty(B, T, H, dv, device=q.device, dtype=cdt).permute(0, 2, 1, 3)
 
             o_c, o_s, o_w, out = bthd(), bthd(), bthd(), bthd()
-            gates = _gate_activation(gate_logits.float(), act).permute(3, 0, 1, 2).contiguous()  # [3,B,H,T]
+            gates = _gate_activation(gate_logits, act)  # [3,B,H,T] fp32
             _, Lc, Mc = _ops.attn_fwd(COMPRESSION, q, _kt(k_compressed), v_compressed, scale, block_ends=block_ends,
                                       out=o_c)
             _, Ls, Ms = _ops.attn_fwd(SELECTION, q, _kt(k_sel), v_sel, scale, indices=indices, lprime=lp,
@@ -339,7 +339,7 @@ class NSACore(torch.autograd.Function):
                                         row_dot=rdot[1])
             _, dkw, dvw = _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, d, Lw, Mw, sc, window=ctx.window, dq=dq,
                                         dq_accumulate=True, row_gate=g[2], row_dot=rdot[2])
-            dg = _gate_activation_grad(g, rdot, ctx.act).permute(1, 2, 3, 0)
+            dg = _gate_activation_grad(g, rdot, ctx.act, ctx.gdtype)
         else:
             dos, dg, deltas = _mix_bwd(dout, [o_c, o_s, o_w], g, want_delta=True, act=ctx.act)
             _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, dos[0], Lc, Mc, sc, block_ends=be, dq=dq,
@@ -349,7 +349,7 @@ class NSACore(torch.autograd.Function):
             _, dkw, dvw = _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, dos[2], Lw, Mw, sc, window=ctx.window, dq=dq,
                                         dq_accumulate=True, delta=deltas[2])
         return (dq.to(q.dtype), dkc.transpose(-1, -2), dvc, None, dks.transpose(-1, -2), dvs, None,
-                dkw.transpose(-1, -2), dvw, dg.to(ctx.gdtype), None, None)
+                dkw.transpose(-1, -2), dvw, dg if dg.dtype == ctx.gdtype else dg.to(ctx.gdtype), None, None)
 
 
 @functools.lru_cache(maxsize=32)
@@ -364,23 +364,28 @@ def _block_ends(n_pad: int, n_act: int, d: int, l: int, device) -> torch.Tensor:
 
 
 def _gate_activation(z, act):
-    """Gates from the gate input z [..., 3] (fp32): z itself, sigmoid(z) or softmax over
-    the three (reference nsa/kernels.py:2436-2440)."""
-    if act == 1:
-        return torch.sigmoid(z)
-    if act == 2:
-        return torch.softmax(z, dim=-1)
-    return z
+    """Gates [3,B,H,T] fp32 from the gate input z [B,H,T,3] (any strides): z itself,
+    sigmoid(z) or softmax over the three (reference nsa/kernels.py:2436-2440), one HIP
+    pass (nsa_gate_act_fwd)."""
+    B, H, T, _ = z.shape
+    if z.dtype not in (torch.float32, torch.bfloat16):
+        z = z.float()
+    g = torch.empty(3, B, H, T, device=z.device, dtype=torch.float32)
+    _lib.call("nsa_gate_act_fwd", _ops._ptr(z), *z.stride(), _ops._ptr(g), B, H, T, act, _ops._dtype_code(z.dtype),
+              _ops._stream(z.device))
+    return g
 
 
-def _gate_activation_grad(a, r, act):
-    """Gradient of the gate input from the gates a and r_k = sum_d dout . o_k (both
-    [3, ...] fp32): r (identity), r a (1 - a) (sigmoid), a (r - sum_j a_j r_j) (softmax)."""
-    if act == 1:
-        return r * a * (1 - a)
-    if act == 2:
-        return a * (r - (a * r).sum(0, keepdim=True))
-    return r
+def _gate_activation_grad(a, r, act, dtype):
+    """Gradient [B,H,T,3] of the gate input from the gates a and r_k = sum_d dout . o_k
+    (both [3,B,H,T] fp32): r (identity), r a (1 - a) (sigmoid), a (r - sum_j a_j r_j)
+    (softmax); one HIP pass (nsa_gate_act_bwd), in dtype when fp32 / bf16, else fp32."""
+    _, B, H, T = a.shape
+    dt = dtype if dtype in (torch.float32, torch.bfloat16) else torch.float32
+    dz = torch.empty(B, H, T, 3, device=a.device, dtype=dt)
+    _lib.call("nsa_gate_act_bwd", _ops._ptr(a), _ops._ptr(r), _ops._ptr(dz), *dz.stride(), B, H, T, act,
+              _ops._dtype_code(dt), _ops._stream(a.device))
+    return dz
 
 
 class _LinearSplitK(torch.autograd.Function):

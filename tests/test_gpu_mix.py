@@ -41,3 +41,29 @@ def test_gated_mix_matches_formula(dev, B, H, T, dv, dtype):
     assert rel_err(out.double(), ref) < tol
     for got, want in zip([t.grad for t in os_] + [g.grad], [t.grad for t in r] + [rg.grad]):
         assert rel_err(got.double(), want) < tol
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gate_activation_matches_torch(dev, act, dtype):
+    """nsa_gate_act_fwd / _bwd (the fused path's gate activation and its gradient)
+    against the torch fp32 formulas: the gate input is the module's [B,H,T,3] view of
+    [B,T,H,3] storage; gates fp32 [3,B,H,T]; the input gradient in the input's dtype."""
+    from nsa.kernels import _gate_activation, _gate_activation_grad
+    B, H, T = 2, 5, 37
+    g = torch.Generator().manual_seed(act)
+    z = (torch.randn(B, T, H, 3, generator=g) * 3).to(dtype).to(dev).permute(0, 2, 1, 3)
+    r = torch.randn(3, B, H, T, generator=g).to(dev)
+    a = _gate_activation(z, act)
+    dz = _gate_activation_grad(a, r, act, dtype)
+    torch.cuda.synchronize()
+    zf = z.double()
+    ref = zf if act == 0 else torch.sigmoid(zf) if act == 1 else torch.softmax(zf, dim=-1)
+    ref = ref.permute(3, 0, 1, 2)
+    assert a.shape == (3, B, H, T) and a.dtype == torch.float32 and a.is_contiguous()
+    assert (a.double() - ref).abs().max().item() < 2e-6
+    ad, rd = a.double(), r.double()
+    gref = rd if act == 0 else rd * ad * (1 - ad) if act == 1 else ad * (rd - (ad * rd).sum(0, keepdim=True))
+    gref = gref.permute(1, 2, 3, 0)
+    assert dz.shape == (B, H, T, 3) and dz.dtype == dtype
+    assert _rel(dz.double().cpu().numpy(), gref.cpu().numpy()) < (1e-6 if dtype == torch.float32 else 1e-2)
