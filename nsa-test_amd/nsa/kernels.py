@@ -424,6 +424,28 @@ class _LinearSplitK(torch.autograd.Function):
         return dx, dW, db
 
 
+class _SplitCols(torch.autograd.Function):
+    """(W[:, :k], W[:, k:]) whose backward writes W's gradient as one concatenation of
+    the two parts' gradients (two slicing backwards would zero-fill and copy each part
+    into its own full-size gradient, then add the two)."""
+
+    @staticmethod
+    def forward(ctx, W, k):
+        ctx.k, ctx.n = k, W.shape[1]
+        return W[:, :k], W[:, k:]
+
+    @staticmethod
+    def backward(ctx, g1, g2):
+        if g1 is None and g2 is None:
+            return None, None
+        ref = g1 if g1 is not None else g2
+        if g1 is None:
+            g1 = ref.new_zeros(ref.shape[0], ctx.k)
+        if g2 is None:
+            g2 = ref.new_zeros(ref.shape[0], ctx.n - ctx.k)
+        return torch.cat([g1, g2], dim=1), None
+
+
 class _CompressPool(torch.autograd.Function):
     """R[i] = mean_u relu(Y[d*i+u] + C[u]),  V_cmp[i] = mean_u v[d*i+u]  (HIP)."""
 
@@ -687,7 +709,7 @@ class NSAAttention(torch.nn.Module):
             return (torch.zeros(B, G, dk, n_pad, device=dev, dtype=dt), torch.zeros(B, G, n_pad, dv, device=dev, dtype=dt),
                     block_ends, n_act)
         l1, l2 = self.compress_mlp[0], self.compress_mlp[2]
-        W1k, W1p = l1.weight[:, :dk], l1.weight[:, dk:]
+        W1k, W1p = _SplitCols.apply(l1.weight, dk)
         Y = _LinearSplitK.apply(keys, W1k.to(dt), None)                          # [B,G,T,2dk]
         C = F.linear(self.pos_embed.weight.to(dt), W1p.to(dt),
                      l1.bias.to(dt) if l1.bias is not None else None)             # [l,2dk]

@@ -173,3 +173,16 @@ def test_launcher_rejects_out_of_storage_strides():
             q, k, v, out, 0.1, L, L, *q.stride(), *k.stride(), *v.stride(), *out.stride(), *L.stride(), *L.stride(),
             Z=1, H=2, N_KV_GROUPS=2, N_CTX=64, WINDOW_SIZE=16, HEAD_DIM_QK=32, HEAD_DIM_V=32, BLOCK_M=32,
             BLOCK_N=32)
+
+
+def test_split_cols_gradient():
+    """compress_tokens splits the first MLP weight into its key and position columns
+    with one autograd function whose backward concatenates the two gradients: checked
+    against finite differences, and with one part unused (its columns get zeros)."""
+    from nsa.kernels import _SplitCols
+    W = torch.randn(5, 9, dtype=torch.float64, requires_grad=True)
+    assert torch.autograd.gradcheck(lambda w: _SplitCols.apply(w, 3), (W,))
+    a, b = _SplitCols.apply(W, 3)
+    (a * a).sum().backward()
+    assert torch.equal(W.grad[:, 3:], torch.zeros(5, 6, dtype=torch.float64))
+    assert torch.allclose(W.grad[:, :3], 2 * W.detach()[:, :3])
