@@ -13,7 +13,7 @@
 
 namespace nsa {
 
-constexpr int kReduceSplit = 10;
+constexpr int kReduceSplit = 20;
 
 bool dispatch_attn_fwd_f32(int, int, int, const AttnArgs&, hipStream_t);
 bool dispatch_attn_fwd_bf16(int, int, int, const AttnArgs&, hipStream_t);
@@ -90,6 +90,18 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
     const float* src = base + (int64_t)first * keys * width + e;
     float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
     int k = 0;
+    for (; k + 8 <= count; k += 8) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4*>(src + (k + u) * istride);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        sum.x += v[u].x;
+        sum.y += v[u].y;
+        sum.z += v[u].z;
+        sum.w += v[u].w;
+      }
+    }
     for (; k + 4 <= count; k += 4) {
       float4 v[4];
 #pragma unroll
