@@ -86,7 +86,7 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
     // the destination's current values are requested first (independent of the sum)
     typename Raw4<T>::type old{};
     if (vec && !ow) old = load4_raw<T>(p);
-    // the items' partials in item order (fixed: reproducible), four loads in flight
+    // the items' partials in item order (fixed: reproducible), eight (then four) loads in flight
     const float* src = base + (int64_t)first * keys * width + e;
     float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
     int k = 0;
