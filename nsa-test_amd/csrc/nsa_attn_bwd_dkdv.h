@@ -224,10 +224,20 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     return BR == kSelection ? s_tl[e - e_base] : e;
   };
 
-  // ---- register prefetch of one chunk (pairs of adjacent rows) ----
-  uint4 pq[NQ][2], po[NO][2];
-  int pr_t = -1;
-  float pr_l2 = INFINITY, pr_dl = 0.f, pr_g = 1.f;
+  // ---- register prefetch of row chunks (pairs of adjacent rows): bf16 keeps two chunks
+  // in flight (chunk c + 2 is requested into the registers chunk c was just staged from),
+  // fp32 one ----
+  struct Stage {
+    uint4 pq[NQ][2], po[NO][2];
+    int t;
+    float l2, dl, g;
+  };
+  constexpr int kDepth = kTr ? 2 : 1;
+  Stage stg0, stg1;
+  stg0.t = stg1.t = -1;
+  stg0.l2 = stg1.l2 = INFINITY;
+  stg0.dl = stg1.dl = 0.f;
+  stg0.g = stg1.g = 1.f;
   // Rows past the item's end re-read its last row (finite data); they are masked
   // (p = 0) through s_t = -1, so every load is unconditional and the loads of a chunk
   // issue back to back.
@@ -242,17 +252,17 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   // is a multiple of NT (known at compile time: no branch)
   auto in_q = [&](int c) { return QPCS % NT == 0 || c < QPCS; };
   auto in_o = [&](int c) { return OPCS % NT == 0 || c < OPCS; };
-  auto load_chunk = [&](int fc) {
+  auto load_chunk = [&](int fc, Stage& sg) __attribute__((always_inline)) {
     if constexpr (kTr) {
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
         const int c = tid + NT * j;
-        if (in_q(c)) pq[j][0] = load_row(fc + c / (DK / EPF), qbase, sqh, sqt, (c % (DK / EPF)) * EPF);
+        if (in_q(c)) sg.pq[j][0] = load_row(fc + c / (DK / EPF), qbase, sqh, sqt, (c % (DK / EPF)) * EPF);
       }
 #pragma unroll
       for (int j = 0; j < NO; ++j) {
         const int c = tid + NT * j;
-        if (in_o(c)) po[j][0] = load_row(fc + c / (DV / EPF), obase, soh, sot, (c % (DV / EPF)) * EPF);
+        if (in_o(c)) sg.po[j][0] = load_row(fc + c / (DV / EPF), obase, soh, sot, (c % (DV / EPF)) * EPF);
       }
     } else {
 #pragma unroll
@@ -261,8 +271,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
       if (c < QPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
-        pq[j][0] = load_row(fc + 2 * rp, qbase, sqh, sqt, e);
-        pq[j][1] = load_row(fc + 2 * rp + 1, qbase, sqh, sqt, e);
+        sg.pq[j][0] = load_row(fc + 2 * rp, qbase, sqh, sqt, e);
+        sg.pq[j][1] = load_row(fc + 2 * rp + 1, qbase, sqh, sqt, e);
       }
     }
 #pragma unroll
@@ -271,8 +281,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
       if (c < OPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
-        po[j][0] = load_row(fc + 2 * rp, obase, soh, sot, e);
-        po[j][1] = load_row(fc + 2 * rp + 1, obase, soh, sot, e);
+        sg.po[j][0] = load_row(fc + 2 * rp, obase, soh, sot, e);
+        sg.po[j][1] = load_row(fc + 2 * rp + 1, obase, soh, sot, e);
       }
     }
     }
@@ -282,28 +292,28 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
       const int t = row_t(fe);
       const int h = grp * hpg + hdiv.mod(fe);
       const int64_t srow = ((int64_t)b * a.H + h) * a.Tq + t;
-      pr_l2 = a.lse2[srow];
-      pr_dl = a.delta[srow];
-      pr_g = a.row_gate ? a.row_gate[srow] : 1.f;
-      pr_t = f < f_hi ? t : -1;
+      sg.l2 = a.lse2[srow];
+      sg.dl = a.delta[srow];
+      sg.g = a.row_gate ? a.row_gate[srow] : 1.f;
+      sg.t = f < f_hi ? t : -1;
     }
   };
   // position of chunk row r in the transposed (C-permuted for bf16) stage; rows 2k and
   // 2k+1 stay adjacent
   auto rowpos = [](int r) -> int { return sizeof(S) == 2 ? cperm_pos32(r) : r; };
-  auto store_chunk = [&](int buf) {
+  auto store_chunk = [&](int buf, const Stage& sg) __attribute__((always_inline)) {
     if constexpr (kTr) {
 #pragma unroll
       for (int j = 0; j < NQ; ++j) {
         const int c = tid + NT * j;
         if (in_q(c))
-          *reinterpret_cast<uint4*>(&Qs[buf][(c / (DK / EPF)) * QP + (c % (DK / EPF)) * EPF]) = pq[j][0];
+          *reinterpret_cast<uint4*>(&Qs[buf][(c / (DK / EPF)) * QP + (c % (DK / EPF)) * EPF]) = sg.pq[j][0];
       }
 #pragma unroll
       for (int j = 0; j < NO; ++j) {
         const int c = tid + NT * j;
         if (in_o(c))
-          *reinterpret_cast<uint4*>(&Os[buf][(c / (DV / EPF)) * OP + (c % (DV / EPF)) * EPF]) = po[j][0];
+          *reinterpret_cast<uint4*>(&Os[buf][(c / (DV / EPF)) * OP + (c % (DV / EPF)) * EPF]) = sg.po[j][0];
       }
     } else {
 #pragma unroll
@@ -312,9 +322,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
       if (c < QPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
-        *reinterpret_cast<uint4*>(&Qs[buf][(2 * rp) * QP + e]) = pq[j][0];
-        *reinterpret_cast<uint4*>(&Qs[buf][(2 * rp + 1) * QP + e]) = pq[j][1];
-        PairT<S>::store(&QTs[buf][e * RP + rowpos(2 * rp)], RP, pq[j][0], pq[j][1]);
+        *reinterpret_cast<uint4*>(&Qs[buf][(2 * rp) * QP + e]) = sg.pq[j][0];
+        *reinterpret_cast<uint4*>(&Qs[buf][(2 * rp + 1) * QP + e]) = sg.pq[j][1];
+        PairT<S>::store(&QTs[buf][e * RP + rowpos(2 * rp)], RP, sg.pq[j][0], sg.pq[j][1]);
       }
     }
 #pragma unroll
@@ -323,33 +333,38 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
       if (c < OPC) {
         const int rp = c % RPAIRS;
         const int e = (c / RPAIRS) * EPF;
-        *reinterpret_cast<uint4*>(&Os[buf][(2 * rp) * OP + e]) = po[j][0];
-        *reinterpret_cast<uint4*>(&Os[buf][(2 * rp + 1) * OP + e]) = po[j][1];
-        PairT<S>::store(&OTs[buf][e * RP + rowpos(2 * rp)], RP, po[j][0], po[j][1]);
+        *reinterpret_cast<uint4*>(&Os[buf][(2 * rp) * OP + e]) = sg.po[j][0];
+        *reinterpret_cast<uint4*>(&Os[buf][(2 * rp + 1) * OP + e]) = sg.po[j][1];
+        PairT<S>::store(&OTs[buf][e * RP + rowpos(2 * rp)], RP, sg.po[j][0], sg.po[j][1]);
       }
     }
     }
     if (tid < RC) {
-      s_t[buf][tid] = pr_t;
-      s_l2[buf][tid] = pr_l2;
-      s_dl[buf][tid] = pr_dl;
-      s_g[buf][tid] = pr_g;
+      s_t[buf][tid] = sg.t;
+      s_l2[buf][tid] = sg.l2;
+      s_dl[buf][tid] = sg.dl;
+      s_g[buf][tid] = sg.g;
     }
   };
 
   const int nchunks = (f_hi - f_lo + RC - 1) / RC;
-  if (nchunks > 0) load_chunk(f_lo);
-  for (int c = 0; c < nchunks; ++c) {
+  // One chunk: stage it from its registers, request the chunk kDepth further on into
+  // them (bf16: unconditionally -- rows past the item's end re-read its last row and are
+  // masked -- so that no load sits in a branch, whose join would make the compiler wait
+  // for every load in flight), then the products.  A chunk wholly past the end (the
+  // pair loop's padding) contributes nothing: its rows are masked.
+  auto chunk = [&](int c, Stage& cur) __attribute__((always_inline)) {
     const int buf = c % NB;
     const int fc = f_lo + c * RC;
     if (NB == 1 && c > 0) __syncthreads();  // the previous chunk's reads are done
-    store_chunk(buf);
-    if (c + 1 < nchunks) load_chunk(fc + RC);
+    store_chunk(buf, cur);
+    if constexpr (kDepth == 2) load_chunk(fc + 2 * RC, cur);
+    else if (c + 1 < nchunks) load_chunk(fc + RC, cur);
     __syncthreads();
 
     // rows are in ascending t, so the chunk spans [t_min, t_max]
     const bool full = fc + RC <= f_hi;
-    const int t_min = row_t(fc);
+    const int t_min = row_t(min(fc, f_hi - 1));
     const int t_max = row_t(min(fc + RC, f_hi) - 1);
     bool active, all_visible;
     if (BR == kSliding) {
@@ -429,6 +444,19 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
         }
       }
     }
+  };
+  if constexpr (kDepth == 2) {
+    if (nchunks > 0) {
+      load_chunk(f_lo, stg0);
+      load_chunk(f_lo + RC, stg1);
+    }
+    for (int c = 0; c < nchunks; c += 2) {  // an odd count runs one padding chunk
+      chunk(c, stg0);
+      chunk(c + 1, stg1);
+    }
+  } else {
+    if (nchunks > 0) load_chunk(f_lo, stg0);
+    for (int c = 0; c < nchunks; ++c) chunk(c, stg0);
   }
 
   // ---- direct mode: add this item's dK / dV into the caller's, or store them (lane holds
