@@ -45,6 +45,10 @@ struct FwdTile {
   // epilogue overlap the other's tile loop: a double buffer when two workgroups' stages
   // fit the 160 KB of LDS, else one stage (the other workgroup covers the refill)
   static constexpr int NBUF = 2 * BYTES <= 76 * 1024 ? 2 : 1;
+  // when two whole stages do not fit: one K region and two V regions, so that the next
+  // tile's V copy overlaps this tile's products and its K copy this tile's softmax and P V
+  static constexpr bool SPLIT = NBUF == 1 && 2 * (NKF + 2 * NVF) * 1024 <= 152 * 1024;
+  static constexpr int LDS = NBUF == 2 ? 2 * BYTES : SPLIT ? (NKF + 2 * NVF) * 1024 : BYTES;
 };
 
 template <typename T, int DK, int DV, int BR>
@@ -61,7 +65,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   constexpr int NW = kFwdWaves;
   static_assert(DK % KC == 0 && DV % 16 == 0, "head dims");
 
-  extern __shared__ __attribute__((aligned(16))) uint4 fwd_lds[];  // [NBUF][NKF + NVF][64]
+  extern __shared__ __attribute__((aligned(16))) uint4 fwd_lds[];  // [NBUF][NKF + NVF][64] or [NKF + 2 NVF][64]
   __shared__ int s_be[2][64];
   __shared__ int s_misc[4];
 
@@ -145,10 +149,12 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
     ntiles = (s_misc[0] + 63) / 64;
   }
 
-  // ---- the direct-to-LDS copy of one tile: wave w copies fragments w, w + NW, ... ----
-  auto copy_tile = [&](int key0, int buf) __attribute__((always_inline)) {
-    uint4* dst = fwd_lds + buf * (FT::NKF + FT::NVF) * 64;
-    for (int f = wave; f < FT::NKF + FT::NVF; f += NW) {
+  // ---- direct-to-LDS copies of fragments [f0, f1) of one tile (K rowfrags first, then
+  // V^T colfrags) to dst: wave w copies fragments f0 + w, f0 + w + NW, ...; async: the
+  // in-loop copies, hidden from the compiler's wait insertion (the loop waits for them
+  // itself before its barrier) ----
+  auto copy_frags = [&](int key0, uint4* dst, int f0, int f1, auto async) __attribute__((always_inline)) {
+    for (int f = f0 + wave; f < f1; f += NW) {
       const S* src;
       if (f < FT::NKF) {  // K rowfrag (16-key group (key0 >> 4) + ks, feature chunk kc)
         const int ks = f / NKC, kc = f % NKC;
@@ -157,8 +163,12 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
         const int v = f - FT::NKF, kc2 = v / (DV / 16), j = v % (DV / 16);
         src = vcf + ((((int64_t)(key0 / CK) + kc2) * (DV / 16) + j) * 64 + lane) * EPF;
       }
-      copy16_to_lds(src, dst + f * 64);
+      if constexpr (decltype(async)::value) copy16_to_lds_async(src, dst + (f - f0) * 64);
+      else copy16_to_lds(src, dst + (f - f0) * 64);
     }
+  };
+  auto copy_tile = [&](int key0, int buf, auto async) __attribute__((always_inline)) {
+    copy_frags(key0, fwd_lds + buf * (FT::NKF + FT::NVF) * 64, 0, FT::NKF + FT::NVF, async);
   };
   auto tile_key0 = [&](int it) -> int { return BR == kSliding ? key_lo + it * 64 : it * 64; };
   int pbe = 0x7fffffff;
@@ -169,8 +179,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
     }
   };
   // S^T for every subtile: each K fragment read from LDS feeds NSUB products
-  auto compute_s = [&](f32x4 (&st)[NSUB][4], int buf) __attribute__((always_inline)) {
-    const uint4* kb = fwd_lds + buf * (FT::NKF + FT::NVF) * 64;
+  auto compute_s = [&](f32x4 (&st)[NSUB][4], const uint4* kb) __attribute__((always_inline)) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
@@ -184,8 +193,7 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
     }
   };
   // masking, online softmax and O^T += V^T P^T for the tile at key0 in stage buf
-  auto softmax_pv = [&](f32x4 (&st)[NSUB][4], int key0, int buf, const int* sbe) __attribute__((always_inline)) {
-    const uint4* vb = fwd_lds + buf * (FT::NKF + FT::NVF) * 64 + FT::NKF * 64;
+  auto softmax_pv = [&](f32x4 (&st)[NSUB][4], int key0, const uint4* vb, const int* sbe) __attribute__((always_inline)) {
     int be_max = 0;
     if (BR == kCompression) {
       be_max = wave_butterfly(sbe[lane], [](int x, int y) { return max(x, y); });
@@ -282,25 +290,55 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   };
 
   f32x4 st[NSUB][4];
-  if (ntiles > 0) {
-    copy_tile(tile_key0(0), 0);
-    load_be(tile_key0(0));
-  }
-  for (int it = 0; it < ntiles; ++it) {
-    const int buf = FT::NBUF == 2 ? (it & 1) : 0;
-    if (BR == kCompression && tid < 64) s_be[it & 1][tid] = pbe;
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile it have landed
-    __syncthreads();                // every wave's have; tile it-1 is no longer read
-    if (FT::NBUF == 2 && it + 1 < ntiles) {
-      copy_tile(tile_key0(it + 1), buf ^ 1);
-      load_be(tile_key0(it + 1));
+  if constexpr (FT::SPLIT) {
+    // [K][V0][V1]: tile it's V in region it & 1.  The next tile's V is copied at the top
+    // (its region held tile it-1's V, which every wave is past), its K once every wave's
+    // S^T products have read this tile's K.
+    uint4* kreg = fwd_lds;
+    auto vreg = [&](int vb) { return fwd_lds + (FT::NKF + vb * FT::NVF) * 64; };
+    if (ntiles > 0) {
+      copy_frags(tile_key0(0), kreg, 0, FT::NKF, std::false_type{});
+      copy_frags(tile_key0(0), vreg(0), FT::NKF, FT::NKF + FT::NVF, std::false_type{});
+      load_be(tile_key0(0));
     }
-    compute_s(st, buf);
-    softmax_pv(st, tile_key0(it), buf, s_be[it & 1]);
-    if (FT::NBUF == 1 && it + 1 < ntiles) {  // single buffer: refill once every wave is done
-      __syncthreads();
-      copy_tile(tile_key0(it + 1), 0);
-      load_be(tile_key0(it + 1));
+    for (int it = 0; it < ntiles; ++it) {
+      const int vb = it & 1;
+      if (BR == kCompression && tid < 64) s_be[it & 1][tid] = pbe;
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile it have landed
+      __syncthreads();                // every wave's have; tile it-1 is no longer read
+      if (it + 1 < ntiles) {
+        copy_frags(tile_key0(it + 1), vreg(vb ^ 1), FT::NKF, FT::NKF + FT::NVF, std::true_type{});
+        load_be(tile_key0(it + 1));
+      }
+      compute_s(st, kreg);
+      if (it + 1 < ntiles) {
+        __syncthreads();  // every wave's S^T products have read this tile's K
+        copy_frags(tile_key0(it + 1), kreg, 0, FT::NKF, std::true_type{});
+      }
+      softmax_pv(st, tile_key0(it), vreg(vb), s_be[it & 1]);
+    }
+  } else {
+    if (ntiles > 0) {
+      copy_tile(tile_key0(0), 0, std::false_type{});
+      load_be(tile_key0(0));
+    }
+    for (int it = 0; it < ntiles; ++it) {
+      const int buf = FT::NBUF == 2 ? (it & 1) : 0;
+      if (BR == kCompression && tid < 64) s_be[it & 1][tid] = pbe;
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile it have landed
+      __syncthreads();                // every wave's have; tile it-1 is no longer read
+      if (FT::NBUF == 2 && it + 1 < ntiles) {
+        copy_tile(tile_key0(it + 1), buf ^ 1, std::true_type{});
+        load_be(tile_key0(it + 1));
+      }
+      const uint4* kb = fwd_lds + buf * (FT::NKF + FT::NVF) * 64;
+      compute_s(st, kb);
+      softmax_pv(st, tile_key0(it), kb + FT::NKF * 64, s_be[it & 1]);
+      if (FT::NBUF == 1 && it + 1 < ntiles) {  // single buffer: refill once every wave is done
+        __syncthreads();
+        copy_tile(tile_key0(it + 1), 0, std::true_type{});
+        load_be(tile_key0(it + 1));
+      }
     }
   }
 
@@ -404,7 +442,7 @@ void launch_attn_fwd(const AttnArgs& a, hipStream_t s) {
     using FT = FwdTile<T, DK, DV>;
     // the K/V tile stages, reused by the bf16 epilogue for the workgroup's output rows
     const size_t stage = sizeof(typename Store<T>::type) == 2 ? (size_t)kFwdCols * (DV + 8) * 2 : 0;
-    const size_t lds = std::max((size_t)FT::NBUF * FT::BYTES, stage);
+    const size_t lds = std::max((size_t)FT::LDS, stage);
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, DK, DV, BR>),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     dim3 grid((a.Tq * a.hpg + kFwdCols - 1) / kFwdCols, a.B * a.G);

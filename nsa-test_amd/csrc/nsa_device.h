@@ -188,6 +188,18 @@ __device__ __forceinline__ void copy16_to_lds(const void* src, void* lds_base) {
                                    (__attribute__((address_space(3))) void*)(lds_base), 16, 0, 0);
 }
 
+// The same copy issued from inline assembly, so that the compiler's wait insertion does
+// not see it.  The compiler cannot tell which LDS bytes a direct-to-LDS copy writes, so
+// it makes every later LDS read wait for every such copy in flight, which would stall a
+// tile's reads on the copy of the next tile.  A caller of this variant waits for the copy
+// itself (s_waitcnt vmcnt(0)) before the barrier that publishes the data.
+__device__ __forceinline__ void copy16_to_lds_async(const void* src, void* lds_base) {
+  // wave-uniform by contract: taken from the first lane so that it lives in an SGPR
+  const uint32_t lds =
+      __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)((__attribute__((address_space(3))) char*)(lds_base)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(lds) : "memory", "m0");
+}
+
 // Orders a wave's LDS stores before its later LDS loads of other lanes' data: waits
 // for the wave's LDS operations only (lgkmcnt(0), vmcnt / expcnt left at their
 // maximum), so global loads and stores stay in flight.
