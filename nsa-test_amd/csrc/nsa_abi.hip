@@ -69,11 +69,17 @@ struct Shape {
     return (int64_t)Z * G * items_for(kSegTMax) < 4096 ? kSegTMax / 2 : kSegTMax;
   }
   int items_per_bg() const { return items_for(seg()); }
+  // selection backward with stored dS (bf16, whole 16-head groups, 64-key sub-blocks):
+  // the dK/dV kernel runs first and stores dS, the dQ kernel reads it
+  bool stored_ds() const {
+    return br == kSelection && dtype == NSA_BF16 && hpg() % 16 == 0 && lprime % 64 == 0 && nslots > 0;
+  }
+  size_t ds_bytes() const { return stored_ds() ? (size_t)Z * H * Tq * nslots * lprime * 2 : 0; }
 };
 
 struct Layout {
   size_t krf = 0, kcf = 0, vrf = 0, vcf = 0, lse2 = 0, delta = 0, clean = 0, chunk = 0, csr_off = 0, csr_t = 0,
-         seg_off = 0, partial = 0, total = 0;
+         seg_off = 0, csr_s = 0, ds = 0, partial = 0, total = 0;
 };
 
 // Offsets into the caller's workspace (every buffer 256-byte aligned).
@@ -107,6 +113,10 @@ Layout make_layout(const Shape& s, bool bwd) {
       L.csr_off = take(BG * (s.nblk() + 1) * 4);
       L.seg_off = take(BG * (s.nblk() + 1) * 4);
       L.csr_t = take(BG * s.Tq * s.nslots * 4);
+      if (s.stored_ds()) {
+        L.csr_s = take(BG * s.Tq * s.nslots * 4);
+        L.ds = take(s.ds_bytes());
+      }
     }
   }
   if (bwd && !s.direct()) L.partial = take(BG * s.items_per_bg() * dkdv_keys(s.br) * (size_t)(s.dk + s.dv) * 4);
@@ -334,18 +344,34 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
     launch_sel_clean(idx, idx64, sidx[0], sidx[1], sidx[2], sidx[3], s.Z, s.G, s.Tq, s.nslots, s.nslots, s.lprime,
                      s.Tkv, fallback, causal, at<int>(ws, L.clean), at<int>(ws, L.chunk), s.nblk(), 0, st);
     launch_sel_csr(at<int>(ws, L.clean), at<int>(ws, L.chunk), s.Z, s.G, s.Tq, s.nslots, s.nblk(),
-                   at<int>(ws, L.csr_off), at<int>(ws, L.csr_t), at<int>(ws, L.seg_off), s.seg(), st);
+                   at<int>(ws, L.csr_off), at<int>(ws, L.csr_t), s.stored_ds() ? at<int>(ws, L.csr_s) : nullptr,
+                   at<int>(ws, L.seg_off), s.seg(), st);
     a.sel = at<int>(ws, L.clean);
     a.csr_off = at<int>(ws, L.csr_off);
     a.csr_t = at<int>(ws, L.csr_t);
     a.seg_off = at<int>(ws, L.seg_off);
   }
   if ((rc = check_hip("backward prep"))) return rc;
-  {
-    TimingScope ts(kIdDq + s.br, st);
-    if (!dispatch_attn_bwd_dq(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no dQ kernel");
+  auto dq = [&]() -> int {
+    {
+      TimingScope ts(kIdDq + s.br, st);
+      if (!dispatch_attn_bwd_dq(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no dQ kernel");
+    }
+    return check_hip("dQ kernel");
+  };
+  // stored dS: the row statistics first, then dK/dV (which stores dS), then dQ from it;
+  // otherwise the dQ kernel computes the statistics and dK/dV follows
+  if (s.stored_ds()) {
+    a.csr_s = at<int>(ws, L.csr_s);
+    a.ds = at<char>(ws, L.ds);
+    {
+      TimingScope ts(kIdPrep, st);
+      if (!launch_row_stats(s.dtype, s.dv, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no row statistics kernel");
+    }
+    if ((rc = check_hip("row statistics"))) return rc;
+  } else if ((rc = dq())) {
+    return rc;
   }
-  if ((rc = check_hip("dQ kernel"))) return rc;
   {
     TimingScope ts(kIdDkdv + s.br, st);
     if (!dispatch_attn_bwd_dkdv(s.dtype, s.dk, s.dv, s.br, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no dK/dV kernel");
@@ -356,6 +382,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
     if (!a.direct) launch_partial_reduce(s.dtype, s.dk, s.dv, s.br, a, st);
   }
   if ((rc = check_hip("dK/dV reduce"))) return rc;
+  if (s.stored_ds() && (rc = dq())) return rc;
   return NSA_OK;
 }
 

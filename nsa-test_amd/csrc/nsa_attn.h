@@ -90,6 +90,12 @@ struct AttnArgs {
   const int* csr_off;     // [B,G,nblk+1]
   const int* csr_t;       // [B,G,Tq*nslots] query timesteps per block, ascending
   const int* seg_off;     // [B,G,nblk+1] work-item prefix per block
+  const int* csr_s;       // [B,G,Tq*nslots] the slot of each CSR entry in its timestep's cleaned list
+  // selection, stored-dS backward (bf16, hpg and l' multiples of 16 and 64): the dK/dV
+  // kernel writes every (timestep, slot) pair's dS in the MFMA operand order of the dQ
+  // product, and the dQ kernel reads it instead of recomputing S and dP:
+  //   ds[b,g][t][slot][64-key sub-block][16-head group] = 2 fragments x 64 lanes x 8 bf16
+  void* ds;
 };
 
 template <typename T, int DK, int DV, int BR>

@@ -13,6 +13,13 @@
 // two rows at once, and the transposed row pitch (RC + 4) keeps those writes free of
 // bank conflicts.
 //
+// Selection, bf16, heads per group a multiple of 16 (a.ds set): the kernel also stores
+// every (timestep, slot) pair's dS for the dQ kernel, which then needs no S / dP
+// recomputation.  A 16-row subtile is the 16 heads of one head group of one entry; the
+// wave's 16 x 16 dS tile goes through LDS ([key][head], written as the lane's four
+// heads of one key) and comes back through the transpose load as the lane's four keys
+// of one head, which is exactly its share of the dQ product's dS^T operand fragment.
+//
 // Every item writes its fp32 dK/dV partial for its keys; a reduce kernel sums the
 // segments of each key tile in a fixed order and accumulates into the caller's dK/dV.
 // Direct mode (sliding window with at least kDkdvDirectItems key tiles over all batches
@@ -112,6 +119,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) float s_g[NB][RC];
   __shared__ int s_be[KEYS];
   __shared__ int s_tl[kSegTMax];  // selection: the item's query timesteps
+  // stored dS (selection, bf16): the entries' slots and one 16 x 16 transpose tile per
+  // wave and row subtile
+  constexpr bool kStoreDs = BR == kSelection && sizeof(S) == 2;
+  __shared__ int s_sl[kStoreDs ? kSegTMax : 1];
+  // [chunk parity][row subtile][64 keys][16 heads]: a chunk's dS tiles, written by the
+  // four waves (their 16 keys each) and stored after the next chunk's barrier
+  __shared__ __attribute__((aligned(16))) uint16_t s_dst[kStoreDs ? 2 : 1][RC / 16][kStoreDs ? KEYS * 16 : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -130,6 +144,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   int key0, blk_hi = a.Tkv;
   int f_lo, f_hi;              // flattened row range (row f -> (t, head))
   int e_base = 0;              // selection: row f -> t = s_tl[f / hpg - e_base]
+  int sub = 0;                 // selection: the item's 64-key sub-block of its block
   if (BR == kSliding) {
     const int nseg = dkdv_nseg(kSliding, a.Tq, a.window, a.seg);
     const int tile = item / nseg, seg = item % nseg;
@@ -158,7 +173,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     f_hi = t_hi > t_lo ? t_hi * hpg : f_lo;
   } else {
     const int nsubblk = (a.lprime + 63) / 64;
-    const int sidx = item / nsubblk, sub = item % nsubblk;
+    const int sidx = item / nsubblk;
+    sub = item % nsubblk;
     const int* so = a.seg_off + (int64_t)bg * (a.nblk + 1);
     if (sidx >= so[a.nblk]) return;  // beyond this group's work list (uniform)
     int lo = 0, hi = a.nblk;         // largest j with so[j] <= sidx
@@ -180,6 +196,10 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     e_base = e_lo;
     const int* tlist = a.csr_t + (int64_t)bg * a.Tq * a.nslots;
     for (int i = tid; i < e_hi - e_lo; i += NT) s_tl[i] = tlist[e_lo + i];
+    if (kStoreDs && a.ds) {
+      const int* slist = a.csr_s + (int64_t)bg * a.Tq * a.nslots;
+      for (int i = tid; i < e_hi - e_lo; i += NT) s_sl[i] = slist[e_lo + i];
+    }
     __syncthreads();
   }
 
@@ -347,6 +367,26 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     }
   };
 
+  // stored dS of chunk cp (after a barrier that follows its tile writes): wave w stores
+  // fragment (w & 1) of row subtile w >> 1, lane (g4, c16) reading head c16 at the
+  // 32-key chunk's keys 4 g4 + i and 16 + 4 g4 + i (its 8 slots) with two transpose loads
+  auto flush_ds = [&](int cp) __attribute__((always_inline)) {
+    if constexpr (kStoreDs) {
+      const int rs = wave >> 1, kc2 = wave & 1;
+      const int fr = f_lo + cp * RC + rs * 16;  // the subtile's rows: 16 heads of one entry
+      if (!a.ds || fr >= f_hi) return;           // wave-uniform
+      const int e = hdiv.div(fr);
+      const int hg = (fr - e * hpg) >> 4;
+      const int t = s_tl[e - e_base], slot = s_sl[e - e_base];
+      const uint4 v = ld_tr_pair(&s_dst[cp & 1][rs][(kc2 * 32 + 4 * g4 + (c16 >> 2)) * 16 + 4 * (c16 & 3)], 16 * 16);
+      const int nhg = hpg >> 4, nsub = a.lprime >> 6;
+      uint16_t* dsp = reinterpret_cast<uint16_t*>(a.ds) +
+                      ((((int64_t)bg * a.Tq + t) * a.nslots + slot) * nsub + sub) * nhg * 1024 + hg * 1024 +
+                      (kc2 * 64 + lane) * 8;
+      // written once and read once by the dQ kernel: non-temporal
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dsp));
+    }
+  };
   const int nchunks = (f_hi - f_lo + RC - 1) / RC;
   // One chunk: stage it from its registers, request the chunk kDepth further on into
   // them (bf16: unconditionally -- rows past the item's end re-read its last row and are
@@ -361,6 +401,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     if constexpr (kDepth == 2) load_chunk(fc + 2 * RC, cur);
     else if (c + 1 < nchunks) load_chunk(fc + RC, cur);
     __syncthreads();
+    if (c > 0) flush_ds(c - 1);  // the previous chunk's dS tiles are complete
 
     // rows are in ascending t, so the chunk spans [t_min, t_max]
     const bool full = fc + RC <= f_hi;
@@ -417,6 +458,11 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
           pt[rs][i] = p;
           dst[rs][i] = p * (pacc[i] - dla[i]);
         }
+        if constexpr (kStoreDs) {  // the lane's four heads of its key, into the chunk's tile
+          if (a.ds)
+            *reinterpret_cast<uint2*>(&s_dst[c & 1][rs][(wave * 16 + c16) * 16 + 4 * g4]) =
+                make_uint2(pack_bf16x2(dst[rs][0], dst[rs][1]), pack_bf16x2(dst[rs][2], dst[rs][3]));
+        }
       }
 #pragma unroll
       for (int kc2 = 0; kc2 < RC / CK; ++kc2) {
@@ -450,9 +496,14 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
       load_chunk(f_lo, stg0);
       load_chunk(f_lo + RC, stg1);
     }
-    for (int c = 0; c < nchunks; c += 2) {  // an odd count runs one padding chunk
+    int c = 0;
+    for (; c < nchunks; c += 2) {  // an odd count runs one padding chunk
       chunk(c, stg0);
       chunk(c + 1, stg1);
+    }
+    if (kStoreDs && a.ds && c > 0) {
+      __syncthreads();
+      flush_ds(c - 1);
     }
   } else {
     if (nchunks > 0) load_chunk(f_lo, stg0);

@@ -583,8 +583,93 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
   }
 }
 
+// ============================================================== dQ from stored dS
+// bf16, heads per group a multiple of 16, l' a multiple of 64, after the dK/dV kernel
+// has stored every (timestep, slot) pair's dS (nsa_attn_bwd_dkdv.h): one wave = the 16
+// heads of one head group at one timestep, dQ^T += K^T dS^T over the 64-key sub-blocks
+// of the timestep's cleaned list (ascending; the visible ones form a prefix of the
+// (slot, sub-block) order).  Both operands are fragment-native in memory -- K^T from
+// the re-packed colfrag copy, dS^T as stored -- so every fragment is one coalesced 1 KB
+// load straight into registers: no LDS, no S / dP recomputation, no softmax.  The
+// next tile's fragments of one 32-key chunk are requested as soon as this tile's
+// products have read that chunk.  The stored dS already carries the row gate, so the
+// epilogue scales by sm_scale only.
+template <typename T, int DK>
+__global__ __launch_bounds__(256) void attn_sel_dq_ds_kernel(AttnArgs a, int nwaves) {
+  using S = typename Store<T>::type;
+  constexpr int EPF = Elem<T>::kPerFrag;
+  static_assert(sizeof(S) == 2, "stored dS is bf16");
+  const int lane = threadIdx.x & 63;
+  const int g4 = lane >> 4, c16 = lane & 15;
+  const int W = xcd_contiguous(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (W >= nwaves) return;
+  const int nhg = a.hpg >> 4, nsub = a.lprime >> 6;
+  const int per_bg = a.Tq * nhg;
+  const int bg = W / per_bg, rem = W - bg * per_bg;
+  const int t = rem / nhg, hg = rem - t * nhg;
+  const int b = bg / a.G, grp = bg % a.G;
+  const int colh = grp * a.hpg + hg * 16 + c16;
+
+  // the timestep's cleaned list (lane s holds slot s) and its visible tile count: slot s
+  // contributes the sub-blocks of its block that start before kend
+  const int lv = lane < a.nslots ? a.sel[((int64_t)bg * a.Tq + t) * a.nslots + lane] : -1;
+  const int kend = a.causal ? min(a.Tkv, t + 1) : a.Tkv;
+  int nt = 0;
+  if (lv >= 0) nt = min(nsub, max(0, (kend - lv * a.lprime + 63) >> 6));
+  nt = __builtin_amdgcn_readfirstlane(wave_butterfly(nt, [](int x, int y) { return x + y; }));
+
+  const S* kcf = reinterpret_cast<const S*>(a.kcf) + (int64_t)bg * DK * a.Tp;
+  const S* dsb = reinterpret_cast<const S*>(a.ds) + (((int64_t)bg * a.Tq + t) * a.nslots * nsub * nhg + hg) * 1024;
+  uint4 kf[2][DK / 16];
+  u32x4 df[2];
+  auto load = [&](int i, int kc2) __attribute__((always_inline)) {
+    const int slot = i / nsub, sub = i - slot * nsub;
+    const int key0 = __builtin_amdgcn_readlane(lv, slot) * a.lprime + sub * 64;
+#pragma unroll
+    for (int j = 0; j < DK / 16; ++j) kf[kc2][j] = ld_colfrag<T>(kcf, key0 / 32 + kc2, j, DK, lane);
+    // dS is read once: non-temporal, so the stream does not evict the group's K^T from L2
+    df[kc2] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(dsb + (int64_t)i * nhg * 1024 + (kc2 * 64 + lane) * EPF));
+  };
+  f32x4 dqa[DK / 16];
+#pragma unroll
+  for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
+  if (nt > 0) {
+    load(0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    load(0, 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  for (int i = 0; i < nt; ++i) {
+    const int nx = i + 1 < nt ? i + 1 : i;  // unconditional loads (the last tile re-reads itself)
+#pragma unroll
+    for (int kc2 = 0; kc2 < 2; ++kc2) {
+#pragma unroll
+      for (int j = 0; j < DK / 16; ++j) dqa[j] = Mma<T>::run(dqa[j], kf[kc2][j], __builtin_bit_cast(uint4, df[kc2]));
+      // keep the order: this chunk's products, then the next tile's loads into its
+      // registers (the scheduler would otherwise hoist the loads and wait for all of them)
+      __builtin_amdgcn_sched_barrier(0);
+      load(nx, kc2);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)t * a.sdq_t;
+#pragma unroll
+  for (int j = 0; j < DK / 16; ++j) {
+    f32x4 v = dqa[j] * a.scale;
+    if (a.dq_acc) v += load4<T>(dqp + j * 16 + 4 * g4);  // the caller's running dQ sum
+    store4<T>(dqp + j * 16 + 4 * g4, v);
+  }
+}
+
 template <typename T, int DK, int DV>
 void launch_attn_sel_dq(const AttnArgs& a, hipStream_t s) {
+  if constexpr (sizeof(typename Store<T>::type) == 2) {
+    if (a.ds) {
+      const int nwaves = a.B * a.G * a.Tq * (a.hpg / 16);
+      hipLaunchKernelGGL((attn_sel_dq_ds_kernel<T, DK>), dim3((nwaves + 3) / 4), dim3(256), 0, s, a, nwaves);
+      return;
+    }
+  }
   const int ncoltiles = (a.Tq * a.hpg + 63) / 64;
   hipLaunchKernelGGL((attn_sel_dq_kernel<T, DK, DV>), dim3(ncoltiles * a.B * a.G), dim3(256), 0, s, a, ncoltiles);
 }

@@ -22,6 +22,8 @@ void launch_repack_kv(int dtype, const void* k, const int64_t* sk, int dk, void*
 bool dispatch_attn_fwd(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
 bool dispatch_attn_bwd_dq(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
 bool dispatch_attn_bwd_dkdv(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
+// lse2 / delta (/ row_dot) of every query row before a dK/dV kernel that runs first
+bool launch_row_stats(int dtype, int dv, const AttnArgs& a, hipStream_t st);
 void launch_partial_reduce(int dtype, int dk, int dv, int br, const AttnArgs& a, hipStream_t st);
 // dK / dV [B, G, Tkv, dk | dv] (a.dk / a.dv, any strides) set to zero
 void launch_zero_dkdv(int dtype, int dk, int dv, const AttnArgs& a, hipStream_t st);
@@ -30,8 +32,9 @@ void launch_zero_dkdv(int dtype, int dk, int dv, const AttnArgs& a, hipStream_t 
 void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g, int64_t si_t, int64_t si_n, int B,
                       int G, int Tq, int n_in, int nslots, int lprime, int Tkv, int fallback, int causal, int* clean,
                       int* chunk_cnt, int nblk, int q0, hipStream_t st);
+// csr_s (nullable) receives each entry's slot in its timestep's cleaned list
 void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int nslots, int nblk, int* csr_off,
-                    int* csr_t, int* seg_off, int seg, hipStream_t st);
+                    int* csr_t, int* csr_s, int* seg_off, int seg, hipStream_t st);
 int sel_csr_chunks(int Tq);
 
 // record an error message for nsa_last_error(); returns `code`

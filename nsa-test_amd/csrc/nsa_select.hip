@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void sel_csr_block_scan_kernel(int nblk, int s
 // so the lanes of one step never collide.
 __global__ __launch_bounds__(64) void sel_csr_fill_kernel(const int* clean, const int* chunk_base,
                                                           const int* csr_off, int Tq, int nslots, int nchunks,
-                                                          int nblk, int* csr_t, int64_t csr_stride) {
+                                                          int nblk, int* csr_t, int* csr_s, int64_t csr_stride) {
   extern __shared__ int cur[];  // nblk
   const int c = blockIdx.x, bg = blockIdx.y;
   const int lane = threadIdx.x;
@@ -150,6 +150,7 @@ __global__ __launch_bounds__(64) void sel_csr_fill_kernel(const int* clean, cons
   for (int j = lane; j < nblk; j += 64) cur[j] = off[j] + cb[j];
   __syncthreads();
   int* out = csr_t + (int64_t)bg * csr_stride;
+  int* out_s = csr_s ? csr_s + (int64_t)bg * csr_stride : nullptr;
   const int t0 = c * kCsrChunk;
   const int t1 = min(Tq, t0 + kCsrChunk);
   for (int t = t0; t < t1; ++t) {
@@ -159,6 +160,7 @@ __global__ __launch_bounds__(64) void sel_csr_fill_kernel(const int* clean, cons
       if (v >= 0) {
         const int pos = cur[v];
         out[pos] = t;
+        if (out_s) out_s[pos] = s;
         cur[v] = pos + 1;
       }
     }
@@ -190,13 +192,13 @@ void launch_sel_clean(const void* idx, int idx_is64, int64_t si_b, int64_t si_g,
 }
 
 void launch_sel_csr(const int* clean, int* chunk_cnt, int B, int G, int Tq, int nslots, int nblk, int* csr_off,
-                    int* csr_t, int* seg_off, int seg, hipStream_t st) {
+                    int* csr_t, int* csr_s, int* seg_off, int seg, hipStream_t st) {
   const int nchunks = (Tq + kCsrChunk - 1) / kCsrChunk;
   hipLaunchKernelGGL(sel_csr_chunk_scan_kernel, dim3((nblk + 3) / 4, B * G), dim3(256), 0, st, chunk_cnt, nchunks,
                      nblk, csr_off);
   hipLaunchKernelGGL(sel_csr_block_scan_kernel, dim3(B * G), dim3(256), 0, st, nblk, seg, csr_off, seg_off);
   hipLaunchKernelGGL(sel_csr_fill_kernel, dim3(nchunks, B * G), dim3(64), nblk * sizeof(int), st, clean, chunk_cnt,
-                     csr_off, Tq, nslots, nchunks, nblk, csr_t, (int64_t)Tq * nslots);
+                     csr_off, Tq, nslots, nchunks, nblk, csr_t, csr_s, (int64_t)Tq * nslots);
 }
 
 int sel_csr_chunks(int Tq) { return (Tq + kCsrChunk - 1) / kCsrChunk; }

@@ -128,6 +128,10 @@ SELECTION_CASES = [
     (1, 32, 2, 1024, 128, 128, 64, 16, torch.bfloat16),
     (1, 2, 2, 400, 64, 64, 32, 16, torch.bfloat16),  # one head per group, 16 slots
     (1, 6, 2, 333, 64, 64, 48, 5, torch.float32),    # 3 heads per group, blocks straddling 32-key chunks
+    # bf16 with whole 16-head groups: dQ from the dS the dK/dV kernel stores
+    (1, 64, 2, 300, 64, 64, 64, 8, torch.bfloat16),   # two head groups per KV group
+    (1, 16, 1, 500, 128, 128, 128, 4, torch.bfloat16),  # two 64-key sub-blocks per block
+    (2, 32, 2, 200, 32, 32, 64, 16, torch.bfloat16),  # n larger than the number of blocks
 ]
 
 

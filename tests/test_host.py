@@ -117,6 +117,16 @@ def test_workspace_sizes():
     assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 16, 1, 8192, 8192, 192, 128, 0, 64, 8192) > b1
     s = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 16, 64, 1)
     assert s > f
+    # selection, bf16, 16 heads per group: the stored dS (2 bytes per (row, slot, key of
+    # the block)) and the CSR entries' slots (4 bytes per (group row, slot)); fp32 and
+    # 3 heads per group keep the recomputing dQ kernel and neither buffer
+    sf = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_F32, 1, 64, 4, 8192, 8192, 192, 128, 16, 64, 1)
+    tp = 8192 + 64  # re-packed K/V rows (a multiple of 64, plus 64 zero rows)
+    kv16 = 4 * tp * (2 * 192 + 128) * 2  # K rowfrag + K colfrag + V rowfrag copies, bf16
+    assert s - (sf - kv16) == 64 * 8192 * 16 * 64 * 2 + 4 * 8192 * 16 * 4
+    s3 = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_BF16, 1, 12, 4, 8192, 8192, 192, 128, 16, 64, 1)
+    s3f = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_F32, 1, 12, 4, 8192, 8192, 192, 128, 16, 64, 1)
+    assert s3f - s3 > 0  # only the fp32 K/V copies are larger
     # scoring: fp32 logits [Z*H][T][N rounded up to 64], then one int per 128-row tile of
     # a group's (timestep, head) rows, padded to 256 bytes
     sc = _lib.load().nsa_score_topn_workspace_size
