@@ -10,7 +10,8 @@ of all of it.  Inputs (q, k, v, dO ~ N(0,1)/sqrt(d), gate logits, N(0,0.02) MLP
 weights) are synthetic and resident in HBM before the timed region.
 
 The JSON line also carries the long-context configuration (T=32768, configs[3]) as
-`secondary`, a per-kernel breakdown, the roofline of the dominant kernel (timed with
+`secondary`, the sliding-window branch alone at configs[1] as `config2_sliding`, a
+per-kernel breakdown, per-branch fwd and fwd+bwd tokens/s, the roofline of the dominant kernel (timed with
 HIP events inside the timed region) and a CPU baseline (the C oracle on all host cores,
 one thread each, on a sample of query rows, extrapolated linearly: each row's work is
 independent).
@@ -138,6 +139,67 @@ def kernel_flops(cfg, pairs):
         out[3 + br] = 2 * dk * p
         out[6 + br] = 2 * (2 * dk + 2 * dv) * p
     return out
+
+
+def per_branch(cfg, breakdown, pairs, tokens):
+    """Per-branch fwd and fwd+bwd tokens/s from the per-kernel breakdown (forward, dQ
+    and dK/dV kernels; the dK/dV partial reduce, shared by the branches, is left out),
+    with the algorithmic bf16 MFMA fraction of each (forward 2(dk+dv), backward
+    2(3dk+2dv) FLOP per valid pair)."""
+    dk, dv = cfg.head_dim_qk, cfg.head_dim_v
+    out = {}
+    for br, name in enumerate(("sliding", "compression", "selection")):
+        f = breakdown.get(f"fwd_{name}", {"ms": 0.0})["ms"]
+        bwd = breakdown.get(f"dq_{name}", {"ms": 0.0})["ms"] + breakdown.get(f"dkdv_{name}", {"ms": 0.0})["ms"]
+        fb = f + bwd
+        out[name] = {
+            "fwd_ms": round(f, 4), "fwd_bwd_ms": round(fb, 4),
+            "fwd_tokens_per_s": round(tokens / (f * 1e-3), 1) if f else None,
+            "fwd_bwd_tokens_per_s": round(tokens / (fb * 1e-3), 1) if fb else None,
+            "fwd_mfma_frac": round(2 * (dk + dv) * pairs[br] / (f * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4) if f else None,
+            "fwd_bwd_mfma_frac": round(2 * (4 * dk + 3 * dv) * pairs[br] / (fb * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)
+            if fb else None,
+        }
+    return out
+
+
+def sliding_only(dev, steps, warmup):
+    """Benchmark configuration 2: the sliding-window branch alone, fwd+bwd (B=2, H=8,
+    G=2, T=4096, dk=dv=64, window 512, bf16, K in [B,G,dk,T], dK as [B,G,T,dk])."""
+    import torch
+    from nsa import NSAConfig, SlidingWindowAttention
+
+    B, H, G, T, d, win = 2, 8, 2, 4096, 64, 512
+    cfg = NSAConfig(d_model=256, head_dim_qk=d, head_dim_v=d, n_heads=H, n_kv_groups=G, w=win)
+    g = torch.Generator(device=dev).manual_seed(2)
+    q = torch.randn(B, H, T, d, device=dev, generator=g).to(torch.bfloat16).requires_grad_()
+    k = torch.randn(B, G, d, T, device=dev, generator=g).to(torch.bfloat16).requires_grad_()
+    v = torch.randn(B, G, T, d, device=dev, generator=g).to(torch.bfloat16).requires_grad_()
+    do = torch.randn(B, H, T, d, device=dev, generator=g).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(d)
+
+    def step(bwd=True):
+        o = SlidingWindowAttention.apply(q, k, v, scale, win, cfg)
+        if bwd:
+            o.backward(do)
+            q.grad = k.grad = v.grad = None
+
+    def timed(bwd):
+        for _ in range(warmup):
+            step(bwd)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(bwd)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / steps
+
+    fb, f = timed(True), timed(False)
+    pairs = sum(min(t + 1, win) for t in range(T)) * B * H
+    return {"workload": "config 2: sliding window alone, B2 H8 G2 T4096 dk=dv=64 w512 bf16",
+            "value": round(B * T / fb, 1), "fwd_tokens_per_s": round(B * T / f, 1), "ms_per_step": round(fb * 1e3, 4),
+            "fwd_ms": round(f * 1e3, 4),
+            "fwd_bwd_mfma_frac": round(2 * (4 * d + 3 * d) * pairs / fb / 1e12 / PEAK_BF16_TFLOPS, 4)}
 
 
 def time_steps(cfg, mod, w, steps, warmup, backward=True):
@@ -333,6 +395,7 @@ def main():
                      "traffic": measured_traffic(args.config, KERNELS[dominant])},
         "valid_pairs": {"sliding": pairs[0], "compression": pairs[1], "selection": pairs[2]},
         "breakdown_ms": {k: v["ms"] for k, v in breakdown.items()},
+        "per_branch": per_branch(cfg, breakdown, pairs, tokens),
     }
     if not args.no_secondary and args.config == "paper":
         cfg2, mod2, w2 = make_workload("long", dev, seed=1)
@@ -343,6 +406,8 @@ def main():
                                "value": round(t2 / s2, 1), "fwd_tokens_per_s": round(t2 / f2, 1),
                                "ms_per_step": round(s2 * 1e3, 3)}
         del mod2, w2
+    if not args.no_secondary and args.config == "paper":
+        result["config2_sliding"] = sliding_only(dev, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         print("[bench] cpu baseline ...", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.config, args.cpu_rows_per_thread)
