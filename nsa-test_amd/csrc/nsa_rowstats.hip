@@ -3,57 +3,86 @@
 //   lse2  = (M + L) * log2(e)       (+inf when L = -inf: the row saw no key)
 //   delta = sum_d O[d] * dO[d]      (fp32; or the caller's precomputed delta_in)
 //   row_dot (when asked)  = delta   (the gate's gradient, see nsa_attn_rowstats.h)
-// 16 lanes per row, 16-byte pieces of O and dO.
+// 16 lanes per row, 16-byte pieces of O and dO, four rows per lane group.
 #include "nsa_attn.h"
 #include "nsa_device.h"
 #include "nsa_kernels.h"
 
 namespace nsa {
 
+// kStatRows rows per 16-lane group (consecutive timesteps of a head across the groups,
+// so the statistics reads and writes coalesce), all their O / dO pieces requested
+// before any is used
+constexpr int kStatRows = 4;
+
 template <typename T, int DV>
 __global__ __launch_bounds__(256) void row_stats_kernel(AttnArgs a) {
   using S = typename Store<T>::type;
   constexpr int EPF = 16 / (int)sizeof(S);
-  constexpr int NP = DV / EPF;  // 16-byte pieces per row
+  constexpr int NP = (DV / EPF + 15) / 16;  // 16-byte pieces per lane and row
   const int64_t nrows = (int64_t)a.B * a.H * a.Tq;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int l = threadIdx.x & 15;
-  const bool ok = row < nrows;
-  const int64_t r = ok ? row : 0;
-  const int t = (int)(r % a.Tq);
-  const int64_t bh = r / a.Tq;
-  const int h = (int)(bh % a.H), b = (int)(bh / a.H);
-  float dl = 0.f;
+  int64_t r[kStatRows];
+  int b[kStatRows], h[kStatRows], t[kStatRows];
+#pragma unroll
+  for (int k = 0; k < kStatRows; ++k) {
+    const int64_t row = (int64_t)blockIdx.x * (16 * kStatRows) + k * 16 + (threadIdx.x >> 4);
+    r[k] = row < nrows ? row : nrows - 1;  // past the end: the last row again (not stored)
+    t[k] = (int)(r[k] % a.Tq);
+    const int64_t bh = r[k] / a.Tq;
+    h[k] = (int)(bh % a.H);
+    b[k] = (int)(bh / a.H);
+  }
+  float dl[kStatRows];
   if (a.delta_in) {
-    dl = a.delta_in[r];
+#pragma unroll
+    for (int k = 0; k < kStatRows; ++k) dl[k] = a.delta_in[r[k]];
   } else {
-    const S* op = reinterpret_cast<const S*>(a.o) + b * a.so_b + (int64_t)h * a.so_h + (int64_t)t * a.so_t;
-    const S* dp = reinterpret_cast<const S*>(a.dout) + b * a.sdo_b + (int64_t)h * a.sdo_h + (int64_t)t * a.sdo_t;
-    float acc = 0.f;
+    uint4 ov[kStatRows][NP], dv[kStatRows][NP];
 #pragma unroll
-    for (int p = l; p < NP; p += 16) {
-      const uint4 ov = *reinterpret_cast<const uint4*>(op + p * EPF);
-      const uint4 dv = *reinterpret_cast<const uint4*>(dp + p * EPF);
-      const S* o = reinterpret_cast<const S*>(&ov);
-      const S* d = reinterpret_cast<const S*>(&dv);
+    for (int k = 0; k < kStatRows; ++k) {
+      const S* op = reinterpret_cast<const S*>(a.o) + b[k] * a.so_b + (int64_t)h[k] * a.so_h + (int64_t)t[k] * a.so_t;
+      const S* dp = reinterpret_cast<const S*>(a.dout) + b[k] * a.sdo_b + (int64_t)h[k] * a.sdo_h +
+                    (int64_t)t[k] * a.sdo_t;
 #pragma unroll
-      for (int u = 0; u < EPF; ++u) acc = fmaf(Elem<T>::to_f32(o[u]), Elem<T>::to_f32(d[u]), acc);
+      for (int j = 0; j < NP; ++j) {
+        const int p = l + 16 * j;
+        const bool in = p < DV / EPF;
+        ov[k][j] = in ? *reinterpret_cast<const uint4*>(op + p * EPF) : make_uint4(0, 0, 0, 0);
+        dv[k][j] = in ? *reinterpret_cast<const uint4*>(dp + p * EPF) : make_uint4(0, 0, 0, 0);
+      }
     }
 #pragma unroll
-    for (int o = 8; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 16);
-    dl = acc;
+    for (int k = 0; k < kStatRows; ++k) {
+      float acc = 0.f;
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        const S* o = reinterpret_cast<const S*>(&ov[k][j]);
+        const S* d = reinterpret_cast<const S*>(&dv[k][j]);
+#pragma unroll
+        for (int u = 0; u < EPF; ++u) acc = fmaf(Elem<T>::to_f32(o[u]), Elem<T>::to_f32(d[u]), acc);
+      }
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 16);
+      dl[k] = acc;
+    }
   }
-  if (!ok || l != 0) return;
-  const float L = a.L[b * a.sl_b + (int64_t)h * a.sl_h + (int64_t)t * a.sl_t];
-  const float M = a.M[b * a.sm_b + (int64_t)h * a.sm_h + (int64_t)t * a.sm_t];
-  const_cast<float*>(a.lse2)[r] = L == -INFINITY ? INFINITY : (M + L) * kLog2e;
-  const_cast<float*>(a.delta)[r] = dl;
-  if (a.row_dot) a.row_dot[r] = dl;
+  if (l != 0) return;
+#pragma unroll
+  for (int k = 0; k < kStatRows; ++k) {
+    const int64_t row = (int64_t)blockIdx.x * (16 * kStatRows) + k * 16 + (threadIdx.x >> 4);
+    if (row >= nrows) continue;
+    const float L = a.L[b[k] * a.sl_b + (int64_t)h[k] * a.sl_h + (int64_t)t[k] * a.sl_t];
+    const float M = a.M[b[k] * a.sm_b + (int64_t)h[k] * a.sm_h + (int64_t)t[k] * a.sm_t];
+    const_cast<float*>(a.lse2)[r[k]] = L == -INFINITY ? INFINITY : (M + L) * kLog2e;
+    const_cast<float*>(a.delta)[r[k]] = dl[k];
+    if (a.row_dot) a.row_dot[r[k]] = dl[k];
+  }
 }
 
 bool launch_row_stats(int dtype, int dv, const AttnArgs& a, hipStream_t st) {
   const int64_t nrows = (int64_t)a.B * a.H * a.Tq;
-  const dim3 grid((unsigned)((nrows + 15) / 16));
+  const dim3 grid((unsigned)((nrows + 16 * kStatRows - 1) / (16 * kStatRows)));
 #define NSA_ROWSTATS(DVV)                                                                             \
   if (dv == DVV) {                                                                                    \
     if (dtype == kBF16) hipLaunchKernelGGL((row_stats_kernel<bf16, DVV>), grid, dim3(256), 0, st, a); \
