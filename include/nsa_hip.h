@@ -375,6 +375,17 @@ int nsa_gate_act_fwd(const void* gate_in, int64_t sz_b, int64_t sz_h, int64_t sz
 int nsa_gate_act_bwd(const float* gates, const float* row_dots, void* dgate_in, int64_t sz_b, int64_t sz_h,
                      int64_t sz_t, int64_t sz_k, int B, int H, int T, int gate_act, int dtype, nsa_stream_t stream);
 
+/* Row dots of the gated mix for the module backward (no reference counterpart: the
+ * reference's autograd forms d out / d g_k = dout . o_k inside the mix backward,
+ * nsa/kernels.py:2429-2463): dots[k][b][h][t] = sum_d dout[b,h,t,d] * o_k[b,h,t,d] for
+ * k = 0 (o_cmp), 1 (o_sel), 2 (o_win), fp32 contiguous [3,B,H,T], dout read once.  They
+ * feed nsa_gate_act_bwd as row_dots and each branch backward extension as delta_in, so
+ * no branch backward reads its output.  dout and the o_k share the strides so_*, unit
+ * feature stride, 16-byte aligned rows; dv 32, 64 or 128. */
+int nsa_mix_row_dots(const void* dout, const void* o_cmp, const void* o_sel, const void* o_win, int64_t so_b,
+                     int64_t so_h, int64_t so_t, float* dots, int B, int H, int T, int dv, int dtype,
+                     nsa_stream_t stream);
+
 /* ---- compression pooling (compress_tokens, nsa/kernels.py:2119-2208) --------
  * With the first MLP layer split as W1 = [W1k | W1p]:  Y = k W1k^T  [Z,G,T,width],
  * C = E W1p^T + b1  [l,width].  Forward writes R[i] = mean_{u<l} relu(Y[d*i+u] + C[u])

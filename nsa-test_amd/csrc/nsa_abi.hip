@@ -71,10 +71,27 @@ struct Shape {
   int items_per_bg() const { return items_for(seg()); }
   // selection backward with stored dS (bf16, whole 16-head groups, 64-key sub-blocks):
   // the dK/dV kernel runs first and stores dS, the dQ kernel reads it
+  // (selection); sliding window / compression: bf16, whole 16-head groups, dS stored per
+  // (timestep, 32-key chunk it sees)
+  // The dense dS grows with the window / the compressed length (about 2 bytes per
+  // visible (query row, key) pair): beyond kMaxStoredDs the branches recompute dS instead.
+  static constexpr size_t kMaxStoredDs = size_t(6) << 30;
   bool stored_ds() const {
-    return br == kSelection && dtype == NSA_BF16 && hpg() % 16 == 0 && lprime % 64 == 0 && nslots > 0;
+    if (dtype != NSA_BF16 || hpg() % 16) return false;
+    if (br == kSelection) return lprime % 64 == 0 && nslots > 0;
+    return dense_ds_bytes() <= kMaxStoredDs;
   }
-  size_t ds_bytes() const { return stored_ds() ? (size_t)Z * H * Tq * nslots * lprime * 2 : 0; }
+  size_t dense_ds_bytes() const { return (size_t)Z * G * Tq * (hpg() / 16) * ds_nch() * 1024; }
+  // dense: 32-key chunks stored per (timestep, head group)
+  int ds_nch() const {
+    const int all = (Tkv + 31) / 32;
+    return br == kSliding ? min((window + 62) / 32, all + 1) : all;
+  }
+  size_t ds_bytes() const {
+    if (!stored_ds()) return 0;
+    if (br == kSelection) return (size_t)Z * H * Tq * nslots * lprime * 2;
+    return dense_ds_bytes();
+  }
 };
 
 struct Layout {
@@ -119,6 +136,7 @@ Layout make_layout(const Shape& s, bool bwd) {
       }
     }
   }
+  if (bwd && s.br != kSelection && s.stored_ds()) L.ds = take(s.ds_bytes());
   if (bwd && !s.direct()) L.partial = take(BG * s.items_per_bg() * dkdv_keys(s.br) * (size_t)(s.dk + s.dv) * 4);
   L.total = off;
   return L;
@@ -362,8 +380,9 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   // stored dS: the row statistics first, then dK/dV (which stores dS), then dQ from it;
   // otherwise the dQ kernel computes the statistics and dK/dV follows
   if (s.stored_ds()) {
-    a.csr_s = at<int>(ws, L.csr_s);
+    if (s.br == kSelection) a.csr_s = at<int>(ws, L.csr_s);
     a.ds = at<char>(ws, L.ds);
+    a.ds_nch = s.ds_nch();
     {
       TimingScope ts(kIdPrep, st);
       if (!launch_row_stats(s.dtype, s.dv, a, st)) return fail(NSA_ERR_UNSUPPORTED, "no row statistics kernel");

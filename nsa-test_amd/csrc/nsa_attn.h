@@ -95,7 +95,12 @@ struct AttnArgs {
   // kernel writes every (timestep, slot) pair's dS in the MFMA operand order of the dQ
   // product, and the dQ kernel reads it instead of recomputing S and dP:
   //   ds[b,g][t][slot][64-key sub-block][16-head group] = 2 fragments x 64 lanes x 8 bf16
+  // and the same for the sliding-window / compression backward, per 32-key chunk:
+  //   ds[b,g][t][16-head group][ds_nch chunks from the timestep's first visible one]
+  //   = 64 lanes x 8 bf16 (sliding: chunks from max(0, t - window + 1) / 32; compression:
+  //   from chunk 0)
   void* ds;
+  int ds_nch;
 };
 
 template <typename T, int DK, int DV, int BR>

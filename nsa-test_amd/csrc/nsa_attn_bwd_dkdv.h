@@ -13,12 +13,14 @@
 // two rows at once, and the transposed row pitch (RC + 4) keeps those writes free of
 // bank conflicts.
 //
-// Selection, bf16, heads per group a multiple of 16 (a.ds set): the kernel also stores
-// every (timestep, slot) pair's dS for the dQ kernel, which then needs no S / dP
-// recomputation.  A 16-row subtile is the 16 heads of one head group of one entry; the
-// wave's 16 x 16 dS tile goes through LDS ([key][head], written as the lane's four
-// heads of one key) and comes back through the transpose load as the lane's four keys
-// of one head, which is exactly its share of the dQ product's dS^T operand fragment.
+// bf16, heads per group a multiple of 16 (a.ds set): the kernel also stores the dS it
+// forms (selection: per (timestep, slot) pair; sliding window / compression: per
+// (timestep, 32-key chunk) the timestep sees) for the dQ kernel, which then needs no
+// S / dP recomputation.  A 16-row subtile is the 16 heads of one head group of one
+// entry / timestep; every wave writes its 16 x 16 dS tiles into a per-chunk LDS tile
+// ([key][head], the lane's four heads of one key), and after the next chunk's barrier
+// each wave stores one whole 1 KB fragment of it, read back with two transpose loads as
+// the lane's eight keys of one head: its share of the dQ product's dS^T operand.
 //
 // Every item writes its fp32 dK/dV partial for its keys; a reduce kernel sums the
 // segments of each key tile in a fixed order and accumulates into the caller's dK/dV.
@@ -121,8 +123,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   __shared__ int s_tl[kSegTMax];  // selection: the item's query timesteps
   // stored dS (selection, bf16): the entries' slots and one 16 x 16 transpose tile per
   // wave and row subtile
-  constexpr bool kStoreDs = BR == kSelection && sizeof(S) == 2;
-  __shared__ int s_sl[kStoreDs ? kSegTMax : 1];
+  constexpr bool kStoreDs = sizeof(S) == 2;
+  __shared__ int s_sl[kStoreDs && BR == kSelection ? kSegTMax : 1];
   // [chunk parity][row subtile][64 keys][16 heads]: a chunk's dS tiles, written by the
   // four waves (their 16 keys each) and stored after the next chunk's barrier
   __shared__ __attribute__((aligned(16))) uint16_t s_dst[kStoreDs ? 2 : 1][RC / 16][kStoreDs ? KEYS * 16 : 1];
@@ -368,10 +370,30 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   };
 
   // stored dS of chunk cp (after a barrier that follows its tile writes): wave w stores
-  // fragment (w & 1) of row subtile w >> 1, lane (g4, c16) reading head c16 at the
+  // one 32-key fragment of one row subtile (selection: fragment w & 1 of subtile w >> 1;
+  // otherwise fragment w & 3 of subtile w >> 2), lane (g4, c16) reading head c16 at the
   // 32-key chunk's keys 4 g4 + i and 16 + 4 g4 + i (its 8 slots) with two transpose loads
   auto flush_ds = [&](int cp) __attribute__((always_inline)) {
-    if constexpr (kStoreDs) {
+    if constexpr (kStoreDs && BR != kSelection) {
+      const int rs = wave >> 2, kq = wave & 3;
+      const int fr = f_lo + cp * RC + rs * 16;  // the subtile's rows: 16 heads of one timestep
+      if (!a.ds || fr >= f_hi) return;           // wave-uniform
+      const int t = hdiv.div(fr);
+      const int hg = (fr - t * hpg) >> 4;
+      const int kg = (key0 >> 5) + kq;  // the 32-key chunk
+      int rel = kg;                     // its index among the timestep's stored chunks
+      if (BR == kSliding) {             // chunks holding a key of (t - window, t]
+        rel = kg - (max(0, t - a.window + 1) >> 5);
+        if (rel < 0 || kg > (min(t, a.Tkv - 1) >> 5)) return;
+      } else if (s_be[kq * 32] > t) {   // no key of the chunk visible (ascending block ends)
+        return;
+      }
+      const uint4 v = ld_tr_pair(&s_dst[cp & 1][rs][(kq * 32 + 4 * g4 + (c16 >> 2)) * 16 + 4 * (c16 & 3)], 16 * 16);
+      uint16_t* dsp = reinterpret_cast<uint16_t*>(a.ds) +
+                      ((((int64_t)bg * a.Tq + t) * (hpg >> 4) + hg) * a.ds_nch + rel) * 512 + lane * 8;
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, v), reinterpret_cast<u32x4*>(dsp));
+    }
+    if constexpr (kStoreDs && BR == kSelection) {
       const int rs = wave >> 1, kc2 = wave & 1;
       const int fr = f_lo + cp * RC + rs * 16;  // the subtile's rows: 16 heads of one entry
       if (!a.ds || fr >= f_hi) return;           // wave-uniform

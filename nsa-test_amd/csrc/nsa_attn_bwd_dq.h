@@ -270,11 +270,138 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) 
   }
 }
 
+// ============================ dQ from the stored dS =============================
+// Sliding window / compression, bf16, heads per group a multiple of 16, after the dK/dV
+// kernel has stored dS per (timestep, 32-key chunk).  The workgroup walks the 64-key
+// tiles of its columns' key span as the dQ kernel above does, with only the K^T
+// colfrags of a tile in LDS (direct-to-LDS copies, double-buffered); each wave (the
+// 16 heads of one head group at one timestep) reads its two stored dS fragments of the
+// tile from HBM, one tile ahead, zeros for chunks its timestep does not see, and runs
+// the one product dQ^T += K^T dS^T.  The stored dS carries the row gate: the epilogue
+// scales by sm_scale only.
+template <typename T, int DK, int BR>
+__global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_ds_kernel(AttnArgs a) {
+  static_assert(BR == kSliding || BR == kCompression, "dense branches");
+  using S = typename Store<T>::type;
+  static_assert(sizeof(S) == 2, "stored dS is bf16");
+  constexpr int EPF = Elem<T>::kPerFrag;
+  constexpr int NW = kDqWaves;
+  constexpr int NTF = 2 * (DK / 16);  // K^T colfrags of a 64-key tile (kc2, j)
+  extern __shared__ __attribute__((aligned(16))) uint4 dqds_lds[];  // [2][NTF][64]
+  __shared__ int s_misc[4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4;
+  const int c16 = lane & 15;
+  const int bg = blockIdx.y;
+  const int b = bg / a.G;
+  const int grp = bg % a.G;
+  const int hpg = a.hpg;
+  const int ncols = a.Tq * hpg;
+  const int col_base = blockIdx.x * kDqCols;
+  const int t_first = col_base / hpg;
+  const int t_last = min(a.Tq - 1, (col_base + kDqCols - 1) / hpg);
+  const S* kcf = reinterpret_cast<const S*>(a.kcf) + (int64_t)bg * DK * a.Tp;
+
+  // the wave's 16 columns: one head group at one timestep
+  const int f0 = col_base + wave * 16;
+  const bool wv = f0 < ncols;
+  const int t = wv ? f0 / hpg : t_first;
+  const int hg = (f0 - t * hpg) >> 4;
+  const int colh = grp * hpg + (f0 - t * hpg) + c16;
+  // the timestep's stored chunks: sliding [c_lo, c_hi]; compression those whose first
+  // key is visible (block ends ascend)
+  const int c_lo = BR == kSliding ? max(0, t - a.window + 1) >> 5 : 0;
+  const int c_hi = BR == kSliding ? (min(t, a.Tkv - 1) >> 5) : 0x7fffffff;
+  const S* dsb = reinterpret_cast<const S*>(a.ds) + (((int64_t)bg * a.Tq + t) * (hpg >> 4) + hg) * a.ds_nch * 512;
+
+  int ntiles = 0, key_lo = 0;
+  if (BR == kSliding) {
+    key_lo = max(0, t_first - a.window + 1) & ~31;
+    const int hi = min(t_last, a.Tkv - 1);
+    ntiles = hi >= key_lo ? (hi - key_lo) / 64 + 1 : 0;
+  } else {
+    if (tid == 0) s_misc[0] = 0;
+    __syncthreads();
+    int mx = 0;
+    for (int i = tid; i < a.Tkv; i += blockDim.x)
+      if (a.block_ends[i] <= t_last) mx = i + 1;
+    if (mx) atomicMax(&s_misc[0], mx);
+    __syncthreads();
+    ntiles = (s_misc[0] + 63) / 64;
+  }
+  auto tile_key0 = [&](int it) -> int { return BR == kSliding ? key_lo + it * 64 : it * 64; };
+  auto copy_tile = [&](int key0, int buf) __attribute__((always_inline)) {
+    uint4* dst = dqds_lds + buf * NTF * 64;
+    for (int fr = wave; fr < NTF; fr += NW) {
+      const int kc2 = fr / (DK / 16), j = fr % (DK / 16);
+      copy16_to_lds(kcf + ((((int64_t)(key0 >> 5) + kc2) * (DK / 16) + j) * 64 + lane) * EPF, dst + fr * 64);
+    }
+  };
+  // the wave's dS fragments of the tile at key0 (zero for chunks it does not see)
+  auto load_ds = [&](int key0, u32x4 (&df)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kc2 = 0; kc2 < 2; ++kc2) {
+      const int kg = (key0 >> 5) + kc2;
+      bool vis = wv && kg >= c_lo && kg <= c_hi && kg * 32 < a.Tkv;
+      if (BR == kCompression && vis) vis = a.block_ends[kg * 32] <= t;
+      df[kc2] = vis ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(dsb + (int64_t)(kg - c_lo) * 512 + lane * EPF))
+                    : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+
+  f32x4 dqa[DK / 16];
+#pragma unroll
+  for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
+  u32x4 df[2], dfn[2];
+  if (ntiles > 0) {
+    copy_tile(tile_key0(0), 0);
+    load_ds(tile_key0(0), df);
+  }
+  for (int it = 0; it < ntiles; ++it) {
+    const int buf = it & 1;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of tile it (and its dS) have landed
+    __syncthreads();                // every wave's have; tile it-1 is no longer read
+    if (it + 1 < ntiles) {
+      copy_tile(tile_key0(it + 1), buf ^ 1);
+      load_ds(tile_key0(it + 1), dfn);
+    }
+    const uint4* tb = dqds_lds + buf * NTF * 64;
+#pragma unroll
+    for (int kc2 = 0; kc2 < 2; ++kc2)
+#pragma unroll
+      for (int j = 0; j < DK / 16; ++j)
+        dqa[j] = Mma<T>::run(dqa[j], tb[(kc2 * (DK / 16) + j) * 64 + lane], __builtin_bit_cast(uint4, df[kc2]));
+    df[0] = dfn[0];
+    df[1] = dfn[1];
+  }
+  if (!wv) return;
+  S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)t * a.sdq_t;
+#pragma unroll
+  for (int j = 0; j < DK / 16; ++j) {
+    f32x4 v = dqa[j] * a.scale;
+    if (a.dq_acc) v += load4<T>(dqp + j * 16 + 4 * g4);  // the caller's running dQ sum
+    store4<T>(dqp + j * 16 + 4 * g4, v);
+  }
+}
+
 template <typename T, int DK, int DV, int BR>
 void launch_attn_bwd_dq(const AttnArgs& a, hipStream_t s) {
   if constexpr (BR == kSelection) {
     launch_attn_sel_dq<T, DK, DV>(a, s);  // per-wave selection kernel
   } else {
+    if constexpr (sizeof(typename Store<T>::type) == 2) {
+      if (a.ds) {
+        const size_t lds = (size_t)2 * 2 * (DK / 16) * 1024;
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_ds_kernel<T, DK, BR>),
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        dim3 grid((a.Tq * a.hpg + kDqCols - 1) / kDqCols, a.B * a.G);
+        hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<T, DK, BR>), grid, dim3(64 * kDqWaves), lds, s, a);
+        return;
+      }
+    }
     using TL = DqTile<T, DK, DV>;
     const size_t lds = (size_t)TL::NBUF * TL::BYTES;
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_kernel<T, DK, DV, BR>),

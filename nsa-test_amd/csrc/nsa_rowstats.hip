@@ -4,6 +4,7 @@
 //   delta = sum_d O[d] * dO[d]      (fp32; or the caller's precomputed delta_in)
 //   row_dot (when asked)  = delta   (the gate's gradient, see nsa_attn_rowstats.h)
 // 16 lanes per row, 16-byte pieces of O and dO, four rows per lane group.
+#include "../../include/nsa_hip.h"
 #include "nsa_attn.h"
 #include "nsa_device.h"
 #include "nsa_kernels.h"
@@ -96,4 +97,99 @@ bool launch_row_stats(int dtype, int dv, const AttnArgs& a, hipStream_t st) {
   return false;
 }
 
+// Row dots of the gated mix (the module backward): dots[k][row] = sum_d dout . o_k for
+// the three branch outputs, dout read once.  They are the gate gradient's inputs and the
+// branches' delta_in, so no branch backward reads its output again.  Same lane layout
+// as row_stats_kernel.
+template <typename T, int DV>
+__global__ __launch_bounds__(256) void mix_row_dots_kernel(const void* dout, const void* o0, const void* o1,
+                                                           const void* o2, int64_t s_b, int64_t s_h, int64_t s_t,
+                                                           float* dots, int B, int H, int Tq) {
+  using S = typename Store<T>::type;
+  constexpr int EPF = 16 / (int)sizeof(S);
+  constexpr int NP = (DV / EPF + 15) / 16;
+  const int64_t nrows = (int64_t)B * H * Tq;
+  const int l = threadIdx.x & 15;
+  const S* src[4] = {reinterpret_cast<const S*>(dout), reinterpret_cast<const S*>(o0), reinterpret_cast<const S*>(o1),
+                     reinterpret_cast<const S*>(o2)};
+  int64_t r[kStatRows], off[kStatRows];
+#pragma unroll
+  for (int k = 0; k < kStatRows; ++k) {
+    const int64_t row = (int64_t)blockIdx.x * (16 * kStatRows) + k * 16 + (threadIdx.x >> 4);
+    r[k] = row < nrows ? row : nrows - 1;
+    const int t = (int)(r[k] % Tq);
+    const int64_t bh = r[k] / Tq;
+    off[k] = (bh / H) * s_b + (bh % H) * s_h + (int64_t)t * s_t;
+  }
+  uint4 v[4][kStatRows][NP];
+#pragma unroll
+  for (int x = 0; x < 4; ++x)
+#pragma unroll
+    for (int k = 0; k < kStatRows; ++k)
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        const int p = l + 16 * j;
+        v[x][k][j] = p < DV / EPF ? *reinterpret_cast<const uint4*>(src[x] + off[k] + p * EPF) : make_uint4(0, 0, 0, 0);
+      }
+  const int64_t plane = nrows;
+#pragma unroll
+  for (int k = 0; k < kStatRows; ++k) {
+    float acc[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const S* d = reinterpret_cast<const S*>(&v[0][k][j]);
+#pragma unroll
+      for (int x = 0; x < 3; ++x) {
+        const S* o = reinterpret_cast<const S*>(&v[x + 1][k][j]);
+#pragma unroll
+        for (int u = 0; u < EPF; ++u) acc[x] = fmaf(Elem<T>::to_f32(o[u]), Elem<T>::to_f32(d[u]), acc[x]);
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < 3; ++x)
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) acc[x] += __shfl_xor(acc[x], o, 16);
+    const int64_t row = (int64_t)blockIdx.x * (16 * kStatRows) + k * 16 + (threadIdx.x >> 4);
+    if (l == 0 && row < nrows) {
+#pragma unroll
+      for (int x = 0; x < 3; ++x) dots[x * plane + row] = acc[x];
+    }
+  }
+}
+
 }  // namespace nsa
+
+extern "C" int nsa_mix_row_dots(const void* dout, const void* o_cmp, const void* o_sel, const void* o_win,
+                                int64_t so_b, int64_t so_h, int64_t so_t, float* dots, int B, int H, int T, int dv,
+                                int dtype, nsa_stream_t stream) {
+  using namespace nsa;
+  if (dtype != NSA_F32 && dtype != NSA_BF16) return set_error(NSA_ERR_INVALID, "dtype not supported");
+  if (B < 0 || H < 0 || T < 0) return set_error(NSA_ERR_INVALID, "bad shape");
+  const int64_t nrows = (int64_t)B * H * T;
+  if (nrows == 0) return NSA_OK;
+  if (!dout || !o_cmp || !o_sel || !o_win || !dots) return set_error(NSA_ERR_INVALID, "null pointer");
+  const int esz = dtype == NSA_F32 ? 4 : 2;
+  const void* ptrs[4] = {dout, o_cmp, o_sel, o_win};
+  for (const void* p : ptrs)
+    if ((uintptr_t)p % 16) return set_error(NSA_ERR_LAYOUT, "rows must be 16-byte aligned");
+  if ((so_t * esz) % 16 || (so_h * esz) % 16 || (so_b * esz) % 16)
+    return set_error(NSA_ERR_LAYOUT, "rows must be 16-byte aligned");
+  const dim3 grid((unsigned)((nrows + 16 * kStatRows - 1) / (16 * kStatRows)));
+  hipStream_t st = (hipStream_t)stream;
+#define NSA_DOTS(DVV)                                                                                             \
+  if (dv == DVV) {                                                                                                \
+    if (dtype == NSA_BF16)                                                                                        \
+      hipLaunchKernelGGL((mix_row_dots_kernel<bf16, DVV>), grid, dim3(256), 0, st, dout, o_cmp, o_sel, o_win, so_b, \
+                         so_h, so_t, dots, B, H, T);                                                              \
+    else                                                                                                          \
+      hipLaunchKernelGGL((mix_row_dots_kernel<float, DVV>), grid, dim3(256), 0, st, dout, o_cmp, o_sel, o_win,    \
+                         so_b, so_h, so_t, dots, B, H, T);                                                        \
+    hipError_t e = hipGetLastError();                                                                             \
+    return e == hipSuccess ? NSA_OK : set_error(NSA_ERR_HIP, hipGetErrorString(e));                              \
+  }
+  NSA_DOTS(32)
+  NSA_DOTS(64)
+  NSA_DOTS(128)
+#undef NSA_DOTS
+  return set_error(NSA_ERR_UNSUPPORTED, "head_dim_v must be 32, 64 or 128");
+}

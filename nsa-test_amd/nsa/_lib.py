@@ -69,6 +69,7 @@ SIGNATURES.update({
     "nsa_gate_mix_bwd": (_I, [_P] + [_L] * 3 + [_P] * 3 + [_L] * 3 + [_P] + [_L] * 4 + [_P] * 5 + [_I] * 6 + [_P]),
     "nsa_gate_act_fwd": (_I, [_P] + [_L] * 4 + [_P] + [_I] * 5 + [_P]),
     "nsa_gate_act_bwd": (_I, [_P] * 3 + [_L] * 4 + [_I] * 5 + [_P]),
+    "nsa_mix_row_dots": (_I, [_P] * 4 + [_L] * 3 + [_P] + [_I] * 5 + [_P]),
     "nsa_compress_pool_fwd": (_I, [_P] * 5 + [_I] * 9 + [_P]),
     "nsa_compress_pool_bwd": (_I, [_P] * 7 + [_I] * 9 + [_P]),
     "nsa_bwd_dkdv_plan": (_I, [_I] * 9 + [_P, _P]),

@@ -331,14 +331,20 @@ class NSACore(torch.autograd.Function):
             d = dout.to(o_c.dtype)
             if d.stride() != o_c.stride():  # one copy into the branch outputs' layout
                 d = torch.empty_like(o_c).copy_(d)
+            # r_k = sum_d dout . o_k for the three branches in one pass (dout read once): the
+            # gate gradient's inputs and each branch's row sums, so no branch reads o_k again
             rdot = torch.empty(g.shape, device=q.device, dtype=torch.float32)  # [3,B,H,T]
+            B, H, T = q.shape[:3]
+            _lib.call("nsa_mix_row_dots", _ops._ptr(d), _ops._ptr(o_c), _ops._ptr(o_s), _ops._ptr(o_w),
+                      *o_c.stride()[:3], _ops._ptr(rdot), B, H, T, o_c.shape[-1], _ops._dtype_code(d.dtype),
+                      _ops._stream(q.device))
             _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, d, Lc, Mc, sc, block_ends=be, dq=dq,
-                                        row_gate=g[0], row_dot=rdot[0])
+                                        row_gate=g[0], delta=rdot[0])
             _, dks, dvs = _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, d, Ls, Ms, sc, indices=idx,
                                         lprime=ctx.lprime, fallback=True, dq=dq, dq_accumulate=True, row_gate=g[1],
-                                        row_dot=rdot[1])
+                                        delta=rdot[1])
             _, dkw, dvw = _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, d, Lw, Mw, sc, window=ctx.window, dq=dq,
-                                        dq_accumulate=True, row_gate=g[2], row_dot=rdot[2])
+                                        dq_accumulate=True, row_gate=g[2], delta=rdot[2])
             dg = _gate_activation_grad(g, rdot, ctx.act, ctx.gdtype)
         else:
             dos, dg, deltas = _mix_bwd(dout, [o_c, o_s, o_w], g, want_delta=True, act=ctx.act)

@@ -66,6 +66,9 @@ SLIDING_CASES = [
     (1, 8, 2, 700, 128, 128, 512, torch.bfloat16),
     (1, 6, 3, 96, 48, 48, 40, torch.float32),     # head dims zero-padded to a compiled pair
     (1, 6, 2, 333, 64, 64, 70, torch.bfloat16),   # 3 heads per group (not a power of two)
+    # bf16 with whole 16-head groups: dQ from the dS the dK/dV kernel stores
+    (1, 64, 2, 300, 64, 64, 40, torch.bfloat16),  # two head groups, a window shorter than a tile
+    (2, 16, 1, 457, 128, 128, 200, torch.bfloat16),  # ragged T, window not a multiple of 32
 ]
 
 
@@ -94,6 +97,7 @@ COMPRESSION_CASES = [
     (1, 4, 2, 20, 64, 64, 32, 16, torch.float32),  # no row sees a block: all zero, L = -inf
     (1, 4, 1, 5000, 128, 128, 32, 16, torch.bfloat16),
     (1, 6, 2, 400, 64, 64, 32, 16, torch.bfloat16),  # 3 heads per group
+    (1, 32, 1, 777, 64, 64, 32, 16, torch.bfloat16),  # stored dS, two head groups, ragged T
 ]
 
 

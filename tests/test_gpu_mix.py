@@ -67,3 +67,21 @@ def test_gate_activation_matches_torch(dev, act, dtype):
     gref = gref.permute(1, 2, 3, 0)
     assert dz.shape == (B, H, T, 3) and dz.dtype == dtype
     assert _rel(dz.double().cpu().numpy(), gref.cpu().numpy()) < (1e-6 if dtype == torch.float32 else 1e-2)
+
+
+@pytest.mark.parametrize("B,H,T,dv,dtype", [(1, 16, 300, 128, torch.bfloat16), (2, 4, 77, 64, torch.float32),
+                                             (1, 8, 1000, 32, torch.bfloat16)])
+def test_mix_row_dots(dev, B, H, T, dv, dtype):
+    """nsa_mix_row_dots: dots[k] = sum_d dout . o_k for the three branch outputs, read in
+    the module's [B,T,H,dv] storage, against float64 torch on the same values."""
+    from nsa import _lib, _ops
+
+    g = torch.Generator().manual_seed(7)
+    ts = [torch.randn(B, T, H, dv, generator=g).to(dtype).to(dev).permute(0, 2, 1, 3) for _ in range(4)]
+    d, o = ts[0], ts[1:]
+    dots = torch.empty(3, B, H, T, device=dev, dtype=torch.float32)
+    _lib.call("nsa_mix_row_dots", *[_ops._ptr(t) for t in ts], *d.stride()[:3], _ops._ptr(dots), B, H, T, dv,
+              _ops._dtype_code(dtype), _ops._stream(dev))
+    torch.cuda.synchronize()
+    ref = torch.stack([(d.double() * x.double()).sum(-1) for x in o])
+    assert _rel(dots.double().cpu().numpy(), ref.cpu().numpy()) < 1e-6

@@ -107,14 +107,23 @@ def test_ctypes_signatures_match_header():
 
 def test_workspace_sizes():
     f = _lib.size("nsa_fwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64)
-    b = _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 512)
+    b = _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_F32, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 512)
     assert 0 < f < b
     # with >= 256 key tiles (Z*G*tiles) the sliding dK/dV adds straight into dK/dV:
-    # a wider window needs no partials then
-    assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 8192) == b
+    # a wider window needs no partials then (fp32: no stored dS)
+    assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_F32, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 8192) == b
     # with fewer tiles a wider window spreads each key tile over more query segments
-    b1 = _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 16, 1, 8192, 8192, 192, 128, 0, 64, 512)
-    assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 16, 1, 8192, 8192, 192, 128, 0, 64, 8192) > b1
+    b1 = _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_F32, 1, 16, 1, 8192, 8192, 192, 128, 0, 64, 512)
+    assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_F32, 1, 16, 1, 8192, 8192, 192, 128, 0, 64, 8192) > b1
+    # bf16 with whole 16-head groups: the sliding window's dS stored per (timestep, head
+    # group, 32-key chunk it sees: min((w + 62) / 32, T / 32 + 1) of them, 1 KB each);
+    # a window whose dS would exceed 6 GiB recomputes it instead (w = 8192: 8.6 GB)
+    tp = 8192 + 64
+    kv = 4 * tp * (2 * 192 + 128) * 2  # bf16 K rowfrag + K colfrag + V rowfrag copies
+    b16 = _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 512)
+    ds = 4 * 8192 * ((512 + 62) // 32) * 1024
+    assert b16 - (b - kv) == ds
+    assert _lib.size("nsa_bwd_workspace_size", 0, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 0, 64, 8192) == b16 - ds
     s = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_BF16, 1, 64, 4, 8192, 8192, 192, 128, 16, 64, 1)
     assert s > f
     # selection, bf16, 16 heads per group: the stored dS (2 bytes per (row, slot, key of
