@@ -95,7 +95,7 @@ struct Shape {
 };
 
 struct Layout {
-  size_t krf = 0, kcf = 0, vrf = 0, vcf = 0, lse2 = 0, delta = 0, clean = 0, chunk = 0, csr_off = 0, csr_t = 0,
+  size_t krf = 0, kcf = 0, vrf = 0, vcf = 0, rstat = 0, clean = 0, chunk = 0, csr_off = 0, csr_t = 0,
          seg_off = 0, csr_s = 0, ds = 0, partial = 0, total = 0;
 };
 
@@ -120,8 +120,7 @@ Layout make_layout(const Shape& s, bool bwd) {
     L.vcf = take(vbytes);
   }
   if (bwd) {
-    L.lse2 = take((size_t)s.Z * s.H * s.Tq * 4);
-    L.delta = take((size_t)s.Z * s.H * s.Tq * 4);
+    L.rstat = take((size_t)s.Z * s.H * s.Tq * 16);
   }
   if (s.br == kSelection) {
     L.clean = take(BG * s.Tq * s.nslots * 4);
@@ -349,8 +348,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.krf = at<char>(ws, L.krf);
   a.kcf = at<char>(ws, L.kcf);
   a.vrf = at<char>(ws, L.vrf);
-  a.lse2 = at<float>(ws, L.lse2);
-  a.delta = at<float>(ws, L.delta);
+  a.rstat = at<float4>(ws, L.rstat);
   a.items_per_bg = s.items_per_bg();
   a.seg = s.seg();
   a.direct = s.direct() ? 1 : 0;

@@ -62,8 +62,10 @@ struct AttnArgs {
   const void* mix_o0;  // the other two branch outputs, with Out's strides
   const void* mix_o1;
   const float* mix_gates;  // [3,B,H,Tq] compact fp32 activated gates (0, 1: mix_o0 / mix_o1, 2: Out)
-  const float* lse2;   // [B,H,Tq] compact: (M+L)*log2(e), +inf for empty rows
-  const float* delta;  // [B,H,Tq] compact: rowsum(O*dO)
+  // per query row, for the dK/dV kernels: {lse2 = (M+L)*log2(e) (+inf for empty rows),
+  // delta = rowsum(O*dO), gate (1 without a row gate), 0}, in [B*G][Tq][hpg] order so the
+  // heads of one timestep share cache lines
+  float4* rstat;
   // dK/dV destination (accumulated into, or overwritten with dkdv_ow; any strides) or fp32 partials
   void* dk;
   int64_t sdk_b, sdk_g, sdk_t, sdk_d;

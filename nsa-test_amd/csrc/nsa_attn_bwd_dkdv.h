@@ -252,14 +252,12 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   struct Stage {
     uint4 pq[NQ][2], po[NO][2];
     int t;
-    float l2, dl, g;
+    float4 st;  // lse2, delta, gate
   };
   constexpr int kDepth = kTr ? 2 : 1;
   Stage stg0, stg1;
   stg0.t = stg1.t = -1;
-  stg0.l2 = stg1.l2 = INFINITY;
-  stg0.dl = stg1.dl = 0.f;
-  stg0.g = stg1.g = 1.f;
+  stg0.st = stg1.st = make_float4(INFINITY, 0.f, 1.f, 0.f);
   // Rows past the item's end re-read its last row (finite data); they are masked
   // (p = 0) through s_t = -1, so every load is unconditional and the loads of a chunk
   // issue back to back.
@@ -313,10 +311,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
       const int fe = min(f, f_hi - 1);
       const int t = row_t(fe);
       const int h = grp * hpg + hdiv.mod(fe);
-      const int64_t srow = ((int64_t)b * a.H + h) * a.Tq + t;
-      sg.l2 = a.lse2[srow];
-      sg.dl = a.delta[srow];
-      sg.g = a.row_gate ? a.row_gate[srow] : 1.f;
+      (void)h;
+      // one 16-byte record per row; the heads of a timestep are adjacent
+      sg.st = a.rstat[((int64_t)bg * a.Tq + t) * hpg + hdiv.mod(fe)];
       sg.t = f < f_hi ? t : -1;
     }
   };
@@ -363,9 +360,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     }
     if (tid < RC) {
       s_t[buf][tid] = sg.t;
-      s_l2[buf][tid] = sg.l2;
-      s_dl[buf][tid] = sg.dl;
-      s_g[buf][tid] = sg.g;
+      s_l2[buf][tid] = sg.st.x;
+      s_dl[buf][tid] = sg.st.y;
+      s_g[buf][tid] = sg.st.z;
     }
   };
 

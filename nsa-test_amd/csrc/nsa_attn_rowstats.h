@@ -6,8 +6,8 @@
 // so the kernels keep D = sum_d O dO unscaled, multiply dQ by g at the end and the
 // probabilities of dK / dV by g per row; row_dot (when given) receives that unscaled D,
 // the gate's own gradient.
-// The dQ kernels use them directly and store them for the dK/dV kernel, which runs
-// after dQ on the same stream (one pass over O fewer than a separate statistics
+// The dQ kernels use them directly and store them (AttnArgs::rstat) for the dK/dV
+// kernel, which runs after dQ on the same stream (one pass over O fewer than a separate statistics
 // kernel: dO is already in the dQ kernel's registers).
 #pragma once
 #include "nsa_attn.h"
@@ -49,8 +49,8 @@ __device__ __forceinline__ void dq_row_stats(const AttnArgs& a, int b, int colh,
     const float M = a.M[b * a.sm_b + (int64_t)colh * a.sm_h + (int64_t)colt * a.sm_t];
     l2 = L == -INFINITY ? INFINITY : (M + L) * kLog2e;
     if (g4 == 0) {
-      const_cast<float*>(a.delta)[srow] = dl;
-      const_cast<float*>(a.lse2)[srow] = l2;
+      const int hh = colh % a.hpg;  // the head within its group
+      a.rstat[((int64_t)(b * a.G + colh / a.hpg) * a.Tq + colt) * a.hpg + hh] = make_float4(l2, dl, gate, 0.f);
       if (a.row_dot) a.row_dot[srow] = dl;
     }
   }

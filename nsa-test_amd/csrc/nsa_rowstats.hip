@@ -1,8 +1,9 @@
-// Backward row statistics as a pass of their own, for the branches whose dK/dV kernel
-// runs before the dQ kernel (the selection backward with stored dS): per query row
+// Backward row statistics as a pass of their own, for the backwards whose dK/dV kernel
+// runs before the dQ kernel (stored dS): per query row the record AttnArgs::rstat
 //   lse2  = (M + L) * log2(e)       (+inf when L = -inf: the row saw no key)
 //   delta = sum_d O[d] * dO[d]      (fp32; or the caller's precomputed delta_in)
-//   row_dot (when asked)  = delta   (the gate's gradient, see nsa_attn_rowstats.h)
+//   gate  = row_gate[row]           (1 without a row gate)
+// and row_dot (when asked) = delta (the gate's gradient, see nsa_attn_rowstats.h).
 // 16 lanes per row, 16-byte pieces of O and dO, four rows per lane group.
 #include "../../include/nsa_hip.h"
 #include "nsa_attn.h"
@@ -35,10 +36,7 @@ __global__ __launch_bounds__(256) void row_stats_kernel(AttnArgs a) {
     b[k] = (int)(bh / a.H);
   }
   float dl[kStatRows];
-  if (a.delta_in) {
-#pragma unroll
-    for (int k = 0; k < kStatRows; ++k) dl[k] = a.delta_in[r[k]];
-  } else {
+  {
     uint4 ov[kStatRows][NP], dv[kStatRows][NP];
 #pragma unroll
     for (int k = 0; k < kStatRows; ++k) {
@@ -75,14 +73,36 @@ __global__ __launch_bounds__(256) void row_stats_kernel(AttnArgs a) {
     if (row >= nrows) continue;
     const float L = a.L[b[k] * a.sl_b + (int64_t)h[k] * a.sl_h + (int64_t)t[k] * a.sl_t];
     const float M = a.M[b[k] * a.sm_b + (int64_t)h[k] * a.sm_h + (int64_t)t[k] * a.sm_t];
-    const_cast<float*>(a.lse2)[r[k]] = L == -INFINITY ? INFINITY : (M + L) * kLog2e;
-    const_cast<float*>(a.delta)[r[k]] = dl[k];
+    const float gate = a.row_gate ? a.row_gate[r[k]] : 1.f;
+    a.rstat[((int64_t)(b[k] * a.G + h[k] / a.hpg) * a.Tq + t[k]) * a.hpg + h[k] % a.hpg] =
+        make_float4(L == -INFINITY ? INFINITY : (M + L) * kLog2e, dl[k], gate, 0.f);
     if (a.row_dot) a.row_dot[r[k]] = dl[k];
   }
 }
 
+// With the caller's row sums (delta_in) nothing is read per feature: one thread per row,
+// rows in the record order ([B*G][Tq][hpg]) so the records are written contiguously.
+__global__ __launch_bounds__(256) void row_stats_in_kernel(AttnArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)a.B * a.H * a.Tq) return;
+  const int hh = (int)(i % a.hpg);
+  const int64_t bt = i / a.hpg;
+  const int t = (int)(bt % a.Tq);
+  const int bg = (int)(bt / a.Tq);
+  const int b = bg / a.G, h = (bg % a.G) * a.hpg + hh;
+  const int64_t srow = ((int64_t)b * a.H + h) * a.Tq + t;
+  const float L = a.L[b * a.sl_b + (int64_t)h * a.sl_h + (int64_t)t * a.sl_t];
+  const float M = a.M[b * a.sm_b + (int64_t)h * a.sm_h + (int64_t)t * a.sm_t];
+  a.rstat[i] = make_float4(L == -INFINITY ? INFINITY : (M + L) * kLog2e, a.delta_in[srow],
+                           a.row_gate ? a.row_gate[srow] : 1.f, 0.f);
+}
+
 bool launch_row_stats(int dtype, int dv, const AttnArgs& a, hipStream_t st) {
   const int64_t nrows = (int64_t)a.B * a.H * a.Tq;
+  if (a.delta_in) {
+    hipLaunchKernelGGL(row_stats_in_kernel, dim3((unsigned)((nrows + 255) / 256)), dim3(256), 0, st, a);
+    return true;
+  }
   const dim3 grid((unsigned)((nrows + 16 * kStatRows - 1) / (16 * kStatRows)));
 #define NSA_ROWSTATS(DVV)                                                                             \
   if (dv == DVV) {                                                                                    \
@@ -99,8 +119,10 @@ bool launch_row_stats(int dtype, int dv, const AttnArgs& a, hipStream_t st) {
 
 // Row dots of the gated mix (the module backward): dots[k][row] = sum_d dout . o_k for
 // the three branch outputs, dout read once.  They are the gate gradient's inputs and the
-// branches' delta_in, so no branch backward reads its output again.  Same lane layout
-// as row_stats_kernel.
+// branches' delta_in, so no branch backward reads its output again.  A workgroup takes
+// 16 heads x 4 timesteps: lane group g owns head h0 + g at the four timesteps, so with
+// heads the contiguous axis ([B,T,H,dv] storage) the 16 groups read one contiguous run
+// per timestep, and each group stores its four dots of a head as one 16-byte vector.
 template <typename T, int DV>
 __global__ __launch_bounds__(256) void mix_row_dots_kernel(const void* dout, const void* o0, const void* o1,
                                                            const void* o2, int64_t s_b, int64_t s_h, int64_t s_t,
@@ -108,33 +130,33 @@ __global__ __launch_bounds__(256) void mix_row_dots_kernel(const void* dout, con
   using S = typename Store<T>::type;
   constexpr int EPF = 16 / (int)sizeof(S);
   constexpr int NP = (DV / EPF + 15) / 16;
-  const int64_t nrows = (int64_t)B * H * Tq;
-  const int l = threadIdx.x & 15;
+  const int l = threadIdx.x & 15, grp = threadIdx.x >> 4;
+  const int ntb = (Tq + 3) / 4;
+  const int t0 = (blockIdx.x % ntb) * 4;
+  const int h = (blockIdx.x / ntb) * 16 + grp;
+  const int b = blockIdx.y;
+  const bool hv = h < H;
   const S* src[4] = {reinterpret_cast<const S*>(dout), reinterpret_cast<const S*>(o0), reinterpret_cast<const S*>(o1),
                      reinterpret_cast<const S*>(o2)};
-  int64_t r[kStatRows], off[kStatRows];
+  int64_t off[4];
 #pragma unroll
-  for (int k = 0; k < kStatRows; ++k) {
-    const int64_t row = (int64_t)blockIdx.x * (16 * kStatRows) + k * 16 + (threadIdx.x >> 4);
-    r[k] = row < nrows ? row : nrows - 1;
-    const int t = (int)(r[k] % Tq);
-    const int64_t bh = r[k] / Tq;
-    off[k] = (bh / H) * s_b + (bh % H) * s_h + (int64_t)t * s_t;
-  }
-  uint4 v[4][kStatRows][NP];
+  for (int k = 0; k < 4; ++k)  // rows past the end re-read a valid row (not stored)
+    off[k] = b * s_b + (int64_t)(hv ? h : H - 1) * s_h + (int64_t)min(t0 + k, Tq - 1) * s_t;
+  uint4 v[4][4][NP];
 #pragma unroll
   for (int x = 0; x < 4; ++x)
 #pragma unroll
-    for (int k = 0; k < kStatRows; ++k)
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
       for (int j = 0; j < NP; ++j) {
         const int p = l + 16 * j;
         v[x][k][j] = p < DV / EPF ? *reinterpret_cast<const uint4*>(src[x] + off[k] + p * EPF) : make_uint4(0, 0, 0, 0);
       }
-  const int64_t plane = nrows;
+  float acc[3][4];
 #pragma unroll
-  for (int k = 0; k < kStatRows; ++k) {
-    float acc[3] = {0.f, 0.f, 0.f};
+  for (int k = 0; k < 4; ++k) {
+#pragma unroll
+    for (int x = 0; x < 3; ++x) acc[x][k] = 0.f;
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
       const S* d = reinterpret_cast<const S*>(&v[0][k][j]);
@@ -142,17 +164,25 @@ __global__ __launch_bounds__(256) void mix_row_dots_kernel(const void* dout, con
       for (int x = 0; x < 3; ++x) {
         const S* o = reinterpret_cast<const S*>(&v[x + 1][k][j]);
 #pragma unroll
-        for (int u = 0; u < EPF; ++u) acc[x] = fmaf(Elem<T>::to_f32(o[u]), Elem<T>::to_f32(d[u]), acc[x]);
+        for (int u = 0; u < EPF; ++u) acc[x][k] = fmaf(Elem<T>::to_f32(o[u]), Elem<T>::to_f32(d[u]), acc[x][k]);
       }
     }
 #pragma unroll
     for (int x = 0; x < 3; ++x)
 #pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) acc[x] += __shfl_xor(acc[x], o, 16);
-    const int64_t row = (int64_t)blockIdx.x * (16 * kStatRows) + k * 16 + (threadIdx.x >> 4);
-    if (l == 0 && row < nrows) {
+      for (int o = 8; o >= 1; o >>= 1) acc[x][k] += __shfl_xor(acc[x][k], o, 16);
+  }
+  if (l != 0 || !hv) return;
+  const int64_t plane = (int64_t)B * H * Tq;
 #pragma unroll
-      for (int x = 0; x < 3; ++x) dots[x * plane + row] = acc[x];
+  for (int x = 0; x < 3; ++x) {
+    float* dp = dots + x * plane + ((int64_t)b * H + h) * Tq + t0;
+    if (t0 + 3 < Tq && (reinterpret_cast<uintptr_t>(dp) & 15) == 0) {
+      *reinterpret_cast<float4*>(dp) = make_float4(acc[x][0], acc[x][1], acc[x][2], acc[x][3]);
+    } else {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (t0 + k < Tq) dp[k] = acc[x][k];
     }
   }
 }
@@ -174,7 +204,7 @@ extern "C" int nsa_mix_row_dots(const void* dout, const void* o_cmp, const void*
     if ((uintptr_t)p % 16) return set_error(NSA_ERR_LAYOUT, "rows must be 16-byte aligned");
   if ((so_t * esz) % 16 || (so_h * esz) % 16 || (so_b * esz) % 16)
     return set_error(NSA_ERR_LAYOUT, "rows must be 16-byte aligned");
-  const dim3 grid((unsigned)((nrows + 16 * kStatRows - 1) / (16 * kStatRows)));
+  const dim3 grid((unsigned)(((T + 3) / 4) * ((H + 15) / 16)), (unsigned)B);
   hipStream_t st = (hipStream_t)stream;
 #define NSA_DOTS(DVV)                                                                                             \
   if (dv == DVV) {                                                                                                \
