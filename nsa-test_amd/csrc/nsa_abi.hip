@@ -136,7 +136,7 @@ Layout make_layout(const Shape& s, bool bwd) {
     }
   }
   if (bwd && s.br != kSelection && s.stored_ds()) L.ds = take(s.ds_bytes());
-  if (bwd && !s.direct()) L.partial = take(BG * s.items_per_bg() * dkdv_keys(s.br) * (size_t)(s.dk + s.dv) * 4);
+  if (bwd && !s.direct()) L.partial = take(BG * s.items_per_bg() * dkdv_keys(s.br) * (size_t)(s.dk + s.dv) * s.esz());
   L.total = off;
   return L;
 }
@@ -352,7 +352,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   a.items_per_bg = s.items_per_bg();
   a.seg = s.seg();
   a.direct = s.direct() ? 1 : 0;
-  a.partial = at<float>(ws, L.partial);
+  a.partial = at<char>(ws, L.partial);
 
   launch_repack_kv(s.dtype, io.K, io.sk, s.dk, const_cast<void*>(a.krf), const_cast<void*>(a.kcf), io.V, io.sv,
                    s.dv, const_cast<void*>(a.vrf), nullptr, s.Z, s.G, s.Tkv, a.Tp, st);

@@ -71,7 +71,7 @@ struct AttnArgs {
   int64_t sdk_b, sdk_g, sdk_t, sdk_d;
   void* dv;
   int64_t sdv_b, sdv_g, sdv_t, sdv_d;
-  float* partial;  // [items][64][DK+DV]
+  void* partial;  // [items][keys][DK+DV] partial sums, fp32 (bf16 for bf16 inputs)
   int items_per_bg;
   int q0;  // absolute position of query row 0 (0 unless a caller decodes past a cache)
   int seg;  // query entries per dK/dV work item

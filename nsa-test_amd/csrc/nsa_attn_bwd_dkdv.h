@@ -548,17 +548,14 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     for (int j = 0; j < DV / 16; ++j) add4<T>(vp, (int64_t)(j * 16 + 4 * g4), a.sdv_d, dva[j]);
     return;
   }
-  // ---- write this item's partial: lane holds dK^T[d = 16j + 4*g4 + i][key = mykey] ----
-  float* pp = a.partial + ((int64_t)bg * a.items_per_bg + item) * KEYS * (DK + DV) +
-              (int64_t)(wave * 16 + c16) * (DK + DV);
+  // ---- write this item's partial (in the element type: the reduce sums the items' partials
+  // in fp32): lane holds dK^T[d = 16j + 4*g4 + i][key = mykey] ----
+  S* pp = reinterpret_cast<S*>(a.partial) + ((int64_t)bg * a.items_per_bg + item) * KEYS * (DK + DV) +
+          (int64_t)(wave * 16 + c16) * (DK + DV);
 #pragma unroll
-  for (int j = 0; j < DK / 16; ++j) {
-    const f32x4 v = dka[j] * a.scale;
-    *reinterpret_cast<float4*>(pp + j * 16 + 4 * g4) = make_float4(v[0], v[1], v[2], v[3]);
-  }
+  for (int j = 0; j < DK / 16; ++j) store4<T>(pp + j * 16 + 4 * g4, dka[j] * a.scale);
 #pragma unroll
-  for (int j = 0; j < DV / 16; ++j)
-    *reinterpret_cast<float4*>(pp + DK + j * 16 + 4 * g4) = make_float4(dva[j][0], dva[j][1], dva[j][2], dva[j][3]);
+  for (int j = 0; j < DV / 16; ++j) store4<T>(pp + DK + j * 16 + 4 * g4, dva[j]);
 }
 
 template <typename T, int DK, int DV, int BR>

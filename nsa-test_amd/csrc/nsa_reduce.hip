@@ -1,7 +1,8 @@
 // dK/dV partial reduction and the dtype dispatch of the attention kernels.
 //
 // Compression and selection split a key tile's queries over several work items;
-// each item wrote fp32 partials [keys][DK + DV].  One workgroup per key tile
+// each item wrote partials [keys][DK + DV] in the element type (fp32 / bf16), summed here
+// in fp32.  One workgroup per key tile
 // sums them in item order (fixed, so the result is reproducible) and accumulates
 // into the caller's dK / dV with their strides (or, in overwrite mode, stores the sum:
 // a tile without items then stores zeros).
@@ -59,8 +60,8 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
     step = nsubblk;
   }
   if ((count == 0 && !a.dkdv_ow) || key0 >= key_hi) return;
-  const float* base = a.partial + (int64_t)bg * a.items_per_bg * keys * width;
-  const int64_t istride = (int64_t)step * keys * width;  // floats between consecutive items
+  const S* base = reinterpret_cast<const S*>(a.partial) + (int64_t)bg * a.items_per_bg * keys * width;
+  const int64_t istride = (int64_t)step * keys * width;  // elements between consecutive items
   // blockIdx.z splits the tile's keys x width elements (in groups of four: DK and DV are
   // multiples of four, so a group never straddles dK / dV) over `split` workgroups
   const int n4 = keys * width / 4;
@@ -87,41 +88,25 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
     typename Raw4<T>::type old{};
     if (vec && !ow) old = load4_raw<T>(p);
     // the items' partials in item order (fixed: reproducible), eight (then four) loads in flight
-    const float* src = base + (int64_t)first * keys * width + e;
-    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+    const S* src = base + (int64_t)first * keys * width + e;
+    f32x4 sum = zero4();
     int k = 0;
     for (; k + 8 <= count; k += 8) {
-      float4 v[8];
+      typename Raw4<T>::type v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = *reinterpret_cast<const float4*>(src + (k + u) * istride);
+      for (int u = 0; u < 8; ++u) v[u] = load4_raw<T>(src + (k + u) * istride);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
-        sum.x += v[u].x;
-        sum.y += v[u].y;
-        sum.z += v[u].z;
-        sum.w += v[u].w;
-      }
+      for (int u = 0; u < 8; ++u) sum += raw4_f32(v[u]);
     }
     for (; k + 4 <= count; k += 4) {
-      float4 v[4];
+      typename Raw4<T>::type v[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4*>(src + (k + u) * istride);
+      for (int u = 0; u < 4; ++u) v[u] = load4_raw<T>(src + (k + u) * istride);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        sum.x += v[u].x;
-        sum.y += v[u].y;
-        sum.z += v[u].z;
-        sum.w += v[u].w;
-      }
+      for (int u = 0; u < 4; ++u) sum += raw4_f32(v[u]);
     }
-    for (; k < count; ++k) {
-      const float4 v = *reinterpret_cast<const float4*>(src + k * istride);
-      sum.x += v.x;
-      sum.y += v.y;
-      sum.z += v.z;
-      sum.w += v.w;
-    }
-    const float sv[4] = {sum.x, sum.y, sum.z, sum.w};
+    for (; k < count; ++k) sum += raw4_f32(load4_raw<T>(src + k * istride));
+    const float sv[4] = {sum[0], sum[1], sum[2], sum[3]};
     if (ow) {
       set4<T>(p, 0, sd, f32x4{sv[0], sv[1], sv[2], sv[3]});
     } else if (vec) {  // one vector read-modify-write

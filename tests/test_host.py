@@ -132,7 +132,10 @@ def test_workspace_sizes():
     sf = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_F32, 1, 64, 4, 8192, 8192, 192, 128, 16, 64, 1)
     tp = 8192 + 64  # re-packed K/V rows (a multiple of 64, plus 64 zero rows)
     kv16 = 4 * tp * (2 * 192 + 128) * 2  # K rowfrag + K colfrag + V rowfrag copies, bf16
-    assert s - (sf - kv16) == 64 * 8192 * 16 * 64 * 2 + 4 * 8192 * 16 * 4
+    # fp32 partials are 4 bytes per (item, key, feature), bf16 ones 2: 1152 items per group
+    # here (128 blocks + 8192 * 16 entries / 128-entry segments), 64 keys, dk + dv = 320
+    part16 = 4 * 1152 * 64 * 320 * 2
+    assert s - (sf - kv16 - part16) == 64 * 8192 * 16 * 64 * 2 + 4 * 8192 * 16 * 4
     s3 = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_BF16, 1, 12, 4, 8192, 8192, 192, 128, 16, 64, 1)
     s3f = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_F32, 1, 12, 4, 8192, 8192, 192, 128, 16, 64, 1)
     assert s3f - s3 > 0  # only the fp32 K/V copies are larger
