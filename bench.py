@@ -7,7 +7,8 @@ compress_tokens (MLP pooling of K, mean pooling of V), the fused Eq. 8 -> 10 top
 selection (l=32, d=16, l'=64, n=16 with 3 fixed blocks), the compression / selection /
 sliding-window (w=512) HIP attention branches, the sigmoid-gated mix, and the backward
 of all of it.  Inputs (q, k, v, dO ~ N(0,1)/sqrt(d), gate logits, N(0,0.02) MLP
-weights) are synthetic and resident in HBM before the timed region.
+weights) are synthetic, in the layouts NSAAttention's projections produce ([B,H,T,d]
+views of [B,T,H,d] storage), and resident in HBM before the timed region.
 
 The JSON line also carries the long-context configuration (T=32768, configs[3]) as
 `secondary`, the sliding-window branch alone at configs[1] as `config2_sliding`, a
@@ -59,17 +60,23 @@ def make_workload(name, dev, seed=0):
     def rnd(*shape, scale=1.0):
         return (torch.randn(*shape, device=dev, generator=g) * scale).to(bf)
 
+    # every per-token tensor in the layout NSAAttention's projections hand over: a
+    # [B,H,T,d] ([B,G,T,d]) view of [B,T,H,d] ([B,T,G,d]) storage
+    def bthd(x):
+        return x.permute(0, 2, 1, 3)
+
     if c["lowrank"]:
         # low-rank (rank 8) component shared by all heads makes block scores peaked
         basis = torch.randn(T, 8, device=dev, generator=g)
         pq = torch.randn(8, dk, device=dev, generator=g)
         pk = torch.randn(8, dk, device=dev, generator=g)
-        q = (torch.randn(B, H, T, dk, device=dev, generator=g) + basis @ pq).to(bf)
-        kk = [(torch.randn(B, G, T, dk, device=dev, generator=g) + basis @ pk).to(bf) for _ in range(3)]
+        q = bthd((torch.randn(B, T, H, dk, device=dev, generator=g) + (basis @ pq).unsqueeze(1)).to(bf))
+        kk = [bthd((torch.randn(B, T, G, dk, device=dev, generator=g) + (basis @ pk).unsqueeze(1)).to(bf))
+              for _ in range(3)]
     else:
-        q = rnd(B, H, T, dk, scale=1 / math.sqrt(dk))
-        kk = [rnd(B, G, T, dk, scale=1 / math.sqrt(dk)) for _ in range(3)]
-    vv = [rnd(B, G, T, dv, scale=1 / math.sqrt(dv)) for _ in range(3)]
+        q = bthd(rnd(B, T, H, dk, scale=1 / math.sqrt(dk)))
+        kk = [bthd(rnd(B, T, G, dk, scale=1 / math.sqrt(dk))) for _ in range(3)]
+    vv = [bthd(rnd(B, T, G, dv, scale=1 / math.sqrt(dv))) for _ in range(3)]
     mod = NSAAttention(cfg)
     with torch.no_grad():
         for p in mod.compress_mlp.parameters():

@@ -391,13 +391,14 @@ int nsa_mix_row_dots(const void* dout, const void* o_cmp, const void* o_sel, con
  * C = E W1p^T + b1  [l,width].  Forward writes R[i] = mean_{u<l} relu(Y[d*i+u] + C[u])
  * [Z,G,n_act,width] and V_cmp[i] = mean_{u<l} v[d*i+u] [Z,G,n_act,dv]; the caller
  * finishes K_cmp = R W2^T + b2.  Backward overwrites dY, dV (dtype) and dC (fp32).
- * All tensors compact row-major. */
+ * All tensors compact row-major; with token_major set, Y / dY and V / dV are stored
+ * [Z,T,G,*] (the layout of the module's K / V projections) instead of [Z,G,T,*]. */
 int nsa_compress_pool_fwd(const void* Y, const void* C, const void* V, void* R, void* V_cmp, int Z, int n_kv_groups,
-                          int n_ctx, int width, int head_dim_v, int l, int d, int n_act, int dtype,
+                          int n_ctx, int width, int head_dim_v, int l, int d, int n_act, int token_major, int dtype,
                           nsa_stream_t stream);
 int nsa_compress_pool_bwd(const void* Y, const void* C, const void* dR, const void* dV_cmp, void* dY, float* dC,
                           void* dV, int Z, int n_kv_groups, int n_ctx, int width, int head_dim_v, int l, int d,
-                          int n_act, int dtype, nsa_stream_t stream);
+                          int n_act, int token_major, int dtype, nsa_stream_t stream);
 
 #ifdef __cplusplus
 }

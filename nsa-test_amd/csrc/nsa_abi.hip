@@ -438,7 +438,7 @@ int nsa::set_error(int code, const char* msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 
-int nsa_abi_version(void) { return 3; }
+int nsa_abi_version(void) { return 4; }
 const char* nsa_last_error(void) { return g_err; }
 int nsa_head_dims_supported(int dtype, int dk, int dv) {
   return (dtype == NSA_F32 || dtype == NSA_BF16) && dims_supported(dk, dv);

@@ -18,29 +18,35 @@
 
 namespace nsa {
 
+// Row of token t of (batch, group) bg: group-major [B,G,T,*] storage (tm = 0) or the
+// token-major [B,T,G,*] storage the module's projections produce (tm = 1).
+__device__ __forceinline__ int64_t pool_row(int64_t bg, int64_t t, int T_, int G, int tm) {
+  return tm ? ((bg / G) * T_ + t) * G + bg % G : bg * T_ + t;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void pool_fwd_kernel(const typename Store<T>::type* __restrict__ Y,
                                                        const typename Store<T>::type* __restrict__ C,
                                                        const typename Store<T>::type* __restrict__ V,
                                                        typename Store<T>::type* __restrict__ R,
                                                        typename Store<T>::type* __restrict__ Vc, int T_, int W, int dv,
-                                                       int l, int d, int n_act) {
+                                                       int l, int d, int n_act, int G, int tm) {
   // grid: (n_act, B*G); threads stride over the W + dv channels
   const int i = blockIdx.x;
   const int64_t bg = blockIdx.y;
   const float inv = 1.0f / (float)l;
-  const int64_t row0 = bg * T_ + (int64_t)i * d;
+  const int64_t t0 = (int64_t)i * d;
   for (int c = threadIdx.x; c < W + dv; c += 256) {
     float acc = 0.f;
     if (c < W) {
       for (int u = 0; u < l; ++u) {
-        const float y = Elem<T>::to_f32(Y[(row0 + u) * W + c]) + Elem<T>::to_f32(C[(int64_t)u * W + c]);
+        const float y = Elem<T>::to_f32(Y[pool_row(bg, t0 + u, T_, G, tm) * W + c]) + Elem<T>::to_f32(C[(int64_t)u * W + c]);
         acc += y > 0.f ? y : 0.f;
       }
       R[(bg * n_act + i) * W + c] = Elem<T>::from_f32(acc * inv);
     } else {
       const int e = c - W;
-      for (int u = 0; u < l; ++u) acc += Elem<T>::to_f32(V[(row0 + u) * dv + e]);
+      for (int u = 0; u < l; ++u) acc += Elem<T>::to_f32(V[pool_row(bg, t0 + u, T_, G, tm) * dv + e]);
       Vc[(bg * n_act + i) * dv + e] = Elem<T>::from_f32(acc * inv);
     }
   }
@@ -55,14 +61,14 @@ __global__ __launch_bounds__(256) void pool_bwd_tok_kernel(const typename Store<
                                                            const typename Store<T>::type* __restrict__ dVc,
                                                            typename Store<T>::type* __restrict__ dY,
                                                            typename Store<T>::type* __restrict__ dV, int T_, int W,
-                                                           int dv, int l, int d, int n_act) {
+                                                           int dv, int l, int d, int n_act, int G, int tm) {
   const int t = blockIdx.x;
   const int64_t bg = blockIdx.y;
   const float inv = 1.0f / (float)l;
   // blocks i with d*i <= t < d*i + l, 0 <= i < n_act (ascending i)
   int i_lo = t - l + 1 <= 0 ? 0 : (t - l + 1 + d - 1) / d;
   int i_hi = min(t / d, n_act - 1);
-  const int64_t row = bg * T_ + t;
+  const int64_t row = pool_row(bg, t, T_, G, tm);
   for (int c = threadIdx.x; c < W + dv; c += 256) {
     float acc = 0.f;
     if (c < W) {
@@ -87,7 +93,7 @@ __global__ __launch_bounds__(256) void pool_bwd_c_kernel(const typename Store<T>
                                                          const typename Store<T>::type* __restrict__ C,
                                                          const typename Store<T>::type* __restrict__ dR,
                                                          float* __restrict__ dC, int BG, int T_, int W, int l, int d,
-                                                         int n_act) {
+                                                         int n_act, int G, int tm) {
   // 64 channels x 4 interleaved block groups per workgroup; the 4 group sums are
   // combined in a fixed order
   __shared__ float part[4][64];
@@ -100,7 +106,7 @@ __global__ __launch_bounds__(256) void pool_bwd_c_kernel(const typename Store<T>
     for (int64_t bg = 0; bg < BG; ++bg) {
 #pragma unroll 4
       for (int i = ig; i < n_act; i += 4) {
-        const float y = Elem<T>::to_f32(Y[(bg * T_ + (int64_t)i * d + u) * W + c]);
+        const float y = Elem<T>::to_f32(Y[pool_row(bg, (int64_t)i * d + u, T_, G, tm) * W + c]);
         const float g = Elem<T>::to_f32(dR[(bg * n_act + i) * W + c]);
         acc += (y + cu > 0.f) ? g : 0.f;
       }
@@ -148,7 +154,7 @@ __global__ __launch_bounds__(256) void pool_bwd_tok_vec_kernel(const typename St
                                                                const typename Store<T>::type* __restrict__ dVc,
                                                                typename Store<T>::type* __restrict__ dY,
                                                                typename Store<T>::type* __restrict__ dV, int T_, int W,
-                                                               int dv, int l, int d, int n_act, int ppt) {
+                                                               int dv, int l, int d, int n_act, int ppt, int G, int tm) {
   constexpr int EPF = 16 / sizeof(typename Store<T>::type);
   const int tpw = 256 / ppt;
   const int t = blockIdx.x * tpw + threadIdx.x / ppt;
@@ -158,7 +164,7 @@ __global__ __launch_bounds__(256) void pool_bwd_tok_vec_kernel(const typename St
   const float inv = 1.0f / (float)l;
   const int i_lo = t - l + 1 <= 0 ? 0 : (t - l + 1 + d - 1) / d;
   const int i_hi = min(t / d, n_act - 1);
-  const int64_t row = bg * T_ + t;
+  const int64_t row = pool_row(bg, t, T_, G, tm);
   float acc[EPF], x[EPF];
 #pragma unroll
   for (int k = 0; k < EPF; ++k) acc[k] = 0.f;
@@ -198,7 +204,7 @@ __global__ __launch_bounds__(1024) void pool_bwd_c_vec_kernel(const typename Sto
                                                               const typename Store<T>::type* __restrict__ C,
                                                               const typename Store<T>::type* __restrict__ dR,
                                                               float* __restrict__ dC, int BG, int T_, int W, int l,
-                                                              int d, int n_act) {
+                                                              int d, int n_act, int G, int tm) {
   constexpr int EPF = 16 / sizeof(typename Store<T>::type);
   constexpr int NPC = 64 / EPF;             // piece columns per workgroup
   constexpr int NG = 1024 / NPC;            // row groups
@@ -216,7 +222,7 @@ __global__ __launch_bounds__(1024) void pool_bwd_c_vec_kernel(const typename Sto
     for (int64_t q = grp; q < nrows; q += NG) {
       const int64_t bg = q / n_act;
       const int i = (int)(q % n_act);
-      unpack16<T>(*reinterpret_cast<const uint4*>(Y + (bg * T_ + (int64_t)i * d + u) * W + c), y);
+      unpack16<T>(*reinterpret_cast<const uint4*>(Y + pool_row(bg, (int64_t)i * d + u, T_, G, tm) * W + c), y);
       unpack16<T>(*reinterpret_cast<const uint4*>(dR + q * W + c), g);
 #pragma unroll
       for (int k = 0; k < EPF; ++k)
@@ -242,7 +248,7 @@ __global__ __launch_bounds__(256) void pool_fwd_vec_kernel(const typename Store<
                                                            const typename Store<T>::type* __restrict__ V,
                                                            typename Store<T>::type* __restrict__ R,
                                                            typename Store<T>::type* __restrict__ Vc, int T_, int W,
-                                                           int dv, int l, int d, int n_act, int ppt) {
+                                                           int dv, int l, int d, int n_act, int ppt, int G, int tm) {
   constexpr int EPF = 16 / sizeof(typename Store<T>::type);
   const int bpw = 256 / ppt;
   const int i = blockIdx.x * bpw + threadIdx.x / ppt;
@@ -250,7 +256,7 @@ __global__ __launch_bounds__(256) void pool_fwd_vec_kernel(const typename Store<
   if (threadIdx.x >= bpw * ppt || i >= n_act) return;
   const int64_t bg = blockIdx.y;
   const float inv = 1.0f / (float)l;
-  const int64_t row0 = bg * T_ + (int64_t)i * d;
+  const int64_t t0 = (int64_t)i * d;
   float acc[EPF], x[EPF];
 #pragma unroll
   for (int k = 0; k < EPF; ++k) acc[k] = 0.f;
@@ -259,7 +265,7 @@ __global__ __launch_bounds__(256) void pool_fwd_vec_kernel(const typename Store<
     float cu[EPF];
 #pragma unroll 8
     for (int u = 0; u < l; ++u) {
-      unpack16<T>(*reinterpret_cast<const uint4*>(Y + (row0 + u) * W + c), x);
+      unpack16<T>(*reinterpret_cast<const uint4*>(Y + pool_row(bg, t0 + u, T_, G, tm) * W + c), x);
       unpack16<T>(*reinterpret_cast<const uint4*>(C + (int64_t)u * W + c), cu);
 #pragma unroll
       for (int k = 0; k < EPF; ++k) {
@@ -274,7 +280,7 @@ __global__ __launch_bounds__(256) void pool_fwd_vec_kernel(const typename Store<
     const int e = c - W;
 #pragma unroll 8
     for (int u = 0; u < l; ++u) {
-      unpack16<T>(*reinterpret_cast<const uint4*>(V + (row0 + u) * dv + e), x);
+      unpack16<T>(*reinterpret_cast<const uint4*>(V + pool_row(bg, t0 + u, T_, G, tm) * dv + e), x);
 #pragma unroll
       for (int k = 0; k < EPF; ++k) acc[k] += x[k];
     }
@@ -288,11 +294,12 @@ __global__ __launch_bounds__(256) void pool_fwd_vec_kernel(const typename Store<
 
 using namespace nsa;
 
-// All tensors compact (row-major): Y [B,G,T,W], C [l,W], V [B,G,T,dv],
-// R [B,G,n_act,W], Vc [B,G,n_act,dv].
+// All tensors compact (row-major): Y [B,G,T,W] (token_major: [B,T,G,W]), C [l,W],
+// V [B,G,T,dv] (token_major: [B,T,G,dv]), R [B,G,n_act,W], Vc [B,G,n_act,dv].
 extern "C" int nsa_compress_pool_fwd(const void* Y, const void* C, const void* V, void* R, void* Vc, int Z, int G,
-                                     int n_ctx, int width, int head_dim_v, int l, int d, int n_act, int dtype,
-                                     nsa_stream_t stream) {
+                                     int n_ctx, int width, int head_dim_v, int l, int d, int n_act, int token_major,
+                                     int dtype, nsa_stream_t stream) {
+  const int tm = token_major ? 1 : 0;
   if (dtype != NSA_F32 && dtype != NSA_BF16) return set_error(NSA_ERR_INVALID, "dtype not supported");
   if (Z <= 0 || G <= 0 || l <= 0 || d <= 0 || n_act < 0 || width <= 0 || head_dim_v <= 0)
     return set_error(NSA_ERR_INVALID, "bad shape");
@@ -310,29 +317,31 @@ extern "C" int nsa_compress_pool_fwd(const void* Y, const void* C, const void* V
       dim3 gv((n_act + bpw - 1) / bpw, Z * G);
       if (dtype == NSA_F32)
         hipLaunchKernelGGL(pool_fwd_vec_kernel<float>, gv, dim3(256), 0, st, (const float*)Y, (const float*)C,
-                           (const float*)V, (float*)R, (float*)Vc, n_ctx, width, head_dim_v, l, d, n_act, ppt);
+                           (const float*)V, (float*)R, (float*)Vc, n_ctx, width, head_dim_v, l, d, n_act, ppt, G, tm);
       else
         hipLaunchKernelGGL(pool_fwd_vec_kernel<bf16>, gv, dim3(256), 0, st, (const uint16_t*)Y, (const uint16_t*)C,
                            (const uint16_t*)V, (uint16_t*)R, (uint16_t*)Vc, n_ctx, width, head_dim_v, l, d, n_act,
-                           ppt);
+                           ppt, G, tm);
       hipError_t e = hipGetLastError();
       return e == hipSuccess ? NSA_OK : set_error(NSA_ERR_HIP, hipGetErrorString(e));
     }
   }
   if (dtype == NSA_F32)
     hipLaunchKernelGGL(pool_fwd_kernel<float>, grid, dim3(256), 0, st, (const float*)Y, (const float*)C,
-                       (const float*)V, (float*)R, (float*)Vc, n_ctx, width, head_dim_v, l, d, n_act);
+                       (const float*)V, (float*)R, (float*)Vc, n_ctx, width, head_dim_v, l, d, n_act, G, tm);
   else
     hipLaunchKernelGGL(pool_fwd_kernel<bf16>, grid, dim3(256), 0, st, (const uint16_t*)Y, (const uint16_t*)C,
-                       (const uint16_t*)V, (uint16_t*)R, (uint16_t*)Vc, n_ctx, width, head_dim_v, l, d, n_act);
+                       (const uint16_t*)V, (uint16_t*)R, (uint16_t*)Vc, n_ctx, width, head_dim_v, l, d, n_act, G, tm);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? NSA_OK : set_error(NSA_ERR_HIP, hipGetErrorString(e));
 }
 
-// dY [B,G,T,W] and dV [B,G,T,dv] are overwritten (element type = dtype); dC [l,W] fp32.
+// dY [B,G,T,W] and dV [B,G,T,dv] (token_major: [B,T,G,*], as Y and V) are overwritten
+// (element type = dtype); dC [l,W] fp32.
 extern "C" int nsa_compress_pool_bwd(const void* Y, const void* C, const void* dR, const void* dVc, void* dY,
                                      float* dC, void* dV, int Z, int G, int n_ctx, int width, int head_dim_v, int l,
-                                     int d, int n_act, int dtype, nsa_stream_t stream) {
+                                     int d, int n_act, int token_major, int dtype, nsa_stream_t stream) {
+  const int tm = token_major ? 1 : 0;
   if (dtype != NSA_F32 && dtype != NSA_BF16) return set_error(NSA_ERR_INVALID, "dtype not supported");
   if (Z <= 0 || G <= 0 || l <= 0 || d <= 0 || n_act < 0 || width <= 0 || head_dim_v <= 0)
     return set_error(NSA_ERR_INVALID, "bad shape");
@@ -351,15 +360,15 @@ extern "C" int nsa_compress_pool_bwd(const void* Y, const void* C, const void* d
       if (dtype == NSA_F32) {
         hipLaunchKernelGGL(pool_bwd_tok_vec_kernel<float>, gv, dim3(256), 0, st, (const float*)Y, (const float*)C,
                            (const float*)dR, (const float*)dVc, (float*)dY, (float*)dV, n_ctx, width, head_dim_v, l,
-                           d, n_act, ppt);
+                           d, n_act, ppt, G, tm);
         hipLaunchKernelGGL(pool_bwd_c_vec_kernel<float>, gc, dim3(1024), 0, st, (const float*)Y, (const float*)C,
-                           (const float*)dR, dC, Z * G, n_ctx, width, l, d, n_act);
+                           (const float*)dR, dC, Z * G, n_ctx, width, l, d, n_act, G, tm);
       } else {
         hipLaunchKernelGGL(pool_bwd_tok_vec_kernel<bf16>, gv, dim3(256), 0, st, (const uint16_t*)Y,
                            (const uint16_t*)C, (const uint16_t*)dR, (const uint16_t*)dVc, (uint16_t*)dY,
-                           (uint16_t*)dV, n_ctx, width, head_dim_v, l, d, n_act, ppt);
+                           (uint16_t*)dV, n_ctx, width, head_dim_v, l, d, n_act, ppt, G, tm);
         hipLaunchKernelGGL(pool_bwd_c_vec_kernel<bf16>, gc, dim3(1024), 0, st, (const uint16_t*)Y,
-                           (const uint16_t*)C, (const uint16_t*)dR, dC, Z * G, n_ctx, width, l, d, n_act);
+                           (const uint16_t*)C, (const uint16_t*)dR, dC, Z * G, n_ctx, width, l, d, n_act, G, tm);
       }
       hipError_t e = hipGetLastError();
       return e == hipSuccess ? NSA_OK : set_error(NSA_ERR_HIP, hipGetErrorString(e));
@@ -368,15 +377,15 @@ extern "C" int nsa_compress_pool_bwd(const void* Y, const void* C, const void* d
   if (dtype == NSA_F32) {
     hipLaunchKernelGGL(pool_bwd_tok_kernel<float>, gt, dim3(256), 0, st, (const float*)Y, (const float*)C,
                        (const float*)dR, (const float*)dVc, (float*)dY, (float*)dV, n_ctx, width, head_dim_v, l, d,
-                       n_act);
+                       n_act, G, tm);
     hipLaunchKernelGGL(pool_bwd_c_kernel<float>, gc, dim3(256), 0, st, (const float*)Y, (const float*)C,
-                       (const float*)dR, dC, Z * G, n_ctx, width, l, d, n_act);
+                       (const float*)dR, dC, Z * G, n_ctx, width, l, d, n_act, G, tm);
   } else {
     hipLaunchKernelGGL(pool_bwd_tok_kernel<bf16>, gt, dim3(256), 0, st, (const uint16_t*)Y, (const uint16_t*)C,
                        (const uint16_t*)dR, (const uint16_t*)dVc, (uint16_t*)dY, (uint16_t*)dV, n_ctx, width,
-                       head_dim_v, l, d, n_act);
+                       head_dim_v, l, d, n_act, G, tm);
     hipLaunchKernelGGL(pool_bwd_c_kernel<bf16>, gc, dim3(256), 0, st, (const uint16_t*)Y, (const uint16_t*)C,
-                       (const uint16_t*)dR, dC, Z * G, n_ctx, width, l, d, n_act);
+                       (const uint16_t*)dR, dC, Z * G, n_ctx, width, l, d, n_act, G, tm);
   }
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? NSA_OK : set_error(NSA_ERR_HIP, hipGetErrorString(e));

@@ -12,7 +12,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libnsa_hip.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 NSA_F32 = 0
 NSA_BF16 = 1
@@ -70,8 +70,8 @@ SIGNATURES.update({
     "nsa_gate_act_fwd": (_I, [_P] + [_L] * 4 + [_P] + [_I] * 5 + [_P]),
     "nsa_gate_act_bwd": (_I, [_P] * 3 + [_L] * 4 + [_I] * 5 + [_P]),
     "nsa_mix_row_dots": (_I, [_P] * 4 + [_L] * 3 + [_P] + [_I] * 5 + [_P]),
-    "nsa_compress_pool_fwd": (_I, [_P] * 5 + [_I] * 9 + [_P]),
-    "nsa_compress_pool_bwd": (_I, [_P] * 7 + [_I] * 9 + [_P]),
+    "nsa_compress_pool_fwd": (_I, [_P] * 5 + [_I] * 10 + [_P]),
+    "nsa_compress_pool_bwd": (_I, [_P] * 7 + [_I] * 10 + [_P]),
     "nsa_bwd_dkdv_plan": (_I, [_I] * 9 + [_P, _P]),
 })
 

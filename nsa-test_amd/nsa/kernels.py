@@ -338,13 +338,22 @@ class NSACore(torch.autograd.Function):
             _lib.call("nsa_mix_row_dots", _ops._ptr(d), _ops._ptr(o_c), _ops._ptr(o_s), _ops._ptr(o_w),
                       *o_c.stride()[:3], _ops._ptr(rdot), B, H, T, o_c.shape[-1], _ops._dtype_code(d.dtype),
                       _ops._stream(q.device))
-            _, dkc, dvc = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, d, Lc, Mc, sc, block_ends=be, dq=dq,
-                                        row_gate=g[0], delta=rdot[0])
-            _, dks, dvs = _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, d, Ls, Ms, sc, indices=idx,
-                                        lprime=ctx.lprime, fallback=True, dq=dq, dq_accumulate=True, row_gate=g[1],
-                                        delta=rdot[1])
-            _, dkw, dvw = _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, d, Lw, Mw, sc, window=ctx.window, dq=dq,
-                                        dq_accumulate=True, row_gate=g[2], delta=rdot[2])
+            # dK / dV written straight into buffers with the inputs' own strides (the
+            # kernels take any dK / dV strides): the gradients need no layout copy on the
+            # way back to the projections
+            cdt = _ops.compute_dtype(q.dtype)
+
+            def like(t):
+                return torch.empty_like(t, dtype=cdt)
+
+            dkc, dvc, dks, dvs, dkw, dvw = like(_kt(kc)), like(vc), like(_kt(ks)), like(vs), like(_kt(kw)), like(vw)
+            _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, d, Lc, Mc, sc, block_ends=be, dq=dq, dk=dkc, dv=dvc,
+                          dkdv_overwrite=True, row_gate=g[0], delta=rdot[0])
+            _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, d, Ls, Ms, sc, indices=idx, lprime=ctx.lprime, fallback=True,
+                          dq=dq, dq_accumulate=True, dk=dks, dv=dvs, dkdv_overwrite=True, row_gate=g[1],
+                          delta=rdot[1])
+            _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, d, Lw, Mw, sc, window=ctx.window, dq=dq, dq_accumulate=True,
+                          dk=dkw, dv=dvw, dkdv_overwrite=True, row_gate=g[2], delta=rdot[2])
             dg = _gate_activation_grad(g, rdot, ctx.act, ctx.gdtype)
         else:
             dos, dg, deltas = _mix_bwd(dout, [o_c, o_s, o_w], g, want_delta=True, act=ctx.act)
@@ -456,34 +465,38 @@ class _CompressPool(torch.autograd.Function):
     """R[i] = mean_u relu(Y[d*i+u] + C[u]),  V_cmp[i] = mean_u v[d*i+u]  (HIP)."""
 
     @staticmethod
-    def forward(ctx, Y, C, v, l, d, n_act):
+    def forward(ctx, Y, C, v, l, d, n_act, token_major=False):
+        """Y, v: [B,G,T,*], or [B,T,G,*] with token_major (the storage order of the
+        module's projections: no transposing copy)."""
         cdt = _ops.compute_dtype(Y.dtype)
         Yc, Cc, vc = Y.to(cdt).contiguous(), C.to(cdt).contiguous(), v.to(cdt).contiguous()
-        B, G, T, W = Yc.shape
+        if token_major:
+            B, T, G, W = Yc.shape
+        else:
+            B, G, T, W = Yc.shape
         dv = vc.shape[-1]
         R = torch.empty(B, G, n_act, W, device=Y.device, dtype=cdt)
         Vc = torch.empty(B, G, n_act, dv, device=Y.device, dtype=cdt)
         _lib.call("nsa_compress_pool_fwd", _ops._ptr(Yc), _ops._ptr(Cc), _ops._ptr(vc), _ops._ptr(R), _ops._ptr(Vc),
-                  B, G, T, W, dv, l, d, n_act, _ops._dtype_code(cdt), _ops._stream(Y.device))
+                  B, G, T, W, dv, l, d, n_act, int(bool(token_major)), _ops._dtype_code(cdt), _ops._stream(Y.device))
         ctx.save_for_backward(Yc, Cc)
-        ctx.meta = (l, d, n_act, dv, Y.dtype, C.dtype, v.dtype)
+        ctx.meta = (l, d, n_act, dv, Y.dtype, C.dtype, v.dtype, bool(token_major), (B, G, T, W))
         return R.to(Y.dtype), Vc.to(v.dtype)
 
     @staticmethod
     def backward(ctx, dR, dVc):
         Yc, Cc = ctx.saved_tensors
-        l, d, n_act, dv, ydt, cdt_in, vdt = ctx.meta
+        l, d, n_act, dv, ydt, cdt_in, vdt, tm, (B, G, T, W) = ctx.meta
         cdt = Yc.dtype
-        B, G, T, W = Yc.shape
         dRc = (dR if dR is not None else torch.zeros(B, G, n_act, W, device=Yc.device)).to(cdt).contiguous()
         dVcc = (dVc if dVc is not None else torch.zeros(B, G, n_act, dv, device=Yc.device)).to(cdt).contiguous()
         dY = torch.empty_like(Yc)
-        dV = torch.empty(B, G, T, dv, device=Yc.device, dtype=cdt)
+        dV = torch.empty(*((B, T, G) if tm else (B, G, T)), dv, device=Yc.device, dtype=cdt)
         dC = torch.empty(l, W, device=Yc.device, dtype=torch.float32)
         _lib.call("nsa_compress_pool_bwd", _ops._ptr(Yc), _ops._ptr(Cc), _ops._ptr(dRc), _ops._ptr(dVcc),
-                  _ops._ptr(dY), _ops._ptr(dC), _ops._ptr(dV), B, G, T, W, dv, l, d, n_act, _ops._dtype_code(cdt),
-                  _ops._stream(Yc.device))
-        return dY.to(ydt), dC.to(cdt_in), dV.to(vdt), None, None, None
+                  _ops._ptr(dY), _ops._ptr(dC), _ops._ptr(dV), B, G, T, W, dv, l, d, n_act, int(tm),
+                  _ops._dtype_code(cdt), _ops._stream(Yc.device))
+        return dY.to(ydt), dC.to(cdt_in), dV.to(vdt), None, None, None, None
 
 
 # ============================================================== selection (Eq. 9 / 10)
@@ -716,10 +729,15 @@ class NSAAttention(torch.nn.Module):
                     block_ends, n_act)
         l1, l2 = self.compress_mlp[0], self.compress_mlp[2]
         W1k, W1p = _SplitCols.apply(l1.weight, dk)
-        Y = _LinearSplitK.apply(keys, W1k.to(dt), None)                          # [B,G,T,2dk]
+        # keys / values as the module's projections store them ([B,T,G,d], viewed
+        # [B,G,T,d]) are used in that order: the GEMM and the pooling then read them
+        # without a transposing copy, and their gradients come back in the same layout
+        tm = G > 1 and keys.transpose(1, 2).is_contiguous() and values.transpose(1, 2).is_contiguous()
+        kin = keys.transpose(1, 2) if tm else keys
+        Y = _LinearSplitK.apply(kin, W1k.to(dt), None)                           # [B,G,T,2dk] ([B,T,G,2dk])
         C = F.linear(self.pos_embed.weight.to(dt), W1p.to(dt),
                      l1.bias.to(dt) if l1.bias is not None else None)             # [l,2dk]
-        R, Vc = _CompressPool.apply(Y, C, values, c.l, c.d, n_act)
+        R, Vc = _CompressPool.apply(Y, C, values.transpose(1, 2) if tm else values, c.l, c.d, n_act, tm)
         Kc = _LinearSplitK.apply(R, l2.weight.to(dt), l2.bias.to(dt) if l2.bias is not None else None)  # [B,G,n,dk]
         Kc = F.pad(Kc, (0, 0, 0, n_pad - n_act)).transpose(-1, -2)               # [B,G,dk,Np]
         Vc = F.pad(Vc, (0, 0, 0, n_pad - n_act))                                 # [B,G,Np,dv]

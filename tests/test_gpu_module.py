@@ -138,13 +138,20 @@ def test_module_bf16_matches_oracle(dev, monkeypatch):
     assert rel_err(f(cap["out"]), mixed) < 2e-2
 
 
-@pytest.mark.parametrize("T,dtype", [(512, torch.float32), (1000, torch.bfloat16), (40, torch.float32)])
-def test_compress_tokens_matches_oracle(dev, T, dtype):
+@pytest.mark.parametrize("T,dtype,token_major", [(512, torch.float32, False), (1000, torch.bfloat16, False),
+                                                 (40, torch.float32, False), (1000, torch.bfloat16, True),
+                                                 (40, torch.float32, True)])
+def test_compress_tokens_matches_oracle(dev, T, dtype, token_major):
+    """token_major: keys / values are [B,G,T,d] views of [B,T,G,d] storage (the module's
+    projections), which the pooling kernels read in place."""
     torch.manual_seed(2)
     cfg = NSAConfig(d_model=64, head_dim_qk=64, head_dim_v=32, n_heads=4, n_kv_groups=2)
     m = NSAAttention(cfg).to(dev, dtype)
     keys = torch.randn(2, 2, T, 64, device=dev, dtype=dtype)
     vals = torch.randn(2, 2, T, 32, device=dev, dtype=dtype)
+    if token_major:
+        keys = keys.transpose(1, 2).contiguous().transpose(1, 2)
+        vals = vals.transpose(1, 2).contiguous().transpose(1, 2)
     with torch.no_grad():
         kc, vc, be, n_act = m.compress_tokens(keys, vals)
     P = {k: v.float().cpu().numpy() for k, v in m.state_dict().items()}
@@ -157,6 +164,37 @@ def test_compress_tokens_matches_oracle(dev, T, dtype):
     tol = 1e-5 if dtype == torch.float32 else 2e-2
     assert rel_err(kc.float().cpu().numpy(), rk) < tol
     assert rel_err(vc.float().cpu().numpy(), rv) < tol
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_compress_tokens_token_major_gradients(dev, dtype):
+    """Gradients of compress_tokens through the token-major pooling path ([B,T,G,d]
+    storage) equal those of the group-major path on the same values."""
+    torch.manual_seed(5)
+    cfg = NSAConfig(d_model=64, head_dim_qk=64, head_dim_v=32, n_heads=4, n_kv_groups=2)
+    m = NSAAttention(cfg).to(dev, dtype)
+    T = 300
+    k0 = torch.randn(2, 2, T, 64, device=dev, dtype=dtype)
+    v0 = torch.randn(2, 2, T, 32, device=dev, dtype=dtype)
+    dk_out = dv_out = None
+    grads = []
+    for tm in (False, True):
+        m.zero_grad()
+        kl = (k0.transpose(1, 2).contiguous() if tm else k0.clone()).requires_grad_()
+        vl = (v0.transpose(1, 2).contiguous() if tm else v0.clone()).requires_grad_()
+        kc, vc, _, _ = m.compress_tokens(kl.transpose(1, 2) if tm else kl, vl.transpose(1, 2) if tm else vl)
+        if dk_out is None:
+            g = torch.Generator(device=dev).manual_seed(6)
+            dk_out = torch.randn(kc.shape, device=dev, generator=g).to(dtype)
+            dv_out = torch.randn(vc.shape, device=dev, generator=g).to(dtype)
+        (kc.float() * dk_out.float()).sum().add((vc.float() * dv_out.float()).sum()).backward()
+        gk = kl.grad.transpose(1, 2) if tm else kl.grad
+        gv = vl.grad.transpose(1, 2) if tm else vl.grad
+        grads.append([gk.float(), gv.float()] + [p.grad.float().clone() for p in m.parameters() if p.grad is not None])
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert len(grads[0]) == len(grads[1]) > 2
+    for a, b in zip(*grads):
+        assert rel_err(b.cpu().numpy(), a.cpu().numpy()) < tol
 
 
 @pytest.mark.parametrize("rows,dtype", [(32768, torch.bfloat16), (4096, torch.float32), (300, torch.float32)])
