@@ -590,18 +590,31 @@ __global__ __launch_bounds__(256) void attn_sel_dq_kernel(AttnArgs a, int ncolti
 // of the timestep's cleaned list (ascending; the visible ones form a prefix of the
 // (slot, sub-block) order).  Both operands are fragment-native in memory -- K^T from
 // the re-packed colfrag copy, dS^T as stored -- so every fragment is one coalesced 1 KB
-// load straight into registers: no LDS, no S / dP recomputation, no softmax.  The
-// next tile's fragments of one 32-key chunk are requested as soon as this tile's
-// products have read that chunk.  The stored dS already carries the row gate, so the
-// epilogue scales by sm_scale only.
+// load: no S / dP recomputation, no softmax.  The K^T fragments go straight into
+// registers; the next tile's fragments of one 32-key chunk are requested as soon as
+// this tile's products have read that chunk.
+//
+// A wave's vector-memory loads complete in issue order, so a dS load from HBM placed
+// between the K^T loads (L2 hits) would make every K^T load behind it wait for the HBM
+// round trip.  The dS fragments of kDsBatch tiles are therefore copied direct-to-LDS
+// in one batch, a batch ahead (two buffers per wave): one HBM round trip per batch
+// instead of one per chunk.  The buffer after the last batch receives the dQ rows the
+// result is added to (accumulate mode), so their HBM round trip overlaps the last
+// batch's tiles instead of following them.  The stored dS already carries the row
+// gate, so the epilogue scales by sm_scale only.
+constexpr int kDsBatch = 3;
 template <typename T, int DK>
-__global__ __launch_bounds__(256) void attn_sel_dq_ds_kernel(AttnArgs a, int nwaves) {
+__global__ __launch_bounds__(256) void attn_sel_dq_ds_kernel(AttnArgs a, int nwaves, int acc_lds) {
   using S = typename Store<T>::type;
   constexpr int EPF = Elem<T>::kPerFrag;
   static_assert(sizeof(S) == 2, "stored dS is bf16");
+  static_assert(DK * 16 * 2 <= kDsBatch * 2 * 1024, "a buffer holds the wave's dQ rows");
+  // per wave: two buffers of kDsBatch tiles x 2 chunks x 64 lanes x 16 bytes
+  __shared__ uint4 s_ds[4][2][kDsBatch * 2][64];
   const int lane = threadIdx.x & 63;
   const int g4 = lane >> 4, c16 = lane & 15;
-  const int W = xcd_contiguous(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int W = xcd_contiguous(blockIdx.x, gridDim.x) * 4 + wave;
   if (W >= nwaves) return;
   const int nhg = a.hpg >> 4, nsub = a.lprime >> 6;
   const int per_bg = a.Tq * nhg;
@@ -620,43 +633,92 @@ __global__ __launch_bounds__(256) void attn_sel_dq_ds_kernel(AttnArgs a, int nwa
 
   const S* kcf = reinterpret_cast<const S*>(a.kcf) + (int64_t)bg * DK * a.Tp;
   const S* dsb = reinterpret_cast<const S*>(a.ds) + (((int64_t)bg * a.Tq + t) * a.nslots * nsub * nhg + hg) * 1024;
+  // the lane's dQ row (head colh at timestep t); formed where used, not kept live
+  auto dq_row = [&]() __attribute__((always_inline)) {
+    return reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)t * a.sdq_t;
+  };
   uint4 kf[2][DK / 16];
-  u32x4 df[2];
   auto load = [&](int i, int kc2) __attribute__((always_inline)) {
     const int slot = i / nsub, sub = i - slot * nsub;
     const int key0 = __builtin_amdgcn_readlane(lv, slot) * a.lprime + sub * 64;
 #pragma unroll
     for (int j = 0; j < DK / 16; ++j) kf[kc2][j] = ld_colfrag<T>(kcf, key0 / 32 + kc2, j, DK, lane);
-    // dS is read once: non-temporal, so the stream does not evict the group's K^T from L2
-    df[kc2] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(dsb + (int64_t)i * nhg * 1024 + (kc2 * 64 + lane) * EPF));
+  };
+  // buffer q & 1 receives batch q's dS fragments, or, for the first q past the last
+  // tile, the dQ rows (copy k, lane L: head L % 16, 16-byte piece 4k + L / 16 of its
+  // row).  The copies are invisible to the compiler's wait insertion; every K^T load of
+  // a batch's tiles is issued after the batch's copies, so the waits for those loads
+  // (loads complete in issue order) cover them.
+  const int nbatch = (nt + kDsBatch - 1) / kDsBatch;
+  auto stage = [&](int q) __attribute__((always_inline)) {
+    if (q < nbatch) {
+#pragma unroll
+      for (int u = 0; u < kDsBatch; ++u) {
+        const int i = min(q * kDsBatch + u, nt - 1);
+#pragma unroll
+        for (int kc2 = 0; kc2 < 2; ++kc2)
+          copy16_to_lds_async(dsb + (int64_t)i * nhg * 1024 + (kc2 * 64 + lane) * EPF, &s_ds[wave][q & 1][u * 2 + kc2][0]);
+      }
+    } else if (q == nbatch && acc_lds) {
+      // one opaque base, so the compiler does not keep every copy's address live
+      // through the tile loop
+      uintptr_t src = reinterpret_cast<uintptr_t>(dq_row() + g4 * 8);
+      asm volatile("" : "+v"(src));
+#pragma unroll
+      for (int k = 0; k < DK / 32; ++k) copy16_to_lds_async(reinterpret_cast<const S*>(src) + 32 * k, &s_ds[wave][q & 1][k][0]);
+    }
   };
   f32x4 dqa[DK / 16];
 #pragma unroll
   for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
+  stage(0);
+  stage(1);
   if (nt > 0) {
+    __builtin_amdgcn_sched_barrier(0);
     load(0, 0);
     __builtin_amdgcn_sched_barrier(0);
     load(0, 1);
     __builtin_amdgcn_sched_barrier(0);
   }
+  int q = 0, u = 0;  // tile i = q * kDsBatch + u
   for (int i = 0; i < nt; ++i) {
     const int nx = i + 1 < nt ? i + 1 : i;  // unconditional loads (the last tile re-reads itself)
+    // a new batch starts: the buffer of the batch before it is free (its fragments were
+    // read in that batch's last tile), so the next stage goes out now
+    if (u == 0 && q > 0) stage(q + 1);
 #pragma unroll
     for (int kc2 = 0; kc2 < 2; ++kc2) {
+      // the wait for this chunk's K^T fragments also covers its dS copy
+      asm volatile("" ::"v"(kf[kc2][DK / 16 - 1].x) : "memory");
+      const uint4 df = s_ds[wave][q & 1][u * 2 + kc2][lane];
 #pragma unroll
-      for (int j = 0; j < DK / 16; ++j) dqa[j] = Mma<T>::run(dqa[j], kf[kc2][j], __builtin_bit_cast(uint4, df[kc2]));
+      for (int j = 0; j < DK / 16; ++j) dqa[j] = Mma<T>::run(dqa[j], kf[kc2][j], df);
       // keep the order: this chunk's products, then the next tile's loads into its
       // registers (the scheduler would otherwise hoist the loads and wait for all of them)
       __builtin_amdgcn_sched_barrier(0);
       load(nx, kc2);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (++u == kDsBatch) { u = 0; ++q; }
   }
-  S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)t * a.sdq_t;
+  // every copy has landed (and none still writes this workgroup's LDS when it ends)
+  wait_vmcnt<0>();
+  asm volatile("" ::: "memory");
+  const char* acc = reinterpret_cast<const char*>(&s_ds[wave][nbatch & 1][0][0]);
+  S* dqp = dq_row();
 #pragma unroll
   for (int j = 0; j < DK / 16; ++j) {
     f32x4 v = dqa[j] * a.scale;
-    if (a.dq_acc) v += load4<T>(dqp + j * 16 + 4 * g4);  // the caller's running dQ sum
+    if (a.dq_acc) {
+      // the caller's running dQ sum: columns 16 j + 4 g4 .. + 3 of head c16 (8 bytes)
+      if (acc_lds) {
+        const int p = 2 * j + (g4 >> 1);  // the 16-byte piece of the row
+        const uint2 r = *reinterpret_cast<const uint2*>(acc + (p >> 2) * 1024 + ((p & 3) * 16 + c16) * 16 + 8 * (g4 & 1));
+        v += raw4_f32(r);
+      } else {
+        v += load4<T>(dqp + j * 16 + 4 * g4);
+      }
+    }
     store4<T>(dqp + j * 16 + 4 * g4, v);
   }
 }
@@ -666,7 +728,9 @@ void launch_attn_sel_dq(const AttnArgs& a, hipStream_t s) {
   if constexpr (sizeof(typename Store<T>::type) == 2) {
     if (a.ds) {
       const int nwaves = a.B * a.G * a.Tq * (a.hpg / 16);
-      hipLaunchKernelGGL((attn_sel_dq_ds_kernel<T, DK>), dim3((nwaves + 3) / 4), dim3(256), 0, s, a, nwaves);
+      // the dQ rows go through LDS when every row start is 16-byte aligned
+      const int acc_lds = a.dq_acc && ((reinterpret_cast<uintptr_t>(a.dq) | (a.sdq_b | a.sdq_h | a.sdq_t) * 2) % 16 == 0);
+      hipLaunchKernelGGL((attn_sel_dq_ds_kernel<T, DK>), dim3((nwaves + 3) / 4), dim3(256), 0, s, a, nwaves, acc_lds);
       return;
     }
   }

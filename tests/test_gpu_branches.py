@@ -377,17 +377,21 @@ def test_strided_views(dev):
     _check(_ops.SLIDING, q, kp, v, do, 0.125, torch.float32, window=50)
 
 
-@pytest.mark.parametrize("dk,dtype,gate_mode", [(64, torch.float32, "sigmoid"), (192, torch.bfloat16, "sigmoid"),
-                                                (48, torch.float32, "softmax")])
-def test_nsa_core_matches_separate_functions(dev, dk, dtype, gate_mode):
+@pytest.mark.parametrize("dk,dtype,gate_mode,H,lp", [(64, torch.float32, "sigmoid", 8, 32),
+                                                      (192, torch.bfloat16, "sigmoid", 8, 32),
+                                                      (192, torch.bfloat16, "softmax", 32, 64),
+                                                      (48, torch.float32, "softmax", 8, 32)])
+def test_nsa_core_matches_separate_functions(dev, dk, dtype, gate_mode, H, lp):
     """NSACore (the module's three branches, gate activation and gated mix, with the branch backwards
     taking the mix's row sums and summing dQ in the dQ kernels) against
     CompressionAttention / SelectionAttention / SlidingWindowAttention and GatedMix
     applied separately (autograd summing dQ): same output, same gradients.  dk = 48 is
-    zero-padded to a compiled head dim, which takes the summed-on-the-host dQ path."""
+    zero-padded to a compiled head dim, which takes the summed-on-the-host dQ path; 16
+    heads per group with l' = 64 (bf16) take the stored-dS backward, whose selection dQ
+    adds into the running dQ through its LDS-staged rows."""
     from nsa import NSACore
     from nsa.kernels import CompressionAttention, GatedMix, SlidingWindowAttention
-    B, H, G, T, dv, l, d, lp, n, w = 1, 8, 2, 300, 64, 32, 16, 32, 4, 64
+    B, G, T, dv, l, d, n, w = 1, 2, 300, 64, 32, 16, 4, 64
     g = torch.Generator().manual_seed(11)
     nb = (T - l) // d + 1
     q = torch.randn(B, H, T, dk, generator=g).to(dtype)
@@ -422,3 +426,30 @@ def test_nsa_core_matches_separate_functions(dev, dk, dtype, gate_mode):
     assert rel_err(_np(out_a), _np(out_b)) < (1e-2 if dtype == torch.bfloat16 else 1e-6)
     for x, y in zip(a, b):
         assert rel_err(_np(x.grad), _np(y.grad)) < tol
+
+
+@pytest.mark.parametrize("kind", [_ops.SLIDING, _ops.COMPRESSION, _ops.SELECTION])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_dq_accumulate_adds_to_running_sum(dev, kind, dtype):
+    """dq_accumulate: the branch's dQ is added to the values already in dq (the module's
+    branches share one dQ buffer).  bf16 with a whole 16-head group takes the stored-dS
+    dQ kernels (selection: the running rows staged through LDS)."""
+    B, H, G, T, dk, dv = 1, 16, 1, 200, 192, 128
+    q, kp, v, do = _make(21, B, H, G, T, T, dk, dv, dtype, dev)
+    k = kp.transpose(-1, -2)
+    if kind == _ops.SLIDING:
+        kw = dict(window=50)
+    elif kind == _ops.COMPRESSION:
+        nb = (T - 32) // 16 + 1
+        k, v = k[:, :, :nb].contiguous(), v[:, :, :nb].contiguous()
+        kw = dict(block_ends=(torch.arange(nb) * 16 + 31).to(torch.int32).to(dev))
+    else:
+        kw = dict(indices=_random_indices(22, B, G, T, T, 64, 4).to(dev), lprime=64, fallback=True)
+    out, L, M = _ops.attn_fwd(kind, q, k, v, 0.1, **kw)
+    dq0, _, _ = _ops.attn_bwd(kind, q, k, v, out, do, L, M, 0.1, **kw)
+    run = torch.randn(q.shape, device=dev).to(dtype)
+    dq = run.clone()
+    _ops.attn_bwd(kind, q, k, v, out, do, L, M, 0.1, dq=dq, dq_accumulate=True, **kw)
+    want = run.float() + dq0.float()
+    tol = 1e-2 if dtype == torch.bfloat16 else 1e-6
+    assert rel_err(_np(dq), want.cpu().numpy()) < tol
