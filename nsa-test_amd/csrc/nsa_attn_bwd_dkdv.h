@@ -465,15 +465,23 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
         const int ta[4] = {tv.x, tv.y, tv.z, tv.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          bool ok = true;
-          if (!all_visible) {
+          // masked elements: the argument clamped to -inf by a min with a selected
+          // constant, the conditions combined with bitwise operators (a select of the
+          // argument itself, or short-circuit ands, become divergent branches in the
+          // loop); chunks whose rows all see the wave's keys skip the mask (uniform)
+          // (compression keeps the select: measured faster there)
+          float arg = sacc[i] * scale2 - l2a[i];
+          if (BR == kCompression) {
+            arg = (all_visible || (ta[i] >= 0 && mybe <= ta[i])) ? arg : -INFINITY;
+          } else if (!all_visible) {
             const int t = ta[i];
-            if (BR == kSliding) ok = t >= 0 && mykey <= t && mykey > t - a.window && mykey < a.Tkv;
-            else if (BR == kCompression) ok = t >= 0 && mybe <= t;
-            else ok = t >= 0 && (!a.causal || mykey <= t) && mykey < blk_hi;
+            bool vis;
+            if (BR == kSliding) vis = (t >= 0) & (mykey <= t) & (mykey > t - a.window) & (mykey < a.Tkv);
+            else vis = (t >= 0) & ((a.causal == 0) | (mykey <= t)) & (mykey < blk_hi);
+            arg = fminf(arg, vis ? INFINITY : -INFINITY);
           }
           // lse2 is +inf for rows that saw no key: p = 0 there
-          const float p = fast_exp2(ok ? sacc[i] * scale2 - l2a[i] : -INFINITY) * ga[i];  // gated: g dO
+          const float p = fast_exp2(arg) * ga[i];  // gated: g dO
           pt[rs][i] = p;
           dst[rs][i] = p * (pacc[i] - dla[i]);
         }
