@@ -254,7 +254,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     int t;
     float4 st;  // lse2, delta, gate
   };
-  constexpr int kDepth = kTr ? 2 : 1;
+  // (the selection kernel at dk > 128 prefetches one chunk: two spill registers there)
+  constexpr int kDepth = kTr && !(BR == kSelection && DK > 128) ? 2 : 1;
   Stage stg0, stg1;
   stg0.t = stg1.t = -1;
   stg0.st = stg1.st = make_float4(INFINITY, 0.f, 1.f, 0.f);
@@ -535,6 +536,10 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
   } else {
     if (nchunks > 0) load_chunk(f_lo, stg0);
     for (int c = 0; c < nchunks; ++c) chunk(c, stg0);
+    if (kStoreDs && a.ds && nchunks > 0) {  // the last chunk's dS tiles
+      __syncthreads();
+      flush_ds(nchunks - 1);
+    }
   }
 
   // ---- direct mode: add this item's dK / dV into the caller's, or store them (lane holds
