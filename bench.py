@@ -331,7 +331,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}): this build targets single-GPU "
-              f"boxes; see DESIGN.md for how the path would shard.", file=sys.stderr)
+              f"boxes (the path shards by (batch, KV group) with no communication; one process per GPU).",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
