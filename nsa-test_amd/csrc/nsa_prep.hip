@@ -158,6 +158,92 @@ __global__ __launch_bounds__(256) void repack_frag_kernel(RepackJob<S> j0, Repac
 }
 
 // the fragment-only kernel applies: unit feature stride, 16-byte aligned rows
+// The fragment layouts from a time-contiguous source (s_r = 1: K in the reference's
+// [B,G,dk,T] layout), vectorised: each thread reads 16-byte runs along time into an LDS
+// tile held feature-major, and writes whole 16-byte fragment pieces (rowfrag: EPF
+// consecutive features of one row; colfrag: the EPF rows of one C-permuted slot group of
+// one feature).  Rows R..Rp-1 are zero.
+template <typename S>
+__global__ __launch_bounds__(256) void repack_tr_kernel(const S* __restrict__ src, int64_t s_b, int64_t s_g,
+                                                        int64_t s_c, int G, int R, int C, int Rp,
+                                                        S* __restrict__ rowf, S* __restrict__ colf) {
+  using T = typename std::conditional<sizeof(S) == 2, bf16, float>::type;
+  constexpr int EPF = 16 / (int)sizeof(S);
+  constexpr int CK = CFrag<T>::kKeys;
+  constexpr int PITCH = 64 + EPF;  // 16-byte aligned rows; strided reads spread over banks
+  __shared__ __attribute__((aligned(16))) S tile[64][PITCH];  // [feature][row]
+  const int bg = blockIdx.z;
+  const int b = bg / G, g = bg % G;
+  const int r0 = blockIdx.x * 64, c0 = blockIdx.y * 64;
+  const S* base = src + b * s_b + g * s_g;
+  const int tid = threadIdx.x;
+  constexpr int NP = 64 * 64 / EPF / 256;  // pieces per thread
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    const int i = tid + 256 * k;
+    const int cc = i / (64 / EPF), rp = (i % (64 / EPF)) * EPF;
+    const int c = c0 + cc, r = r0 + rp;
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (c < C) {
+      const S* p = base + (int64_t)c * s_c + r;
+      if (r + EPF <= R) {
+        v = *reinterpret_cast<const uint4*>(p);
+      } else {
+        S e[EPF];
+#pragma unroll
+        for (int u = 0; u < EPF; ++u) e[u] = r + u < R ? p[u] : S(0);
+        v = *reinterpret_cast<const uint4*>(e);
+      }
+    }
+    *reinterpret_cast<uint4*>(&tile[cc][rp]) = v;
+  }
+  __syncthreads();
+  const int64_t obase = (int64_t)bg * Rp * C;
+  if (rowf) {
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const int i = tid + 256 * k;
+      const int rr = i / (64 / EPF), cp = (i % (64 / EPF)) * EPF;
+      const int r = r0 + rr, c = c0 + cp;
+      if (r < Rp && c < C) {
+        S e[EPF];
+#pragma unroll
+        for (int u = 0; u < EPF; ++u) e[u] = tile[cp + u][rr];
+        *reinterpret_cast<uint4*>(rowf + obase + rowfrag_off<T>(r, c, C)) = *reinterpret_cast<const uint4*>(e);
+      }
+    }
+  }
+  if (colf) {
+    // piece (key chunk, feature, slot group q): the rows at slots EPF q .. EPF q + EPF - 1
+    // of the chunk's order (bf16: keys 4q..4q+3 and 16+4q..16+4q+3; fp32: 4q..4q+3)
+    constexpr int NQ = CK / EPF;
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      const int i = tid + 256 * k;
+      const int q = i % NQ, cc = (i / NQ) % 64, ch = i / NQ / 64;
+      const int rk = ch * CK + 4 * q;  // tile row of the piece's first key
+      const int r = r0 + rk, c = c0 + cc;
+      if (r < Rp && c < C) {
+        S e[EPF];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) e[u] = tile[cc][rk + u];
+        if constexpr (EPF == 8) {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) e[4 + u] = tile[cc][rk + 16 + u];
+        }
+        *reinterpret_cast<uint4*>(colf + obase + colfrag_off<T>(r, c, C)) = *reinterpret_cast<const uint4*>(e);
+      }
+    }
+  }
+}
+
+static bool repack_tr_ok(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t s_r, int64_t s_c, int B,
+                         int G, int C) {
+  const int epf = dtype == kF32 ? 4 : 8;
+  return s_r == 1 && C % epf == 0 && ((uintptr_t)src) % 16 == 0 && (B == 1 || s_b % epf == 0) &&
+         (G == 1 || s_g % epf == 0) && s_c % epf == 0;
+}
+
 static bool repack_vec_ok(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t s_r, int64_t s_c, int B,
                           int G, int R, int C) {
   const int epf = dtype == kF32 ? 4 : 8;
@@ -181,6 +267,15 @@ void launch_repack(int dtype, const void* src, int64_t s_b, int64_t s_g, int64_t
       }
       return;
     }
+  }
+  if (!rowm && !colm && repack_tr_ok(dtype, src, s_b, s_g, s_r, s_c, B, G, C)) {
+    if (dtype == kF32)
+      hipLaunchKernelGGL(repack_tr_kernel<float>, grid, dim3(256), 0, st, (const float*)src, s_b, s_g, s_c, G, R, C,
+                         Rp, (float*)rowf, (float*)colf);
+    else
+      hipLaunchKernelGGL(repack_tr_kernel<uint16_t>, grid, dim3(256), 0, st, (const uint16_t*)src, s_b, s_g, s_c, G,
+                         R, C, Rp, (uint16_t*)rowf, (uint16_t*)colf);
+    return;
   }
   if (dtype == kF32) {
     hipLaunchKernelGGL(repack_kernel<float>, grid, dim3(256), 0, st, (const float*)src, s_b, s_g, s_r, s_c, G, R, C,
