@@ -207,6 +207,13 @@ def _kt(k):
     return k.transpose(-1, -2)
 
 
+def _leaf_grads(q, k, v):
+    """dK / dV destinations in the layouts of k ([B,G,dk,T]) and v, overwritten by the
+    backward (the kernels take any dK / dV strides): the gradients reach the leaves
+    without a layout copy."""
+    return dict(dk=_kt(torch.empty_like(k)), dv=torch.empty_like(v), dkdv_overwrite=True)
+
+
 class CompressionAttention(torch.autograd.Function):
     """Compression branch (reference nsa/kernels.py:34-171).  k_compressed
     [B,G,dk,N], v_compressed [B,G,N,dv], block_ends [N]."""
@@ -221,7 +228,8 @@ class CompressionAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do):
         q, kc, vc, be, o, L, M = ctx.saved_tensors
-        dq, dk, dv = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o, do, L, M, ctx.scale, block_ends=be)
+        dq, dk, dv = _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o, do, L, M, ctx.scale, block_ends=be,
+                                   **_leaf_grads(q, kc, vc))
         return dq, dk.transpose(-1, -2), dv, None, None, None
 
 
@@ -242,7 +250,7 @@ class SelectionAttention(torch.autograd.Function):
     def backward(ctx, do):
         q, k, v, idx, o, L, M = ctx.saved_tensors
         dq, dk, dv = _ops.attn_bwd(SELECTION, q, _kt(k), v, o, do, L, M, ctx.scale, indices=idx, lprime=ctx.lprime,
-                                   fallback=True)
+                                   fallback=True, **_leaf_grads(q, k, v))
         return dq, dk.transpose(-1, -2), dv, None, None, None
 
 
@@ -260,7 +268,8 @@ class SlidingWindowAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do):
         q, k, v, o, L, M = ctx.saved_tensors
-        dq, dk, dv = _ops.attn_bwd(SLIDING, q, _kt(k), v, o, do, L, M, ctx.scale, window=ctx.window)
+        dq, dk, dv = _ops.attn_bwd(SLIDING, q, _kt(k), v, o, do, L, M, ctx.scale, window=ctx.window,
+                                   **_leaf_grads(q, k, v))
         return dq, dk.transpose(-1, -2), dv, None, None, None
 
 
