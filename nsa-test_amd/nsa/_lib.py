@@ -127,8 +127,16 @@ def call(name: str, *args) -> None:
         raise NSAKernelError(name, rc, msg)
 
 
+_SIZE_CACHE: dict = {}
+
+
 def size(name: str, *args) -> int:
-    return int(getattr(load(), name)(*args))
+    """A workspace-size query (a pure function of its integer arguments: memoised)."""
+    key = (name, *args)
+    r = _SIZE_CACHE.get(key)
+    if r is None:
+        r = _SIZE_CACHE[key] = int(getattr(load(), name)(*args))
+    return r
 
 
 def dkdv_plan(branch: int, Z: int, H: int, G: int, Tq: int, Tkv: int, n_slots: int, lprime: int,

@@ -58,7 +58,9 @@ def _pad_last(t: torch.Tensor, width: int) -> torch.Tensor:
 
 
 def _stream(dev: torch.device) -> ctypes.c_void_p:
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    # the raw handle of the device's current stream (the Stream object is not needed)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(idx))
 
 
 def _check_device(*ts):
