@@ -453,3 +453,15 @@ def test_dq_accumulate_adds_to_running_sum(dev, kind, dtype):
     want = run.float() + dq0.float()
     tol = 1e-2 if dtype == torch.bfloat16 else 1e-6
     assert rel_err(_np(dq), want.cpu().numpy()) < tol
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_time_contiguous_k_with_ragged_length(dev, dtype):
+    """K in the reference's [B,G,dk,T] layout as a time slice of a longer buffer (feature
+    stride a multiple of 16 bytes, T not): the transposing re-pack reads the last
+    partial 16-byte run of each feature element by element."""
+    B, H, G, T, d = 1, 16, 1, 300, 64
+    q, _, v, do = _make(31, B, H, G, T, T, d, d, dtype, dev)
+    kbig = torch.randn(B, G, d, 312, generator=torch.Generator().manual_seed(32)).to(dtype).to(dev)
+    kp = kbig[..., :T]
+    _check(_ops.SLIDING, q, kp, v, do, 0.125, dtype, window=77)
