@@ -711,13 +711,9 @@ __global__ __launch_bounds__(256) void attn_sel_dq_ds_kernel(AttnArgs a, int nwa
     f32x4 v = dqa[j] * a.scale;
     if (a.dq_acc) {
       // the caller's running dQ sum: columns 16 j + 4 g4 .. + 3 of head c16 (8 bytes)
-      if (acc_lds) {
-        const int p = 2 * j + (g4 >> 1);  // the 16-byte piece of the row
-        const uint2 r = *reinterpret_cast<const uint2*>(acc + (p >> 2) * 1024 + ((p & 3) * 16 + c16) * 16 + 8 * (g4 & 1));
-        v += raw4_f32(r);
-      } else {
-        v += load4<T>(dqp + j * 16 + 4 * g4);
-      }
+      const int p = 2 * j + (g4 >> 1);  // the 16-byte piece of the row
+      const uint2 r = *reinterpret_cast<const uint2*>(acc + (p >> 2) * 1024 + ((p & 3) * 16 + c16) * 16 + 8 * (g4 & 1));
+      v += raw4_f32(r);
     }
     store4<T>(dqp + j * 16 + 4 * g4, v);
   }
@@ -728,8 +724,9 @@ void launch_attn_sel_dq(const AttnArgs& a, hipStream_t s) {
   if constexpr (sizeof(typename Store<T>::type) == 2) {
     if (a.ds) {
       const int nwaves = a.B * a.G * a.Tq * (a.hpg / 16);
-      // the dQ rows go through LDS when every row start is 16-byte aligned
-      const int acc_lds = a.dq_acc && ((reinterpret_cast<uintptr_t>(a.dq) | (a.sdq_b | a.sdq_h | a.sdq_t) * 2) % 16 == 0);
+      // the dQ rows go through LDS (16-byte pieces: the entry points accept only dQ rows
+      // that start 16-byte aligned)
+      const int acc_lds = a.dq_acc;
       hipLaunchKernelGGL((attn_sel_dq_ds_kernel<T, DK>), dim3((nwaves + 3) / 4), dim3(256), 0, s, a, nwaves, acc_lds);
       return;
     }

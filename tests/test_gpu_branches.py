@@ -465,3 +465,4 @@ def test_time_contiguous_k_with_ragged_length(dev, dtype):
     kbig = torch.randn(B, G, d, 312, generator=torch.Generator().manual_seed(32)).to(dtype).to(dev)
     kp = kbig[..., :T]
     _check(_ops.SLIDING, q, kp, v, do, 0.125, dtype, window=77)
+
