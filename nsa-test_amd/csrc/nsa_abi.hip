@@ -73,14 +73,16 @@ struct Shape {
   // the dK/dV kernel runs first and stores dS, the dQ kernel reads it
   // (selection); sliding window / compression: bf16, whole 16-head groups, dS stored per
   // (timestep, 32-key chunk it sees)
-  // The dense dS grows with the window / the compressed length (about 2 bytes per
-  // visible (query row, key) pair): beyond kMaxStoredDs the branches recompute dS instead.
+  // The stored dS grows with the batch and the window / compressed length / slot count
+  // (about 2 bytes per visible (query row, key) pair): beyond kMaxStoredDs every branch
+  // recomputes dS in its dQ kernel instead.
   static constexpr size_t kMaxStoredDs = size_t(6) << 30;
   bool stored_ds() const {
     if (dtype != NSA_BF16 || hpg() % 16) return false;
-    if (br == kSelection) return lprime % 64 == 0 && nslots > 0;
+    if (br == kSelection) return lprime % 64 == 0 && nslots > 0 && sel_ds_bytes() <= kMaxStoredDs;
     return dense_ds_bytes() <= kMaxStoredDs;
   }
+  size_t sel_ds_bytes() const { return (size_t)Z * H * Tq * nslots * lprime * 2; }
   size_t dense_ds_bytes() const { return (size_t)Z * G * Tq * (hpg() / 16) * ds_nch() * 1024; }
   // dense: 32-key chunks stored per (timestep, head group)
   int ds_nch() const {
@@ -89,7 +91,7 @@ struct Shape {
   }
   size_t ds_bytes() const {
     if (!stored_ds()) return 0;
-    if (br == kSelection) return (size_t)Z * H * Tq * nslots * lprime * 2;
+    if (br == kSelection) return sel_ds_bytes();
     return dense_ds_bytes();
   }
 };
@@ -589,7 +591,7 @@ int nsa_sparse_selection_fwd(const void* Q, const void* K, const void* V, const 
   NSA_FWD_IO
   Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
           block_size_selection};
-  if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
+  if (n_slots > 0 && n_ctx_q > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
   const int64_t sidx[4] = {stride_bz, stride_bg, stride_bm, stride_bn};
   return run_fwd(s, io, sm_scale, 0, nullptr, Block_indices, sidx, index_is_int64, all_invalid_fallback,
                  is_causal ? 1 : 0, workspace, workspace_bytes, (hipStream_t)stream);
@@ -613,7 +615,7 @@ int nsa_sparse_selection_bwd(const void* Q, const void* K, const void* V, const 
   NSA_BWD_IO
   Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
           block_size_selection};
-  if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
+  if (n_slots > 0 && n_ctx_q > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
   const int64_t sidx[4] = {stride_bz, stride_bg, stride_bm, stride_bn};
   return run_bwd(s, io, sm_scale, 0, nullptr, Block_indices, sidx, index_is_int64, all_invalid_fallback,
                  is_causal ? 1 : 0, workspace, workspace_bytes, (hipStream_t)stream);
@@ -700,7 +702,7 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
   io.row_dot = row_dot;
   Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
           block_size_selection};
-  if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
+  if (n_slots > 0 && n_ctx_q > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
   const int64_t sidx[4] = {stride_bz, stride_bg, stride_bm, stride_bn};
   return run_bwd(s, io, sm_scale, 0, nullptr, Block_indices, sidx, index_is_int64, all_invalid_fallback,
                  is_causal ? 1 : 0, workspace, workspace_bytes, (hipStream_t)stream);
@@ -766,7 +768,7 @@ int nsa_sparse_selection_fwd_ex(const void* Q, const void* K, const void* V, con
   Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
           block_size_selection};
   s.q0 = q_offset;
-  if (n_slots > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
+  if (n_slots > 0 && n_ctx_q > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");
   const int64_t sidx[4] = {stride_bz, stride_bg, stride_bm, stride_bn};
   return run_fwd(s, io, sm_scale, 0, nullptr, Block_indices, sidx, index_is_int64, all_invalid_fallback,
                  is_causal ? 1 : 0, workspace, workspace_bytes, (hipStream_t)stream);

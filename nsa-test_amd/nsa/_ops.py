@@ -167,6 +167,8 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     Z, H, Tq, dkw = q.shape
     G, Tkv = k.shape[1], k.shape[2]
     dvw = v.shape[-1]
+    if branch == SLIDING and Tkv < Tq:
+        raise ValueError(f"sliding window backward: {Tkv} keys for {Tq} query rows (needs at least as many)")
     dev = q.device
     cdt = compute_dtype(q.dtype)
     DK, DV = kernel_dims(dkw, dvw)
@@ -227,6 +229,11 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
                   float(scale), _ptr(Lf), _ptr(Mf), *s_main, *idx.stride(), *s_lm, _ptr(dqk), _ptr(dkk), _ptr(dvk),
                   *s_grad, Z, H, G, Tq, Tkv, n_slots, int(lprime), int(bool(causal)), int(idx.dtype == torch.int64),
                   int(bool(fallback)), DK, DV, dt, *tail)
+    if branch == SLIDING and Tkv > Tq and ow:
+        # the sliding-window entry points know one length (N_CTX = Tq): keys past it are
+        # visible to no query row, so their gradient is zero
+        dkk[:, :, Tq:].zero_()
+        dvk[:, :, Tq:].zero_()
     if not direct_dq:
         r = dqk[..., :dkw]
         if dq is not None and dq_accumulate:

@@ -380,10 +380,14 @@ class NSACore(torch.autograd.Function):
 def _block_ends(n_pad: int, n_act: int, d: int, l: int, device) -> torch.Tensor:
     """block_ends [n_pad] int32: block i ends at token i*d + l - 1 for i < n_act, the
     padding blocks at 999999 (never visible).  Built once per shape and device: the
-    per-step rebuild was five small launches."""
-    be = torch.full((n_pad,), 999999, device=device, dtype=torch.int32)
-    if n_act > 0:
-        be[:n_act] = torch.arange(n_act, device=device, dtype=torch.int32) * d + (l - 1)
+    per-step rebuild was five small launches.  Built outside inference mode, so a tensor
+    first made by an eval step under torch.inference_mode() can still be saved for a
+    later training step's backward.  Shared: only module-internal callers get it
+    (NSAAttention.compress_tokens hands out a copy)."""
+    with torch.inference_mode(False):
+        be = torch.full((n_pad,), 999999, device=device, dtype=torch.int32)
+        if n_act > 0:
+            be[:n_act] = torch.arange(n_act, device=device, dtype=torch.int32) * d + (l - 1)
     return be
 
 
@@ -722,8 +726,13 @@ class NSAAttention(torch.nn.Module):
         """keys [B,G,T,dk], values [B,G,T,dv] -> (K_cmp [B,G,dk,Np], V_cmp [B,G,Np,dv],
         block_ends [Np] int32, n_actual) with Np the power-of-two padded block count
         (padding: zero keys/values, block_ends 999999), as nsa/kernels.py:2119-2208.
-        block_ends depends only on (Np, n_actual, d, l) and is a shared cached tensor:
-        treat it as read-only."""
+        block_ends is the caller's own tensor (a copy of the module's cached one)."""
+        kc, vc, be, n_act = self._compress_tokens(keys, values)
+        return kc, vc, be.clone(), n_act
+
+    def _compress_tokens(self, keys: torch.Tensor, values: torch.Tensor):
+        """compress_tokens with block_ends the shared cached tensor (module-internal: it
+        is never modified)."""
         c = self.config
         B, G, T, dk = keys.shape
         dv = values.shape[-1]
@@ -773,7 +782,7 @@ class NSAAttention(torch.nn.Module):
         if n_new <= i0:
             return
         lo, hi = i0 * c.d, (n_new - 1) * c.d + c.l
-        kc, vc, _, n1 = self.compress_tokens(cache.k_cmp_in[:, :, lo:hi], cache.v_cmp_in[:, :, lo:hi])
+        kc, vc, _, n1 = self._compress_tokens(cache.k_cmp_in[:, :, lo:hi], cache.v_cmp_in[:, :, lo:hi])
         assert n1 == n_new - i0
         cache.K_cmp[..., i0:n_new] = kc[..., :n1]
         cache.V_cmp[:, :, i0:n_new] = vc[:, :, :n1]
@@ -850,7 +859,7 @@ class NSAAttention(torch.nn.Module):
         k_sel, v_sel = heads(self.k_select, G, dk), heads(self.v_select, G, dv)
         k_win, v_win = heads(self.k_sliding, G, dk), heads(self.v_sliding, G, dv)
 
-        k_cmp, v_cmp, block_ends, _ = self.compress_tokens(k_comp, v_comp)
+        k_cmp, v_cmp, block_ends, _ = self._compress_tokens(k_comp, v_comp)
         with torch.no_grad():
             sel = score_and_select(q.detach(), k_cmp.detach(), block_ends, self.scale, c, return_scores=output_attentions)
         if output_attentions:

@@ -136,6 +136,8 @@ SELECTION_CASES = [
     (1, 64, 2, 300, 64, 64, 64, 8, torch.bfloat16),   # two head groups per KV group
     (1, 16, 1, 500, 128, 128, 128, 4, torch.bfloat16),  # two 64-key sub-blocks per block
     (2, 32, 2, 200, 32, 32, 64, 16, torch.bfloat16),  # n larger than the number of blocks
+    # bf16 with whole 16-head groups but l' not a multiple of 64: the recomputing dQ kernel
+    (1, 16, 1, 500, 64, 64, 32, 8, torch.bfloat16),
 ]
 
 
@@ -154,6 +156,10 @@ OVERWRITE_CASES = [
     ("compression", 1, 8, 2, 400, 32, 64, {}),
     ("selection", 1, 8, 2, 512, 512, 64, dict(lprime=64)),         # blocks 4.. never selected
     ("compression_empty", 1, 4, 2, 0, 16, 64, {}),                 # no query rows
+    ("sliding_empty", 1, 4, 2, 0, 64, 64, dict(window=16)),        # no query rows
+    ("selection_empty", 1, 4, 2, 0, 256, 64, dict(lprime=64)),     # no query rows
+    ("selection_allneg", 1, 8, 2, 256, 256, 64, dict(lprime=64)),  # every slot -1: no row sees a key
+    ("selection_noslots", 1, 8, 2, 256, 256, 64, dict(lprime=64)),  # n = 0 slots
 ]
 
 
@@ -164,7 +170,9 @@ def test_dkdv_overwrite_matches_accumulate(dev, case, B, H, G, Tq, Tkv, d, extra
     the default call, and without the bit a buffer of ones receives exactly 1 + those
     gradients (fp32: the kernels add the same fp32 sums).  Covers the sliding direct
     mode, the reduce pass (including selection tiles no row selected, which must be
-    written as zeros) and a launch with no query rows."""
+    written as zeros), launches with no query rows and selections with no valid slot
+    or no slots at all (every element zero).  The overwrite buffers start as NaN, so an
+    element no kernel writes cannot pass."""
     kind = {"sliding": _ops.SLIDING, "compression": _ops.COMPRESSION, "selection": _ops.SELECTION}[case.split("_")[0]]
     dtype = torch.float32
     kw = dict(extra)
@@ -174,14 +182,18 @@ def test_dkdv_overwrite_matches_accumulate(dev, case, B, H, G, Tq, Tkv, d, extra
         n_act = Tkv - 4  # four padding blocks that no row sees
         be[:n_act] = torch.arange(n_act, dtype=torch.int32) * 16 + 31
         kw["block_ends"] = be.to(dev)
-    if kind == _ops.SELECTION:
+    if case == "selection_allneg":
+        kw["indices"] = torch.full((B, G, Tq, 3), -1, dtype=torch.int64, device=dev)
+    elif case == "selection_noslots":
+        kw["indices"] = torch.empty((B, G, Tq, 0), dtype=torch.int64, device=dev)
+    elif kind == _ops.SELECTION:
         kw["indices"] = _random_indices(5, B, G, Tq, 4 * 64, 64, 3, p_empty=0.0).to(dev)
     k = kp.transpose(-1, -2)
     print(f"[overwrite] {case} B={B} H={H} G={G} Tq={Tq} Tkv={Tkv}", flush=True)
     out, L, M = _ops.attn_fwd(kind, q, k, v, 1 / math.sqrt(d), **kw)
     _, gk, gv = _ops.attn_bwd(kind, q, k, v, out, do, L, M, 1 / math.sqrt(d), **kw)
-    dk1 = torch.full((B, G, Tkv, d), 7.0, device=dev)
-    dv1 = torch.full((B, G, Tkv, d), -3.0, device=dev)
+    dk1 = torch.full((B, G, Tkv, d), float("nan"), device=dev)
+    dv1 = torch.full((B, G, Tkv, d), float("nan"), device=dev)
     _ops.attn_bwd(kind, q, k, v, out, do, L, M, 1 / math.sqrt(d), dk=dk1, dv=dv1, dkdv_overwrite=True, **kw)
     dk2 = torch.ones(B, G, Tkv, d, device=dev)
     dv2 = torch.ones(B, G, Tkv, d, device=dev)
@@ -191,8 +203,51 @@ def test_dkdv_overwrite_matches_accumulate(dev, case, B, H, G, Tq, Tkv, d, extra
     assert torch.equal(dk2, 1 + gk) and torch.equal(dv2, 1 + gv)
     if kind == _ops.SELECTION:  # keys of blocks no row selected
         assert torch.count_nonzero(gk[:, :, 4 * 64:]) == 0 and torch.count_nonzero(gv[:, :, 4 * 64:]) == 0
-    if Tq == 0:
+    if Tq == 0 or case in ("selection_allneg", "selection_noslots"):
         assert torch.count_nonzero(gk) == 0 and torch.count_nonzero(gv) == 0
+
+
+ROW_DOT_CASES = [
+    # kind, H, G, dtype: bf16 with a whole 16-head group takes the stored-dS backward
+    # (row statistics from row_stats_kernel), the others the recomputing dQ kernels
+    # (row statistics from the dQ kernel)
+    (_ops.SLIDING, 16, 1, torch.bfloat16), (_ops.SLIDING, 8, 2, torch.float32),
+    (_ops.COMPRESSION, 16, 1, torch.bfloat16), (_ops.COMPRESSION, 8, 2, torch.float32),
+    (_ops.SELECTION, 16, 1, torch.bfloat16), (_ops.SELECTION, 8, 2, torch.float32),
+]
+
+
+@pytest.mark.parametrize("kind,H,G,dtype", ROW_DOT_CASES)
+def test_row_dot_and_row_gate(dev, kind, H, G, dtype):
+    """The backward extensions' row_dot output (sum_d dOut * Out per row, written when no
+    delta is passed) and row_gate input (the branch's output gradient is row_gate * dOut):
+    row_dot against the row sums of the forward's Out and dOut, the gradients against the
+    oracle's backward of the gated dOut."""
+    B, T, dk, dv = 1, 260, 64, 64
+    q, kp, v, do = _make(41, B, H, G, T, T, dk, dv, dtype, dev)
+    k = kp.transpose(-1, -2)
+    if kind == _ops.SLIDING:
+        kw = dict(window=70)
+    elif kind == _ops.COMPRESSION:
+        nb = (T - 32) // 16 + 1
+        k, v = k[:, :, :nb].contiguous(), v[:, :, :nb].contiguous()
+        kw = dict(block_ends=(torch.arange(nb) * 16 + 31).to(torch.int32).to(dev))
+    else:
+        kw = dict(indices=_random_indices(42, B, G, T, T, 64, 5).to(dev), lprime=64)
+    scale = 1 / math.sqrt(dk)
+    gate = torch.rand(B, H, T, generator=torch.Generator().manual_seed(43)).to(dev)
+    out, L, M = _ops.attn_fwd(kind, q, k, v, scale, **kw)
+    row_dot = torch.full((B, H, T), float("nan"), device=dev)
+    dq, dk_, dv_ = _ops.attn_bwd(kind, q, k, v, out, do, L, M, scale, row_gate=gate, row_dot=row_dot, **kw)
+    torch.cuda.synchronize()
+    want = (out.double() * do.double()).sum(-1)
+    assert rel_err(_np(row_dot), _np(want)) < 1e-5
+    okw = {key: (val.cpu().numpy() if torch.is_tensor(val) else val) for key, val in kw.items()}
+    dog = _np(do) * _np(gate)[..., None]
+    rq, rk, rv = oracle.attn_bwd(kind, _np(q), _np(k), _np(v), dog, scale, **okw)
+    tol = TOL[dtype][1]
+    errs = {"dq": rel_err(_np(dq), rq), "dk": rel_err(_np(dk_), rk), "dv": rel_err(_np(dv_), rv)}
+    assert max(errs.values()) < tol, errs
 
 
 def test_selection_int32_indices_and_noncausal(dev):

@@ -213,3 +213,27 @@ def test_linear_split_k_gradients(dev, rows, dtype):
     tol = 1e-2 if dtype == torch.bfloat16 else 1e-5
     for got, ref in ((x.grad, xr.grad), (W.grad, Wr.grad), (b.grad, br.grad)):
         assert rel_err(got.double().cpu().numpy(), ref.cpu().numpy()) < tol
+
+
+def test_inference_mode_eval_then_training_step(dev):
+    """An eval step under torch.inference_mode() first (it fills the module's cached
+    block_ends), then a training step with the same shape: its backward saves that
+    tensor and must run.  compress_tokens hands out its own copy of block_ends."""
+    torch.manual_seed(3)
+    cfg = NSAConfig(d_model=64, head_dim_qk=64, head_dim_v=64, n_heads=8, n_kv_groups=2, l=32, d=16, l_prime=64,
+                    n=4, w=64)
+    m = NSAAttention(cfg).to(dev)
+    x = torch.randn(1, 333, cfg.d_model, device=dev)
+    m.eval()
+    with torch.inference_mode():
+        ref, _ = m(x)
+    m.train()
+    xg = x.clone().requires_grad_(True)
+    out, _ = m(xg)
+    out.square().sum().backward()
+    assert torch.isfinite(xg.grad).all() and rel_err(out.detach().cpu().numpy(), ref.cpu().numpy()) < 1e-5
+    k = torch.randn(1, 2, 333, 64, device=dev)
+    _, _, be1, _ = m.compress_tokens(k, k)
+    be1.fill_(0)  # the caller's copy: later calls are unaffected
+    _, _, be2, n_act = m.compress_tokens(k, k)
+    assert be2[:n_act].tolist() == [i * 16 + 31 for i in range(n_act)]

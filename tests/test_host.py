@@ -139,6 +139,17 @@ def test_workspace_sizes():
     s3 = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_BF16, 1, 12, 4, 8192, 8192, 192, 128, 16, 64, 1)
     s3f = _lib.size("nsa_bwd_workspace_size", 2, _lib.NSA_F32, 1, 12, 4, 8192, 8192, 192, 128, 16, 64, 1)
     assert s3f - s3 > 0  # only the fp32 K/V copies are larger
+    # the selection dS grows with the batch: past 6 GiB (here B=4 at the long shape,
+    # 32 * 32768 * 16 * 64 * 2 B = 2.1 GB per batch entry) the backward recomputes it,
+    # so neither the dS nor the CSR slot buffer is allocated
+    def sel(Z, dt):
+        return _lib.size("nsa_bwd_workspace_size", 2, dt, Z, 32, 2, 32768, 32768, 128, 128, 16, 64, 1)
+    ds1 = 32 * 32768 * 16 * 64 * 2
+    assert sel(1, _lib.NSA_BF16) >= ds1
+    kvd = 2 * (32768 + 64) * 3 * 128 * 2  # bf16 vs fp32 K/V copies per batch entry
+    partd = 2 * (512 + 32768 * 16 // 256) * 64 * 256 * 2  # bf16 vs fp32 partials per batch entry
+    assert sel(3, _lib.NSA_BF16) - sel(3, _lib.NSA_F32) > 3 * ds1 - 3 * (kvd + partd)
+    assert sel(4, _lib.NSA_F32) - sel(4, _lib.NSA_BF16) == 4 * (kvd + partd)
     # scoring: fp32 logits [Z*H][T][N rounded up to 64], then one int per 128-row tile of
     # a group's (timestep, head) rows, padded to 256 bytes
     sc = _lib.load().nsa_score_topn_workspace_size
@@ -208,3 +219,13 @@ def test_split_cols_gradient():
     (a * a).sum().backward()
     assert torch.equal(W.grad[:, 3:], torch.zeros(5, 6, dtype=torch.float64))
     assert torch.allclose(W.grad[:, :3], 2 * W.detach()[:, :3])
+
+
+def test_cached_block_ends_survive_inference_mode():
+    """The block_ends cache is filled outside inference mode: a tensor first built by an
+    eval step under torch.inference_mode() can be saved for a later training backward."""
+    from nsa.kernels import _block_ends
+    with torch.inference_mode():
+        be = _block_ends(64, 37, 16, 32, torch.device("cpu"))
+    assert not be.is_inference()
+    assert be[:37].tolist() == [i * 16 + 31 for i in range(37)] and set(be[37:].tolist()) == {999999}
