@@ -124,7 +124,8 @@ int nsa_compression_bwd(const void* Q, const void* K_blocks, const void* V_block
 /* ---- top-n block selection -------------------------------------------------
  * Replaces _nsa_sparse_selection_fwd_kernel (nsa/kernels.py:594-654) and
  * _nsa_sparse_selection_bwd_kernel (nsa/kernels.py:836-906).  Block_indices is
- * [B, G, Tq, n_slots] (int32, or int64 when index_is_int64), -1 = empty slot.
+ * [B, G, Tq, n_slots] (int32, or int64 when index_is_int64), -1 = empty slot; it
+ * may be NULL when n_slots or n_ctx_q is 0 (nothing is read).
  * Key j is visible to query t iff (j <= t when is_causal) and j lies in one of the
  * row's blocks [idx*l', idx*l'+l').  Repeated indices count once.  With
  * all_invalid_fallback set, a row whose slots are all -1 uses block t / l' (the

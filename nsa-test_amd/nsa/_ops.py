@@ -160,7 +160,9 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     so no zero fill is needed).  delta: optional precomputed row sums sum_d o * do [Z,H,Tq]
     (fp32), used instead of reading o.  row_gate: optional fp32 contiguous [Z,H,Tq]; the
     branch's output gradient is then row_gate * do.  row_dot: optional fp32 contiguous
-    [Z,H,Tq] that receives sum_d do * o per row.  Returns (dq, dk, dv)."""
+    [Z,H,Tq] that receives sum_d do * o per row.  Sliding window: k / v may hold more
+    keys than q has rows (none past the last row is visible: their gradient is zero), not
+    fewer.  Returns (dq, dk, dv)."""
     if dq_accumulate and dq is None:
         raise ValueError("dq_accumulate needs the dq tensor to add to")
     _check_device(q, k, v, o, do, L, M, block_ends, indices, dq, dk, dv)
