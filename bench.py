@@ -104,7 +104,9 @@ def nsa_step(cfg, mod, w, backward=True):
 
     scale = 1.0 / math.sqrt(cfg.head_dim_qk)
     q = w["q"]
-    kc, vc, be, _ = mod.compress_tokens(w["k_cmp_in"], w["v_cmp_in"])
+    # as NSAAttention.forward runs it: block_ends is the module's cached tensor (the
+    # public compress_tokens hands out a copy)
+    kc, vc, be, _ = mod._compress_tokens(w["k_cmp_in"], w["v_cmp_in"])
     with torch.no_grad():
         idx = score_and_select(q.detach(), kc.detach(), be, scale, cfg)
     # the three branches, the sigmoid gates (cfg.gate_mode) and the gated mix as
