@@ -204,10 +204,16 @@ def sliding_only(dev, steps, warmup):
         return (time.perf_counter() - t0) / steps
 
     fb, f = timed(True), timed(False)
+    # the same step with PyTorch's autograd engine running the backward in the calling
+    # thread (a PyTorch setting, not this library's): at this size the engine's hand-off
+    # to its device thread costs about as much host time as the GPU work, so the default
+    # step above is bound by the host; this one shows the step the GPU sets
+    with torch.autograd.set_multithreading_enabled(False):
+        fb_st = timed(True)
     pairs = sum(min(t + 1, win) for t in range(T)) * B * H
     return {"workload": "config 2: sliding window alone, B2 H8 G2 T4096 dk=dv=64 w512 bf16",
             "value": round(B * T / fb, 1), "fwd_tokens_per_s": round(B * T / f, 1), "ms_per_step": round(fb * 1e3, 4),
-            "fwd_ms": round(f * 1e3, 4),
+            "fwd_ms": round(f * 1e3, 4), "ms_per_step_autograd_in_caller_thread": round(fb_st * 1e3, 4),
             "fwd_bwd_mfma_frac": round(2 * (4 * d + 3 * d) * pairs / fb / 1e12 / PEAK_BF16_TFLOPS, 4)}
 
 

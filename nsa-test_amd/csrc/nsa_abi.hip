@@ -61,12 +61,20 @@ struct Shape {
   bool direct() const {
     return br == kSliding && (int64_t)Z * G * ((Tkv + dkdv_keys(br) - 1) / dkdv_keys(br)) >= kDkdvDirectItems;
   }
-  // segment length: the whole query span in direct mode; else 128 entries when
-  // 256-entry segments leave fewer than 4096 work items in all (shorter segments then
-  // raise the parallelism by more than their extra partials cost), else 256
+  // segment length: the whole query span in direct mode; 256 entries when that leaves
+  // 4096 work items or more; else the multiple of 32 in [128, 256] that needs the
+  // fewest entry-steps per CU, ceil(items / 256 CUs) x segment (ties to the shorter),
+  // so that a small launch does not end on a partly filled round of work items
   int seg() const {
     if (direct()) return min(window + dkdv_keys(br) - 1, Tq + dkdv_keys(br) - 1);
-    return (int64_t)Z * G * items_for(kSegTMax) < 4096 ? kSegTMax / 2 : kSegTMax;
+    if ((int64_t)Z * G * items_for(kSegTMax) >= 4096) return kSegTMax;
+    int best = kSegTMax / 2;
+    int64_t best_cost = INT64_MAX;
+    for (int sg = kSegTMax / 2; sg <= kSegTMax; sg += 32) {
+      const int64_t cost = ((int64_t)Z * G * items_for(sg) + 255) / 256 * sg;
+      if (cost < best_cost) best = sg, best_cost = cost;
+    }
+    return best;
   }
   int items_per_bg() const { return items_for(seg()); }
   // selection backward with stored dS (bf16, whole 16-head groups, 64-key sub-blocks):

@@ -27,6 +27,12 @@ constexpr int kSegTMax = 256;
 // each tile all its query rows in one work item (one item per CU or more)
 constexpr int kDkdvDirectItems = 256;
 
+// Dynamic LDS above the 64 KB a kernel may use by default needs the kernel's limit
+// raised first; smaller launches skip that runtime call.
+inline void allow_dynamic_lds(const void* fn, size_t bytes) {
+  if (bytes > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+}
+
 struct AttnArgs {
   // queries [B,H,Tq,DK], unit stride on the feature axis
   const void* q;

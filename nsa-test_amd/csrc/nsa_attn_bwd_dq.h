@@ -36,7 +36,11 @@ struct DqTile {
 };
 
 template <typename T, int DK, int DV, int BR>
-__global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_kernel(AttnArgs a) {
+// bf16 sliding window at head dims up to 64: capped at 80 registers (a 20-byte spill)
+// so that two 12-wave workgroups share a CU (small launches fit in one round)
+__global__ __launch_bounds__(64 * kDqWaves)
+__attribute__((amdgpu_waves_per_eu(DK <= 64 && sizeof(T) == 2 && BR == kSliding ? 6 : 1)))
+void attn_bwd_dq_kernel(AttnArgs a) {
   static_assert(BR == kSliding || BR == kCompression, "selection uses attn_sel_dq_kernel");
   using S = typename Store<T>::type;
   using TL = DqTile<T, DK, DV>;
@@ -395,8 +399,7 @@ void launch_attn_bwd_dq(const AttnArgs& a, hipStream_t s) {
     if constexpr (sizeof(typename Store<T>::type) == 2) {
       if (a.ds) {
         const size_t lds = (size_t)2 * 2 * (DK / 16) * 1024;
-        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_ds_kernel<T, DK, BR>),
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        allow_dynamic_lds(reinterpret_cast<const void*>(&attn_bwd_dq_ds_kernel<T, DK, BR>), lds);
         dim3 grid((a.Tq * a.hpg + kDqCols - 1) / kDqCols, a.B * a.G);
         hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<T, DK, BR>), grid, dim3(64 * kDqWaves), lds, s, a);
         return;
@@ -404,8 +407,7 @@ void launch_attn_bwd_dq(const AttnArgs& a, hipStream_t s) {
     }
     using TL = DqTile<T, DK, DV>;
     const size_t lds = (size_t)TL::NBUF * TL::BYTES;
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_bwd_dq_kernel<T, DK, DV, BR>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    allow_dynamic_lds(reinterpret_cast<const void*>(&attn_bwd_dq_kernel<T, DK, DV, BR>), lds);
     dim3 grid((a.Tq * a.hpg + kDqCols - 1) / kDqCols, a.B * a.G);
     hipLaunchKernelGGL((attn_bwd_dq_kernel<T, DK, DV, BR>), grid, dim3(64 * kDqWaves), lds, s, a);
   }

@@ -350,7 +350,37 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   constexpr int DVP = DV + 8;  // staged row pitch (elements): 16-byte pad against bank conflicts
   S* obase = reinterpret_cast<S*>(a.o);
   S* stage = reinterpret_cast<S*>(fwd_lds);
-  if constexpr (kStage) __syncthreads();
+  // bf16 with the gated mix: each thread's pieces of the two other branch outputs and
+  // the gates are requested here, before the normalise and staging below, so their HBM
+  // round trip overlaps that work instead of following it piece by piece
+  constexpr int PPR = DV / EPF;  // 16-byte pieces per row
+  constexpr int NPC = (kFwdCols * PPR + 64 * NW - 1) / (64 * NW);  // pieces per thread
+  uint4 mx0[kStage ? NPC : 1], mx1[kStage ? NPC : 1];
+  float mg[kStage ? NPC : 1][3];
+  const int nrow = min(kFwdCols, ncols - col_base);
+  const IntDiv hdiv = IntDiv::make(hpg);
+  const int64_t bht = (int64_t)a.B * a.H * a.Tq;
+  if constexpr (kStage) {
+    if (a.mix_out) {
+#pragma unroll
+      for (int i = 0; i < NPC; ++i) {
+        const int p = tid + i * 64 * NW;
+        if (p < nrow * PPR) {
+          const int cl = p / PPR, e = (p % PPR) * EPF;
+          const int f = col_base + cl;
+          const int t = hdiv.div(f), h = grp * hpg + hdiv.mod(f);
+          const int64_t ooff = b * a.so_b + (int64_t)h * a.so_h + (int64_t)t * a.so_t;
+          const int64_t srow = ((int64_t)b * a.H + h) * a.Tq + t;
+          mx0[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const S*>(a.mix_o0) + ooff + e);
+          mx1[i] = *reinterpret_cast<const uint4*>(reinterpret_cast<const S*>(a.mix_o1) + ooff + e);
+          mg[i][0] = a.mix_gates[srow];
+          mg[i][1] = a.mix_gates[bht + srow];
+          mg[i][2] = a.mix_gates[2 * bht + srow];
+        }
+      }
+    }
+    __syncthreads();
+  }
 #pragma unroll
   for (int s = 0; s < NSUB; ++s) {
     if (!colv[s]) continue;
@@ -370,7 +400,6 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
         // gated mix of the three branch outputs as stored: g0 o_0 + g1 o_1 + g2 o,
         // summed in fp32 and rounded once
         const int64_t srow = ((int64_t)b * a.H + colh[s]) * a.Tq + colt[s];
-        const int64_t bht = (int64_t)a.B * a.H * a.Tq;
         const float g0 = a.mix_gates[srow], g1 = a.mix_gates[bht + srow], g2 = a.mix_gates[2 * bht + srow];
         const S* o0 = reinterpret_cast<const S*>(a.mix_o0) + ooff;
         const S* o1 = reinterpret_cast<const S*>(a.mix_o1) + ooff;
@@ -398,11 +427,10 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
   }
   if constexpr (kStage) {
     __syncthreads();
-    constexpr int PPR = DV / EPF;  // 16-byte pieces per row
-    const int nrow = min(kFwdCols, ncols - col_base);
-    const IntDiv hdiv = IntDiv::make(hpg);
-    const int64_t bht = (int64_t)a.B * a.H * a.Tq;
-    for (int p = tid; p < nrow * PPR; p += 64 * NW) {
+#pragma unroll
+    for (int i = 0; i < NPC; ++i) {
+      const int p = tid + i * 64 * NW;
+      if (p >= nrow * PPR) break;
       const int cl = p / PPR, e = (p % PPR) * EPF;
       const int f = col_base + cl;
       const int t = hdiv.div(f), h = grp * hpg + hdiv.mod(f);
@@ -412,11 +440,9 @@ __global__ __launch_bounds__(64 * kFwdWaves) void attn_fwd_kernel(AttnArgs a) {
       if (a.mix_out) {
         // gated mix of the three branch outputs as stored: g0 o_0 + g1 o_1 + g2 o,
         // summed in fp32 and rounded once
-        const int64_t srow = ((int64_t)b * a.H + h) * a.Tq + t;
-        const float g0 = a.mix_gates[srow], g1 = a.mix_gates[bht + srow], g2 = a.mix_gates[2 * bht + srow];
-        const uint4 u0 = *reinterpret_cast<const uint4*>(reinterpret_cast<const S*>(a.mix_o0) + ooff + e);
-        const uint4 u1 = *reinterpret_cast<const uint4*>(reinterpret_cast<const S*>(a.mix_o1) + ooff + e);
-        const uint32_t w0[4] = {u0.x, u0.y, u0.z, u0.w}, w1[4] = {u1.x, u1.y, u1.z, u1.w};
+        const float g0 = mg[i][0], g1 = mg[i][1], g2 = mg[i][2];
+        const uint32_t w0[4] = {mx0[i].x, mx0[i].y, mx0[i].z, mx0[i].w};
+        const uint32_t w1[4] = {mx1[i].x, mx1[i].y, mx1[i].z, mx1[i].w};
         const uint32_t w2[4] = {v.x, v.y, v.z, v.w};
         uint32_t r[4];
 #pragma unroll
@@ -443,8 +469,7 @@ void launch_attn_fwd(const AttnArgs& a, hipStream_t s) {
     // the K/V tile stages, reused by the bf16 epilogue for the workgroup's output rows
     const size_t stage = sizeof(typename Store<T>::type) == 2 ? (size_t)kFwdCols * (DV + 8) * 2 : 0;
     const size_t lds = std::max((size_t)FT::LDS, stage);
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd_kernel<T, DK, DV, BR>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    allow_dynamic_lds(reinterpret_cast<const void*>(&attn_fwd_kernel<T, DK, DV, BR>), lds);
     dim3 grid((a.Tq * a.hpg + kFwdCols - 1) / kFwdCols, a.B * a.G);
     hipLaunchKernelGGL((attn_fwd_kernel<T, DK, DV, BR>), grid, dim3(64 * kFwdWaves), lds, s, a);
   }

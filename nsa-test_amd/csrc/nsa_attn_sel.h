@@ -338,8 +338,7 @@ void launch_attn_sel_fwd(const AttnArgs& a, hipStream_t s) {
   using SH = SelFwdShared<T, DK, DV>;
   const int ncoltiles = (a.Tq * a.hpg + 63) / 64;
   if (SH::kLdsBytes > 0)
-    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_sel_fwd_kernel<T, DK, DV>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, SH::kLdsBytes);
+    allow_dynamic_lds(reinterpret_cast<const void*>(&attn_sel_fwd_kernel<T, DK, DV>), SH::kLdsBytes);
   hipLaunchKernelGGL((attn_sel_fwd_kernel<T, DK, DV>), dim3(ncoltiles * a.B * a.G), dim3(256), SH::kLdsBytes, s, a,
                      ncoltiles);
 }

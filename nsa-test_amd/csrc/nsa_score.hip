@@ -520,9 +520,11 @@ static size_t score_rows_lds(int nq, bool fast9, int nw, int nsel) {
 template <int NQ, bool FAST9>
 static hipError_t launch_rows_k(const ScoreArgs& a, int nw, size_t lds, hipStream_t st) {
   auto fn = score_rows_kernel<NQ, FAST9>;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
-                                     (int)lds);
-  if (e != hipSuccess) return e;
+  if (lds > 64 * 1024) {  // beyond the default dynamic LDS limit
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return e;
+  }
   dim3 grid((a.T + nw - 1) / nw, a.B * a.G);
   hipLaunchKernelGGL(fn, grid, dim3(64 * nw), lds, st, a);
   return hipGetLastError();

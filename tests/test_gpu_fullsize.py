@@ -218,6 +218,42 @@ def test_dkdv_256_segments(dev, kind, B, H, G, T, dk, dv, extra):
     _sampled_check(kind, q, kp, v, do, rows, 1 / math.sqrt(dk), **kw)
 
 
+# ------------------------- dK/dV query segments between 128 and 256 entries
+# Small launches take the segment length in [128, 256] (a multiple of 32) that needs the
+# fewest entry-steps per CU; these shapes land on 160, 192 and 224.
+MID_SEG_CASES = [
+    # kind, B, H, G, T, dk, dv, extra, segment
+    (_ops.SLIDING, 1, 64, 4, 3000, 64, 64, dict(window=300), 224),
+    (_ops.COMPRESSION, 2, 16, 4, 3000, 64, 64, {}, 192),
+    (_ops.SELECTION, 4, 64, 4, 700, 64, 64, dict(lprime=64, n=8), 160),
+    (_ops.SELECTION, 3, 16, 1, 1500, 128, 128, dict(lprime=64, n=8), 224),
+]
+
+
+@pytest.mark.parametrize("kind,B,H,G,T,dk,dv,extra,segment", MID_SEG_CASES)
+def test_dkdv_mid_segments(dev, kind, B, H, G, T, dk, dv, extra, segment):
+    from nsa import _lib
+    extra = dict(extra)
+    n = extra.pop("n", 0)
+    Tkv = T if kind != _ops.COMPRESSION else 1 << (((T - 32) // 16 + 1) - 1).bit_length()
+    lp = extra.get("lprime", 64)
+    plan = _lib.dkdv_plan(kind, B, H, G, T, Tkv, n, lp, extra.get("window", 1))
+    assert plan["segment"] == segment, plan
+    c = dict(B=B, H=H, G=G, T=T, dk=dk, dv=dv)
+    q, kp, v, do = _inputs(c, 700 + kind, dev)
+    kw = dict(extra)
+    if kind == _ops.COMPRESSION:
+        kp, v, kw["block_ends"] = _compressed(c, 710, dev)
+    if kind == _ops.SELECTION:
+        rng = np.random.default_rng(8)
+        idx = rng.integers(0, (T + lp - 1) // lp, size=(B, G, T, n))
+        idx[rng.random(idx.shape) < 0.1] = -1
+        kw["indices"] = torch.tensor(idx, device=dev)
+    rows = _rows(T, 11, n_random=96, w=extra.get("window", 512))
+    print(f"[fullsize] mid-segment kind={kind} B={B} T={T} plan={plan}", flush=True)
+    _sampled_check(kind, q, kp, v, do, rows, 1 / math.sqrt(dk), **kw)
+
+
 # ------------------------------------- one whole KV group: every row, the full dO
 # Measured norm-relative errors of the bf16 path against the float64 oracle on one whole
 # KV group (every row of its 16 heads, the full dO), asserted at about twice the value

@@ -177,6 +177,19 @@ def test_error_codes_without_gpu_work():
         _ops.kernel_dims(512, 64)
 
 
+def test_dkdv_segment_choice():
+    # benchmark configuration 2 (sliding window 512, B=2, G=2, T=4096): 32 key tiles per
+    # group see 639 query rows each; 160-row segments give 4 per tile, 512 items (two
+    # full rounds over 256 CUs) where 128-row ones give 640 (a third, half-empty round)
+    assert _lib.dkdv_plan(0, 2, 8, 2, 4096, 4096, 0, 64, 512) == {"items_per_bg": 128, "segment": 160}
+    # the paper selection (4608 items at 128 entries) and a launch with >= 4096 items at
+    # 256 entries (the long selection) keep 128 and 256
+    assert _lib.dkdv_plan(2, 1, 64, 4, 8192, 8192, 16, 64, 1)["segment"] == 128
+    assert _lib.dkdv_plan(2, 1, 32, 2, 32768, 32768, 16, 64, 1)["segment"] == 256
+    # the paper compression: 256 and 128 entries tie at 512 entry-steps; the shorter wins
+    assert _lib.dkdv_plan(1, 1, 64, 4, 8192, 512, 0, 64, 1)["segment"] == 128
+
+
 def test_cpu_tensors_fail_loudly():
     q = torch.randn(1, 2, 8, 32)
     k = torch.randn(1, 1, 32, 8)
