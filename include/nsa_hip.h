@@ -45,7 +45,7 @@ enum {
 };
 
 /* bwd_flags bits of the backward extensions (nsa_*_bwd_ex) */
-enum { NSA_BWD_DQ_ACCUMULATE = 1, NSA_BWD_DKDV_OVERWRITE = 2 };
+enum { NSA_BWD_DQ_ACCUMULATE = 1, NSA_BWD_DKDV_OVERWRITE = 2, NSA_BWD_DQ_DEFER = 4 };
 
 /* ABI revision of this header. */
 int nsa_abi_version(void);
@@ -63,6 +63,12 @@ size_t nsa_fwd_workspace_size(int branch, int dtype, int Z, int H, int n_kv_grou
 size_t nsa_bwd_workspace_size(int branch, int dtype, int Z, int H, int n_kv_groups, int n_ctx_q, int n_ctx_kv,
                               int head_dim_qk, int head_dim_v, int n_slots, int block_size_selection,
                               int window_size);
+/* No counterpart in the reference: 1 when the backward of this shape stores dS for its
+ * dQ kernel (bf16, whole 16-head groups, dS within the size cap), so that its dQ can be
+ * deferred (NSA_BWD_DQ_DEFER) and paired (nsa_sliding_window_bwd_pair); else 0.  Same
+ * arguments as nsa_bwd_workspace_size. */
+int nsa_bwd_dq_deferrable(int branch, int dtype, int Z, int H, int n_kv_groups, int n_ctx_q, int n_ctx_kv,
+                          int head_dim_qk, int head_dim_v, int n_slots, int block_size_selection, int window_size);
 
 /* ---- sliding window --------------------------------------------------------
  * Replaces _nsa_sliding_window_fwd_kernel (reference nsa/kernels.py:1151-1191) and
@@ -226,7 +232,12 @@ int nsa_score_topn_ex(const void* q, const void* k_cmp, const int32_t* Block_end
  *                  NSA_BWD_DKDV_OVERWRITE  dK and dV are overwritten with this
  *                    branch's gradients (every element written, zeros where no query
  *                    sees a key) instead of added to, so the caller needs no zero
- *                    fill.  Other bits are rejected with NSA_ERR_INVALID.
+ *                    fill;
+ *                  NSA_BWD_DQ_DEFER  (compression, for nsa_sliding_window_bwd_pair)
+ *                    everything but the dQ kernel runs: dK / dV, and the stored dS and
+ *                    re-packed K^T stay in the workspace for the paired call; needs
+ *                    nsa_bwd_dq_deferrable() = 1 for the shape, else NSA_ERR_INVALID.
+ *                  Other bits are rejected with NSA_ERR_INVALID.
  *   delta_in       null: as the entry point extended; otherwise the row sums
  *                  D = sum_d Out * dOut per (z, h, t) row, fp32, contiguous [Z, H, n_ctx_q],
  *                  which the backward then uses instead of reading Out.
@@ -252,6 +263,31 @@ int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const
                            int head_dim_qk, int head_dim_v, int dtype,
                            int bwd_flags, const float* delta_in, const float* row_gate, float* row_dot, void* workspace, size_t workspace_bytes,
                            nsa_stream_t stream);
+
+/* No counterpart in the reference (the NSA module's fused backward): the sliding-window
+ * backward extension above, whose dQ kernel also adds the dQ of a compression backward
+ * that ran before it (same stream) with NSA_BWD_DQ_DEFER over the same Q, dOut, sm_scale,
+ * Z, H, n_kv_groups, n_ctx, head dims and dtype: cmp_block_ends / cmp_n_blocks are that
+ * call's Block_ends / n_blocks and cmp_workspace its workspace (not reused in between).
+ * Both branches' dQ are summed in fp32 and added to (NSA_BWD_DQ_ACCUMULATE) or written
+ * over dQ once, so the running dQ is read and written once for the two.  Needs
+ * nsa_bwd_dq_deferrable() = 1 for both shapes, else NSA_ERR_INVALID. */
+int nsa_sliding_window_bwd_pair(const void* Q, const void* K, const void* V, const void* Out, const void* dOut,
+                                float sm_scale, const float* L, const float* M, int64_t stride_qz,
+                                int64_t stride_qh, int64_t stride_qm, int64_t stride_qk, int64_t stride_kz,
+                                int64_t stride_kg, int64_t stride_kn, int64_t stride_kk, int64_t stride_vz,
+                                int64_t stride_vg, int64_t stride_vn, int64_t stride_vk, int64_t stride_oz,
+                                int64_t stride_oh, int64_t stride_om, int64_t stride_ok, int64_t stride_lz,
+                                int64_t stride_lh, int64_t stride_lm, int64_t stride_mz, int64_t stride_mh,
+                                int64_t stride_mm, void* dQ, void* dK, void* dV, int64_t stride_dqz,
+                                int64_t stride_dqh, int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz,
+                                int64_t stride_dkg, int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz,
+                                int64_t stride_dvg, int64_t stride_dvn, int64_t stride_dvk, int Z, int H,
+                                int n_kv_groups, int n_ctx, int window_size, int head_dim_qk, int head_dim_v,
+                                int dtype, int bwd_flags, const float* delta_in, const float* row_gate,
+                                float* row_dot, const int32_t* cmp_block_ends, int cmp_n_blocks,
+                                const void* cmp_workspace, size_t cmp_workspace_bytes, void* workspace,
+                                size_t workspace_bytes, nsa_stream_t stream);
 
 int nsa_compression_bwd_ex(const void* Q, const void* K_blocks, const void* V_blocks, const int32_t* Block_ends,
                         const void* Out, const void* dOut, float sm_scale, const float* L, const float* M,

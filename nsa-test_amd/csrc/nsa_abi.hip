@@ -287,7 +287,26 @@ struct BwdIO {
   const float* delta_in = nullptr;  // extension entry points only: precomputed row sums
   const float* row_gate = nullptr;  // extension entry points only: per-row gate of dOut
   float* row_dot = nullptr;         // extension entry points only: receives sum_d dOut * Out
+  int defer_dq = 0;                 // extension entry points only: everything but the dQ kernel
+  // nsa_sliding_window_bwd_pair only: a deferred compression backward's workspace, whose
+  // dQ the sliding-window dQ kernel adds in the same pass
+  const void* pair_ws = nullptr;
+  size_t pair_ws_bytes = 0;
+  const int32_t* pair_block_ends = nullptr;
+  int pair_n_blocks = 0;
 };
+
+int set_bwd_ext(BwdIO& io, int flags, const float* delta_in, const float* row_gate, float* row_dot) {
+  if (flags & ~(NSA_BWD_DQ_ACCUMULATE | NSA_BWD_DKDV_OVERWRITE | NSA_BWD_DQ_DEFER))
+    return fail(NSA_ERR_INVALID, "bwd_flags=%d has unknown bits", flags);
+  io.dq_acc = (flags & NSA_BWD_DQ_ACCUMULATE) ? 1 : 0;
+  io.dkdv_ow = (flags & NSA_BWD_DKDV_OVERWRITE) ? 1 : 0;
+  io.defer_dq = (flags & NSA_BWD_DQ_DEFER) ? 1 : 0;
+  io.delta_in = delta_in;
+  io.row_gate = row_gate;
+  io.row_dot = row_dot;
+  return NSA_OK;
+}
 
 int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int32_t* block_ends, const void* idx,
             const int64_t* sidx, int idx64, int fallback, int causal, void* ws, size_t ws_bytes, hipStream_t st) {
@@ -303,8 +322,28 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
   if (io.row_dot && io.delta_in) return fail(NSA_ERR_INVALID, "row_dot needs delta_in = null (it is computed from Out)");
   const Layout L = make_layout(s, true);
   if (ws_bytes < L.total) return fail(NSA_ERR_WORKSPACE, "workspace %zu bytes < required %zu", ws_bytes, L.total);
+  if (io.defer_dq && !s.stored_ds())
+    return fail(NSA_ERR_INVALID, "NSA_BWD_DQ_DEFER needs a backward that stores dS (nsa_bwd_dq_deferrable)");
 
   AttnArgs a = base_args(s, scale);
+  if (io.pair_ws) {
+    // the deferred compression backward over the same queries: its workspace layout
+    const Shape sc{kCompression, s.dtype, s.Z, s.H, s.G, s.Tq, io.pair_n_blocks, s.dk, s.dv, 0, 64};
+    if (s.br != kSliding || !s.stored_ds() || !sc.stored_ds())
+      return fail(NSA_ERR_INVALID, "the paired dQ needs both backwards to store dS (nsa_bwd_dq_deferrable)");
+    if (io.pair_n_blocks < 0 || (io.pair_n_blocks > 0 && !io.pair_block_ends))
+      return fail(NSA_ERR_INVALID, "compression block ends are null or n_blocks=%d is negative", io.pair_n_blocks);
+    const Layout Lc = make_layout(sc, true);
+    if (io.pair_ws_bytes < Lc.total)
+      return fail(NSA_ERR_WORKSPACE, "compression workspace %zu bytes < required %zu", io.pair_ws_bytes, Lc.total);
+    void* wc = const_cast<void*>(io.pair_ws);
+    a.pair_kcf = at<char>(wc, Lc.kcf);
+    a.pair_ds = at<char>(wc, Lc.ds);
+    a.pair_block_ends = io.pair_block_ends;
+    a.pair_Tkv = io.pair_n_blocks;
+    a.pair_Tp = sc.Tp();
+    a.pair_ds_nch = sc.ds_nch();
+  }
   a.dk = io.dK;
   a.sdk_b = io.sdk[0];
   a.sdk_g = io.sdk[1];
@@ -409,7 +448,7 @@ int run_bwd(const Shape& s, const BwdIO& io, float scale, int window, const int3
     if (!a.direct) launch_partial_reduce(s.dtype, s.dk, s.dv, s.br, a, st);
   }
   if ((rc = check_hip("dK/dV reduce"))) return rc;
-  if (s.stored_ds() && (rc = dq())) return rc;
+  if (s.stored_ds() && !io.defer_dq && (rc = dq())) return rc;
   return NSA_OK;
 }
 
@@ -448,7 +487,7 @@ int nsa::set_error(int code, const char* msg) { return fail(code, "%s", msg); }
 
 extern "C" {
 
-int nsa_abi_version(void) { return 4; }
+int nsa_abi_version(void) { return 5; }
 const char* nsa_last_error(void) { return g_err; }
 int nsa_head_dims_supported(int dtype, int dk, int dv) {
   return (dtype == NSA_F32 || dtype == NSA_BF16) && dims_supported(dk, dv);
@@ -465,6 +504,13 @@ size_t nsa_bwd_workspace_size(int branch, int dtype, int Z, int H, int G, int Tq
   Shape s{branch, dtype, Z, H, G, Tq, Tkv, dk, dv, nslots, lprime > 0 ? lprime : 64, window_size > 0 ? window_size : 1};
   if (G <= 0 || H % G) return 0;
   return make_layout(s, true).total;
+}
+
+int nsa_bwd_dq_deferrable(int branch, int dtype, int Z, int H, int G, int Tq, int Tkv, int dk, int dv, int nslots,
+                          int lprime, int window_size) {
+  Shape s{branch, dtype, Z, H, G, Tq, Tkv, dk, dv, nslots, lprime > 0 ? lprime : 64, window_size > 0 ? window_size : 1};
+  if (G <= 0 || H % G || Z < 0 || Tq < 0) return 0;
+  return s.stored_ds() ? 1 : 0;
 }
 
 int nsa_bwd_dkdv_plan(int branch, int Z, int H, int G, int Tq, int Tkv, int nslots, int lprime, int window_size,
@@ -644,13 +690,36 @@ int nsa_sliding_window_bwd_ex(const void* Q, const void* K, const void* V, const
                            int bwd_flags, const float* delta_in, const float* row_gate, float* row_dot, void* workspace, size_t workspace_bytes,
                            nsa_stream_t stream) {
   NSA_BWD_IO
-  if (bwd_flags & ~(NSA_BWD_DQ_ACCUMULATE | NSA_BWD_DKDV_OVERWRITE))
-    return fail(NSA_ERR_INVALID, "bwd_flags=%d has unknown bits", bwd_flags);
-  io.dq_acc = (bwd_flags & NSA_BWD_DQ_ACCUMULATE) ? 1 : 0;
-  io.dkdv_ow = (bwd_flags & NSA_BWD_DKDV_OVERWRITE) ? 1 : 0;
-  io.delta_in = delta_in;
-  io.row_gate = row_gate;
-  io.row_dot = row_dot;
+  if (int rc = set_bwd_ext(io, bwd_flags, delta_in, row_gate, row_dot)) return rc;
+  Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64, window_size};
+  return run_bwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
+                 (hipStream_t)stream);
+}
+
+int nsa_sliding_window_bwd_pair(const void* Q, const void* K, const void* V, const void* Out, const void* dOut,
+                                float sm_scale, const float* L, const float* M, int64_t stride_qz,
+                                int64_t stride_qh, int64_t stride_qm, int64_t stride_qk, int64_t stride_kz,
+                                int64_t stride_kg, int64_t stride_kn, int64_t stride_kk, int64_t stride_vz,
+                                int64_t stride_vg, int64_t stride_vn, int64_t stride_vk, int64_t stride_oz,
+                                int64_t stride_oh, int64_t stride_om, int64_t stride_ok, int64_t stride_lz,
+                                int64_t stride_lh, int64_t stride_lm, int64_t stride_mz, int64_t stride_mh,
+                                int64_t stride_mm, void* dQ, void* dK, void* dV, int64_t stride_dqz,
+                                int64_t stride_dqh, int64_t stride_dqm, int64_t stride_dqk, int64_t stride_dkz,
+                                int64_t stride_dkg, int64_t stride_dkn, int64_t stride_dkk, int64_t stride_dvz,
+                                int64_t stride_dvg, int64_t stride_dvn, int64_t stride_dvk, int Z, int H,
+                                int n_kv_groups, int n_ctx, int window_size, int head_dim_qk, int head_dim_v,
+                                int dtype, int bwd_flags, const float* delta_in, const float* row_gate,
+                                float* row_dot, const int32_t* cmp_block_ends, int cmp_n_blocks,
+                                const void* cmp_workspace, size_t cmp_workspace_bytes, void* workspace,
+                                size_t workspace_bytes, nsa_stream_t stream) {
+  NSA_BWD_IO
+  if (int rc = set_bwd_ext(io, bwd_flags, delta_in, row_gate, row_dot)) return rc;
+  if (io.defer_dq) return fail(NSA_ERR_INVALID, "the paired backward runs its dQ kernel (no NSA_BWD_DQ_DEFER)");
+  if (!cmp_workspace) return fail(NSA_ERR_INVALID, "cmp_workspace is null");
+  io.pair_ws = cmp_workspace;
+  io.pair_ws_bytes = cmp_workspace_bytes;
+  io.pair_block_ends = cmp_block_ends;
+  io.pair_n_blocks = cmp_n_blocks;
   Shape s{kSliding, dtype, Z, H, n_kv_groups, n_ctx, n_ctx, head_dim_qk, head_dim_v, 0, 64, window_size};
   return run_bwd(s, io, sm_scale, window_size, nullptr, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
                  (hipStream_t)stream);
@@ -671,13 +740,7 @@ int nsa_compression_bwd_ex(const void* Q, const void* K, const void* V, const in
                         int bwd_flags, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
                         size_t workspace_bytes, nsa_stream_t stream) {
   NSA_BWD_IO
-  if (bwd_flags & ~(NSA_BWD_DQ_ACCUMULATE | NSA_BWD_DKDV_OVERWRITE))
-    return fail(NSA_ERR_INVALID, "bwd_flags=%d has unknown bits", bwd_flags);
-  io.dq_acc = (bwd_flags & NSA_BWD_DQ_ACCUMULATE) ? 1 : 0;
-  io.dkdv_ow = (bwd_flags & NSA_BWD_DKDV_OVERWRITE) ? 1 : 0;
-  io.delta_in = delta_in;
-  io.row_gate = row_gate;
-  io.row_dot = row_dot;
+  if (int rc = set_bwd_ext(io, bwd_flags, delta_in, row_gate, row_dot)) return rc;
   Shape s{kCompression, dtype, Z, H, n_kv_groups, n_ctx_q, n_blocks, head_dim_qk, head_dim_v, 0, 64};
   if (n_blocks > 0 && !Block_ends) return fail(NSA_ERR_INVALID, "Block_ends is null");
   return run_bwd(s, io, sm_scale, 0, Block_ends, nullptr, nullptr, 0, 0, 1, workspace, workspace_bytes,
@@ -701,13 +764,7 @@ int nsa_sparse_selection_bwd_ex(const void* Q, const void* K, const void* V, con
                              int bwd_flags, const float* delta_in, const float* row_gate, float* row_dot, void* workspace,
                              size_t workspace_bytes, nsa_stream_t stream) {
   NSA_BWD_IO
-  if (bwd_flags & ~(NSA_BWD_DQ_ACCUMULATE | NSA_BWD_DKDV_OVERWRITE))
-    return fail(NSA_ERR_INVALID, "bwd_flags=%d has unknown bits", bwd_flags);
-  io.dq_acc = (bwd_flags & NSA_BWD_DQ_ACCUMULATE) ? 1 : 0;
-  io.dkdv_ow = (bwd_flags & NSA_BWD_DKDV_OVERWRITE) ? 1 : 0;
-  io.delta_in = delta_in;
-  io.row_gate = row_gate;
-  io.row_dot = row_dot;
+  if (int rc = set_bwd_ext(io, bwd_flags, delta_in, row_gate, row_dot)) return rc;
   Shape s{kSelection, dtype, Z, H, n_kv_groups, n_ctx_q, n_ctx_kv, head_dim_qk, head_dim_v, n_slots,
           block_size_selection};
   if (n_slots > 0 && n_ctx_q > 0 && !Block_indices) return fail(NSA_ERR_INVALID, "Block_indices is null");

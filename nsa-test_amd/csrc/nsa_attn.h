@@ -109,6 +109,13 @@ struct AttnArgs {
   //   from chunk 0)
   void* ds;
   int ds_nch;
+  // sliding-window dQ from the stored dS only: a compression backward over the same
+  // queries whose dQ is added in the same pass (its K^T colfrags, stored dS, block ends,
+  // compressed length, re-packed rows and dS chunks per timestep; pair_ds null: none)
+  const void* pair_kcf;
+  const void* pair_ds;
+  const int* pair_block_ends;
+  int pair_Tkv, pair_Tp, pair_ds_nch;
 };
 
 template <typename T, int DK, int DV, int BR>

@@ -282,63 +282,58 @@ void attn_bwd_dq_kernel(AttnArgs a) {
 // 16 heads of one head group at one timestep) reads its two stored dS fragments of the
 // tile from HBM, one tile ahead, zeros for chunks its timestep does not see, and runs
 // the one product dQ^T += K^T dS^T.  The stored dS carries the row gate: the epilogue
-// scales by sm_scale only.
+// scales by sm_scale only.  The sliding-window kernel can also run a compression
+// branch's pass (pair_ds set: that backward's stored dS and K^T colfrags) into the same
+// accumulators before its one epilogue, so the running dQ is read and written once for
+// both branches.
+
+// one branch's stored dS and K^T colfrags, as the dQ pass reads them
+struct DqDsSource {
+  const void* kcf;          // K^T colfrags, Tp rows per (batch, group)
+  const void* ds;           // stored dS
+  const int* block_ends;    // compression only
+  int Tkv, Tp, ds_nch, window;
+};
+
+// One branch's tiles for the workgroup's columns, accumulated into dqa.  Every wave
+// takes part (the copies are shared); wv: the wave owns columns.
 template <typename T, int DK, int BR>
-__global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_ds_kernel(AttnArgs a) {
-  static_assert(BR == kSliding || BR == kCompression, "dense branches");
+__device__ __forceinline__ void dq_ds_pass(const AttnArgs& a, const DqDsSource& src, uint4* lds, int* s_misc,
+                                           int bg, int t, int hg, bool wv, int t_first, int t_last,
+                                           f32x4 (&dqa)[DK / 16]) {
   using S = typename Store<T>::type;
-  static_assert(sizeof(S) == 2, "stored dS is bf16");
   constexpr int EPF = Elem<T>::kPerFrag;
   constexpr int NW = kDqWaves;
   constexpr int NTF = 2 * (DK / 16);  // K^T colfrags of a 64-key tile (kc2, j)
-  extern __shared__ __attribute__((aligned(16))) uint4 dqds_lds[];  // [2][NTF][64]
-  __shared__ int s_misc[4];
-
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g4 = lane >> 4;
-  const int c16 = lane & 15;
-  const int bg = blockIdx.y;
-  const int b = bg / a.G;
-  const int grp = bg % a.G;
   const int hpg = a.hpg;
-  const int ncols = a.Tq * hpg;
-  const int col_base = blockIdx.x * kDqCols;
-  const int t_first = col_base / hpg;
-  const int t_last = min(a.Tq - 1, (col_base + kDqCols - 1) / hpg);
-  const S* kcf = reinterpret_cast<const S*>(a.kcf) + (int64_t)bg * DK * a.Tp;
-
-  // the wave's 16 columns: one head group at one timestep
-  const int f0 = col_base + wave * 16;
-  const bool wv = f0 < ncols;
-  const int t = wv ? f0 / hpg : t_first;
-  const int hg = (f0 - t * hpg) >> 4;
-  const int colh = grp * hpg + (f0 - t * hpg) + c16;
+  const S* kcf = reinterpret_cast<const S*>(src.kcf) + (int64_t)bg * DK * src.Tp;
   // the timestep's stored chunks: sliding [c_lo, c_hi]; compression those whose first
   // key is visible (block ends ascend)
-  const int c_lo = BR == kSliding ? max(0, t - a.window + 1) >> 5 : 0;
-  const int c_hi = BR == kSliding ? (min(t, a.Tkv - 1) >> 5) : 0x7fffffff;
-  const S* dsb = reinterpret_cast<const S*>(a.ds) + (((int64_t)bg * a.Tq + t) * (hpg >> 4) + hg) * a.ds_nch * 512;
+  const int c_lo = BR == kSliding ? max(0, t - src.window + 1) >> 5 : 0;
+  const int c_hi = BR == kSliding ? (min(t, src.Tkv - 1) >> 5) : 0x7fffffff;
+  const S* dsb = reinterpret_cast<const S*>(src.ds) + (((int64_t)bg * a.Tq + t) * (hpg >> 4) + hg) * src.ds_nch * 512;
 
   int ntiles = 0, key_lo = 0;
   if (BR == kSliding) {
-    key_lo = max(0, t_first - a.window + 1) & ~31;
-    const int hi = min(t_last, a.Tkv - 1);
+    key_lo = max(0, t_first - src.window + 1) & ~31;
+    const int hi = min(t_last, src.Tkv - 1);
     ntiles = hi >= key_lo ? (hi - key_lo) / 64 + 1 : 0;
   } else {
     if (tid == 0) s_misc[0] = 0;
     __syncthreads();
     int mx = 0;
-    for (int i = tid; i < a.Tkv; i += blockDim.x)
-      if (a.block_ends[i] <= t_last) mx = i + 1;
+    for (int i = tid; i < src.Tkv; i += blockDim.x)
+      if (src.block_ends[i] <= t_last) mx = i + 1;
     if (mx) atomicMax(&s_misc[0], mx);
     __syncthreads();
     ntiles = (s_misc[0] + 63) / 64;
   }
   auto tile_key0 = [&](int it) -> int { return BR == kSliding ? key_lo + it * 64 : it * 64; };
   auto copy_tile = [&](int key0, int buf) __attribute__((always_inline)) {
-    uint4* dst = dqds_lds + buf * NTF * 64;
+    uint4* dst = lds + buf * NTF * 64;
     for (int fr = wave; fr < NTF; fr += NW) {
       const int kc2 = fr / (DK / 16), j = fr % (DK / 16);
       copy16_to_lds(kcf + ((((int64_t)(key0 >> 5) + kc2) * (DK / 16) + j) * 64 + lane) * EPF, dst + fr * 64);
@@ -349,16 +344,13 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_ds_kernel(AttnArgs 
 #pragma unroll
     for (int kc2 = 0; kc2 < 2; ++kc2) {
       const int kg = (key0 >> 5) + kc2;
-      bool vis = wv && kg >= c_lo && kg <= c_hi && kg * 32 < a.Tkv;
-      if (BR == kCompression && vis) vis = a.block_ends[kg * 32] <= t;
+      bool vis = wv && kg >= c_lo && kg <= c_hi && kg * 32 < src.Tkv;
+      if (BR == kCompression && vis) vis = src.block_ends[kg * 32] <= t;
       df[kc2] = vis ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(dsb + (int64_t)(kg - c_lo) * 512 + lane * EPF))
                     : u32x4{0u, 0u, 0u, 0u};
     }
   };
 
-  f32x4 dqa[DK / 16];
-#pragma unroll
-  for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
   u32x4 df[2], dfn[2];
   if (ntiles > 0) {
     copy_tile(tile_key0(0), 0);
@@ -372,7 +364,7 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_ds_kernel(AttnArgs 
       copy_tile(tile_key0(it + 1), buf ^ 1);
       load_ds(tile_key0(it + 1), dfn);
     }
-    const uint4* tb = dqds_lds + buf * NTF * 64;
+    const uint4* tb = lds + buf * NTF * 64;
 #pragma unroll
     for (int kc2 = 0; kc2 < 2; ++kc2)
 #pragma unroll
@@ -380,6 +372,48 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_ds_kernel(AttnArgs 
         dqa[j] = Mma<T>::run(dqa[j], tb[(kc2 * (DK / 16) + j) * 64 + lane], __builtin_bit_cast(uint4, df[kc2]));
     df[0] = dfn[0];
     df[1] = dfn[1];
+  }
+}
+
+template <typename T, int DK, int BR>
+__global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_ds_kernel(AttnArgs a) {
+  static_assert(BR == kSliding || BR == kCompression, "dense branches");
+  using S = typename Store<T>::type;
+  static_assert(sizeof(S) == 2, "stored dS is bf16");
+  extern __shared__ __attribute__((aligned(16))) uint4 dqds_lds[];  // [2][2 DK / 16][64]
+  __shared__ int s_misc[4];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g4 = lane >> 4;
+  const int c16 = lane & 15;
+  const int bg = blockIdx.y;
+  const int b = bg / a.G;
+  const int grp = bg % a.G;
+  const int hpg = a.hpg;
+  const int ncols = a.Tq * hpg;
+  const int col_base = blockIdx.x * kDqCols;
+  const int t_first = col_base / hpg;
+  const int t_last = min(a.Tq - 1, (col_base + kDqCols - 1) / hpg);
+
+  // the wave's 16 columns: one head group at one timestep
+  const int f0 = col_base + wave * 16;
+  const bool wv = f0 < ncols;
+  const int t = wv ? f0 / hpg : t_first;
+  const int hg = (f0 - t * hpg) >> 4;
+  const int colh = grp * hpg + (f0 - t * hpg) + c16;
+
+  f32x4 dqa[DK / 16];
+#pragma unroll
+  for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
+  const DqDsSource own{a.kcf, a.ds, a.block_ends, a.Tkv, a.Tp, a.ds_nch, a.window};
+  dq_ds_pass<T, DK, BR>(a, own, dqds_lds, s_misc, bg, t, hg, wv, t_first, t_last, dqa);
+  if constexpr (BR == kSliding) {
+    if (a.pair_ds) {
+      __syncthreads();  // every wave is past the last tile of the first pass
+      const DqDsSource pair{a.pair_kcf, a.pair_ds, a.pair_block_ends, a.pair_Tkv, a.pair_Tp, a.pair_ds_nch, 0};
+      dq_ds_pass<T, DK, kCompression>(a, pair, dqds_lds, s_misc, bg, t, hg, wv, t_first, t_last, dqa);
+    }
   }
   if (!wv) return;
   S* dqp = reinterpret_cast<S*>(a.dq) + b * a.sdq_b + (int64_t)colh * a.sdq_h + (int64_t)t * a.sdq_t;

@@ -12,7 +12,7 @@ from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().with_name("libnsa_hip.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 NSA_F32 = 0
 NSA_BF16 = 1
@@ -36,6 +36,7 @@ SIGNATURES = {
     "nsa_head_dims_supported": (_I, [_I, _I, _I]),
     "nsa_fwd_workspace_size": (_Z, [_I] * 11),
     "nsa_bwd_workspace_size": (_Z, [_I] * 12),
+    "nsa_bwd_dq_deferrable": (_I, [_I] * 12),
     "nsa_sliding_window_fwd": (_I, [_P, _P, _P, _P, _F, _P, _P, *_S22, *[_I] * 7, _I, _P, _Z, _P]),
     "nsa_sliding_window_bwd": (
         _I, [_P, _P, _P, _P, _P, _F, _P, _P, *_S22, _P, _P, _P, *_S12, *[_I] * 7, _I, _P, _Z, _P]),
@@ -53,6 +54,10 @@ SIGNATURES["nsa_sliding_window_fwd_noalloc"] = (_I, SIGNATURES["nsa_sliding_wind
 for _n in ("nsa_sliding_window_bwd", "nsa_compression_bwd", "nsa_sparse_selection_bwd"):
     _r, _a = SIGNATURES[_n]
     SIGNATURES[_n + "_ex"] = (_r, [*_a[:-3], _I, _P, _P, _P, *_a[-3:]])
+# the sliding-window backward paired with a deferred compression backward: its block
+# ends, block count and workspace (pointer, bytes) before the workspace
+_r, _a = SIGNATURES["nsa_sliding_window_bwd_ex"]
+SIGNATURES["nsa_sliding_window_bwd_pair"] = (_r, [*_a[:-3], _P, _I, _P, _Z, *_a[-3:]])
 # the forward / scoring decode extensions: q_offset (sliding also n_ctx_kv and the gated
 # mix: mix_o0, mix_o1, mix_gates, mix_out, three strides) before the workspace
 for _n, _extra in (("nsa_sliding_window_fwd", [_I, _I, _P, _P, _P, _P, _L, _L, _L]), ("nsa_compression_fwd", [_I]),

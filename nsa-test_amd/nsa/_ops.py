@@ -20,7 +20,7 @@ from . import _lib
 
 SLIDING, COMPRESSION, SELECTION = 0, 1, 2
 # bwd_flags bits of the backward extension entry points (include/nsa_hip.h)
-BWD_DQ_ACCUMULATE, BWD_DKDV_OVERWRITE = 1, 2
+BWD_DQ_ACCUMULATE, BWD_DKDV_OVERWRITE, BWD_DQ_DEFER = 1, 2, 4
 HEAD_DIM_PAIRS = ((32, 32), (64, 64), (128, 128), (192, 128))
 
 
@@ -151,9 +151,31 @@ def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=
     return (res if q.dtype == cdt else res.to(q.dtype)), Lk, Mk
 
 
+class DeferredDq:
+    """What a compression backward run with its dQ deferred leaves for the sliding-window
+    backward that adds that dQ in its own dQ pass: the workspace holding the stored dS
+    and re-packed K^T, and the block ends (held here until the paired call)."""
+
+    __slots__ = ("ws", "block_ends", "n_blocks")
+
+    def __init__(self):
+        self.ws = self.block_ends = None
+        self.n_blocks = 0
+
+
+def dq_deferrable(branch: int, q, k, v, n_slots: int = 0, lprime: int = 64, window: int = 0) -> bool:
+    """Whether this branch's backward stores dS (bf16, whole 16-head groups), so that its
+    dQ can be deferred / paired; q [Z,H,Tq,dk], k [Z,G,Tkv,dk], v [Z,G,Tkv,dv] views."""
+    Z, H, Tq, dkw = q.shape
+    DK, DV = kernel_dims(dkw, v.shape[-1])
+    return _lib.size("nsa_bwd_dq_deferrable", branch, _dtype_code(compute_dtype(q.dtype)), Z, H, k.shape[1], Tq,
+                     k.shape[2], DK, DV, n_slots, lprime, int(window) if branch == SLIDING else 1) == 1
+
+
 def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0, block_ends=None, indices=None,
              lprime: int = 64, causal: bool = True, fallback: bool = False, dq=None, dk=None, dv=None,
-             dq_accumulate: bool = False, delta=None, row_gate=None, row_dot=None, dkdv_overwrite: bool = False):
+             dq_accumulate: bool = False, delta=None, row_gate=None, row_dot=None, dkdv_overwrite: bool = False,
+             defer_dq: DeferredDq | None = None, pair: DeferredDq | None = None):
     """Backward of one NSA branch.  dq is overwritten (added to when dq_accumulate, which
     needs dq), dk / dv ([Z,G,Tkv,*] logical views) are accumulated into, or overwritten
     when dkdv_overwrite (allocated when not given: the kernels then write every element,
@@ -162,9 +184,17 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     branch's output gradient is then row_gate * do.  row_dot: optional fp32 contiguous
     [Z,H,Tq] that receives sum_d do * o per row.  Sliding window: k / v may hold more
     keys than q has rows (none past the last row is visible: their gradient is zero), not
-    fewer.  Returns (dq, dk, dv)."""
+    fewer.  defer_dq (compression, where dq_deferrable): dq is left as it is and the state
+    its dQ needs is stored into the given DeferredDq, for `pair`.  pair (sliding window,
+    same q / do / scale): that compression backward's dQ is added in this call's dQ pass,
+    so both reach dq with one read and write of it (dq must be written in place).
+    Returns (dq, dk, dv)."""
     if dq_accumulate and dq is None:
         raise ValueError("dq_accumulate needs the dq tensor to add to")
+    if defer_dq is not None and branch != COMPRESSION:
+        raise ValueError("defer_dq is for the compression branch")
+    if pair is not None and (branch != SLIDING or pair.ws is None):
+        raise ValueError("pair needs the sliding-window branch and a deferred compression backward")
     _check_device(q, k, v, o, do, L, M, block_ends, indices, dq, dk, dv)
     Z, H, Tq, dkw = q.shape
     G, Tkv = k.shape[1], k.shape[2]
@@ -211,11 +241,19 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     for t in (row_gate, row_dot):
         if t is not None and (t.dtype != torch.float32 or not t.is_contiguous() or tuple(t.shape) != (Z, H, Tq)):
             raise ValueError(f"row_gate / row_dot must be contiguous fp32 [{Z}, {H}, {Tq}]")
-    if acc or ow or dl is not None or row_gate is not None or row_dot is not None:
+    if (defer_dq is not None or pair is not None) and not direct_dq:
+        raise ValueError("a deferred or paired dQ is written in place: dq must be given in the compute dtype "
+                         "with unit-stride, 16-byte aligned rows")
+    if acc or ow or dl is not None or row_gate is not None or row_dot is not None or defer_dq is not None:
         flags = (BWD_DQ_ACCUMULATE if acc else 0) | (BWD_DKDV_OVERWRITE if ow else 0)
+        flags |= BWD_DQ_DEFER if defer_dq is not None else 0
         sfx, tail = "_ex", (flags, _ptr(dl), _ptr(row_gate), _ptr(row_dot), _ptr(ws), ws.numel(), st)
     else:
         sfx, tail = "", (_ptr(ws), ws.numel(), st)
+    if pair is not None:
+        flags = (BWD_DQ_ACCUMULATE if acc else 0) | (BWD_DKDV_OVERWRITE if ow else 0)
+        sfx, tail = "_pair", (flags, _ptr(dl), _ptr(row_gate), _ptr(row_dot), _ptr(pair.block_ends), pair.n_blocks,
+                              _ptr(pair.ws), pair.ws.numel(), _ptr(ws), ws.numel(), st)
     if branch == SLIDING:
         _lib.call("nsa_sliding_window_bwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(ok), _ptr(dok), float(scale),
                   _ptr(Lf), _ptr(Mf), *s_main, *s_lm, _ptr(dqk), _ptr(dkk), _ptr(dvk), *s_grad, Z, H, G, Tq,
@@ -225,6 +263,8 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
         _lib.call("nsa_compression_bwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(be), _ptr(ok), _ptr(dok), float(scale),
                   _ptr(Lf), _ptr(Mf), *s_main, *s_lm, _ptr(dqk), _ptr(dkk), _ptr(dvk), *s_grad, Z, H, G, Tq, Tkv,
                   DK, DV, dt, *tail)
+        if defer_dq is not None:
+            defer_dq.ws, defer_dq.block_ends, defer_dq.n_blocks = ws, be, Tkv
     else:
         idx = indices if indices.dtype in (torch.int32, torch.int64) else indices.to(torch.int64)
         _lib.call("nsa_sparse_selection_bwd" + sfx, _ptr(qk), _ptr(kk), _ptr(vk), _ptr(idx), _ptr(ok), _ptr(dok),

@@ -356,13 +356,28 @@ class NSACore(torch.autograd.Function):
                 return torch.empty_like(t, dtype=cdt)
 
             dkc, dvc, dks, dvs, dkw, dvw = like(_kt(kc)), like(vc), like(_kt(ks)), like(vs), like(_kt(kw)), like(vw)
-            _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, d, Lc, Mc, sc, block_ends=be, dq=dq, dk=dkc, dv=dvc,
-                          dkdv_overwrite=True, row_gate=g[0], delta=rdot[0])
-            _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, d, Ls, Ms, sc, indices=idx, lprime=ctx.lprime, fallback=True,
-                          dq=dq, dq_accumulate=True, dk=dks, dv=dvs, dkdv_overwrite=True, row_gate=g[1],
-                          delta=rdot[1])
-            _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, d, Lw, Mw, sc, window=ctx.window, dq=dq, dq_accumulate=True,
-                          dk=dkw, dv=dvw, dkdv_overwrite=True, row_gate=g[2], delta=rdot[2])
+            if (_ops.dq_deferrable(COMPRESSION, q, _kt(kc), vc) and _ops.dq_deferrable(SLIDING, q, _kt(kw), vw,
+                                                                                          window=ctx.window)):
+                # both dense branches store dS: the selection dQ is written first, and the
+                # sliding-window dQ pass adds the compression dQ as well, so the running dQ
+                # is read and written once for the two
+                _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, d, Ls, Ms, sc, indices=idx, lprime=ctx.lprime,
+                              fallback=True, dq=dq, dk=dks, dv=dvs, dkdv_overwrite=True, row_gate=g[1],
+                              delta=rdot[1])
+                pend = _ops.DeferredDq()
+                _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, d, Lc, Mc, sc, block_ends=be, dq=dq, dk=dkc,
+                              dv=dvc, dkdv_overwrite=True, row_gate=g[0], delta=rdot[0], defer_dq=pend)
+                _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, d, Lw, Mw, sc, window=ctx.window, dq=dq,
+                              dq_accumulate=True, dk=dkw, dv=dvw, dkdv_overwrite=True, row_gate=g[2], delta=rdot[2],
+                              pair=pend)
+            else:
+                _ops.attn_bwd(COMPRESSION, q, _kt(kc), vc, o_c, d, Lc, Mc, sc, block_ends=be, dq=dq, dk=dkc, dv=dvc,
+                              dkdv_overwrite=True, row_gate=g[0], delta=rdot[0])
+                _ops.attn_bwd(SELECTION, q, _kt(ks), vs, o_s, d, Ls, Ms, sc, indices=idx, lprime=ctx.lprime,
+                              fallback=True, dq=dq, dq_accumulate=True, dk=dks, dv=dvs, dkdv_overwrite=True,
+                              row_gate=g[1], delta=rdot[1])
+                _ops.attn_bwd(SLIDING, q, _kt(kw), vw, o_w, d, Lw, Mw, sc, window=ctx.window, dq=dq,
+                              dq_accumulate=True, dk=dkw, dv=dvw, dkdv_overwrite=True, row_gate=g[2], delta=rdot[2])
             dg = _gate_activation_grad(g, rdot, ctx.act, ctx.gdtype)
         else:
             dos, dg, deltas = _mix_bwd(dout, [o_c, o_s, o_w], g, want_delta=True, act=ctx.act)

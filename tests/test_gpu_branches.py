@@ -521,3 +521,64 @@ def test_time_contiguous_k_with_ragged_length(dev, dtype):
     kp = kbig[..., :T]
     _check(_ops.SLIDING, q, kp, v, do, 0.125, dtype, window=77)
 
+
+
+PAIR_CASES = [
+    # B, H, G, T, dk, dv, window, row gates, accumulate
+    (1, 16, 1, 300, 192, 128, 64, False, False),
+    (2, 32, 2, 517, 64, 64, 200, True, True),
+    (1, 16, 1, 1000, 128, 128, 512, True, True),
+]
+
+
+@pytest.mark.parametrize("B,H,G,T,dk,dv,w,gated,acc", PAIR_CASES)
+def test_paired_dense_dq(dev, B, H, G, T, dk, dv, w, gated, acc):
+    """A compression backward with its dQ deferred, then the sliding-window backward that
+    adds it in its own dQ pass (bf16, whole 16-head groups): dQ against the sum of the
+    two branches' oracle dQ (plus the running sum when accumulating) and against the two
+    separate calls; dK / dV of both branches bit-equal to the separate calls."""
+    dt = torch.bfloat16
+    q, kp, v, do = _make(31, B, H, G, T, T, dk, dv, dt, dev)
+    k = kp.transpose(-1, -2)
+    nb = (T - 32) // 16 + 1
+    n_pad = 1 << (nb - 1).bit_length()
+    be = torch.full((n_pad,), 999999, dtype=torch.int32)
+    be[:nb] = torch.arange(nb, dtype=torch.int32) * 16 + 31
+    be = be.to(dev)
+    g = torch.Generator().manual_seed(32)
+    kc = torch.randn(B, G, n_pad, dk, generator=g).to(dt).to(dev)
+    vc = torch.randn(B, G, n_pad, dv, generator=g).to(dt).to(dev)
+    assert _ops.dq_deferrable(_ops.COMPRESSION, q, kc, vc) and _ops.dq_deferrable(_ops.SLIDING, q, k, v, window=w)
+    scale = 1 / math.sqrt(dk)
+    oc, Lc, Mc = _ops.attn_fwd(_ops.COMPRESSION, q, kc, vc, scale, block_ends=be)
+    ow, Lw, Mw = _ops.attn_fwd(_ops.SLIDING, q, k, v, scale, window=w)
+    gates = [torch.rand(B, H, T, device=dev) + 0.5 if gated else None for _ in range(2)]
+    run = torch.randn(q.shape, device=dev).to(dt) if acc else torch.zeros(q.shape, device=dev, dtype=dt)
+    # separate calls
+    dq_sep = run.clone()
+    _, dkc0, dvc0 = _ops.attn_bwd(_ops.COMPRESSION, q, kc, vc, oc, do, Lc, Mc, scale, block_ends=be, dq=dq_sep,
+                                  dq_accumulate=acc, row_gate=gates[0])
+    _, dkw0, dvw0 = _ops.attn_bwd(_ops.SLIDING, q, k, v, ow, do, Lw, Mw, scale, window=w, dq=dq_sep,
+                                  dq_accumulate=True, row_gate=gates[1])
+    # deferred + paired
+    dq = run.clone()
+    pend = _ops.DeferredDq()
+    _, dkc1, dvc1 = _ops.attn_bwd(_ops.COMPRESSION, q, kc, vc, oc, do, Lc, Mc, scale, block_ends=be, dq=dq,
+                                  row_gate=gates[0], defer_dq=pend)
+    torch.cuda.synchronize()
+    assert torch.equal(dq, run)  # the deferred call leaves dq alone
+    _, dkw1, dvw1 = _ops.attn_bwd(_ops.SLIDING, q, k, v, ow, do, Lw, Mw, scale, window=w, dq=dq,
+                                  dq_accumulate=acc, row_gate=gates[1], pair=pend)
+    torch.cuda.synchronize()
+    for a, b in ((dkc0, dkc1), (dvc0, dvc1), (dkw0, dkw1), (dvw0, dvw1)):
+        assert torch.equal(a, b)
+    assert rel_err(_np(dq), _np(dq_sep)) < 1e-2
+    # the oracle: each branch's dQ with its gated dO
+    dos = [do if gt is None else (do.float() * gt.unsqueeze(-1)).to(dt) for gt in gates]
+    rq_c, _, _ = oracle.attn_bwd(oracle.COMPRESSION, _np(q), _np(kc), _np(vc), _np(dos[0]), scale,
+                                 block_ends=be.cpu().numpy())
+    rq_w, _, _ = oracle.attn_bwd(oracle.SLIDING, _np(q), _np(k), _np(v), _np(dos[1]), scale, window=w)
+    want = rq_c + rq_w + (_np(run) if acc else 0)
+    err = rel_err(_np(dq), want)
+    print(f"[pair] B={B} H={H} G={G} T={T} dk={dk} w={w} gated={gated} acc={acc} dq err {err:.2e}", flush=True)
+    assert err < 2e-2

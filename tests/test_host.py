@@ -169,12 +169,37 @@ def test_error_codes_without_gpu_work():
     argt = _lib.SIGNATURES["nsa_sliding_window_bwd_ex"][1]
     args = [1.0 if t is ctypes.c_float else (None if t in (ctypes.c_void_p,) or hasattr(t, "contents") else 0)
             for t in argt]
-    args[len(argt) - 7] = _ops.BWD_DQ_ACCUMULATE | _ops.BWD_DKDV_OVERWRITE | 4
+    args[len(argt) - 7] = _ops.BWD_DQ_ACCUMULATE | _ops.BWD_DKDV_OVERWRITE | 8
     rc = lib.nsa_sliding_window_bwd_ex(*args)
     assert rc == _lib.NSA_ERR_INVALID and b"bwd_flags" in lib.nsa_last_error()
+    # the paired sliding-window backward runs its own dQ and needs the compression
+    # backward's workspace
+    argt = _lib.SIGNATURES["nsa_sliding_window_bwd_pair"][1]
+    args = [1.0 if t is ctypes.c_float else (None if t in (ctypes.c_void_p,) or hasattr(t, "contents") else 0)
+            for t in argt]
+    args[len(argt) - 11] = _ops.BWD_DQ_DEFER
+    assert lib.nsa_sliding_window_bwd_pair(*args) == _lib.NSA_ERR_INVALID
+    assert b"NSA_BWD_DQ_DEFER" in lib.nsa_last_error()
+    args[len(argt) - 11] = 0
+    assert lib.nsa_sliding_window_bwd_pair(*args) == _lib.NSA_ERR_INVALID
+    assert b"cmp_workspace" in lib.nsa_last_error()
     assert _ops.kernel_dims(48, 48) == (64, 64) and _ops.kernel_dims(192, 128) == (192, 128)
     with pytest.raises(ValueError):
         _ops.kernel_dims(512, 64)
+
+
+def test_dq_deferrable_query():
+    # dQ can be deferred / paired exactly where the backward stores dS: bf16 at whole
+    # 16-head groups (selection also needs l' a multiple of 64 and slots)
+    def q(br, dt, H=64, G=4, slots=16, lp=64):
+        return _lib.size("nsa_bwd_dq_deferrable", br, dt, 1, H, G, 8192, 8192 if br != 1 else 512, 192, 128, slots,
+                         lp, 512)
+    for br in (0, 1, 2):
+        assert q(br, _lib.NSA_BF16) == 1
+        assert q(br, _lib.NSA_F32) == 0
+        assert q(br, _lib.NSA_BF16, H=32, G=4) == 0  # 8 heads per group
+    assert q(2, _lib.NSA_BF16, lp=32) == 0 and q(2, _lib.NSA_BF16, slots=0) == 0
+    assert q(2, _lib.NSA_BF16, G=0) == 0
 
 
 def test_dkdv_segment_choice():
