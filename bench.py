@@ -154,12 +154,20 @@ def per_branch(cfg, breakdown, pairs, tokens):
     """Per-branch fwd and fwd+bwd tokens/s from the per-kernel breakdown (forward, dQ
     and dK/dV kernels; the dK/dV partial reduce, shared by the branches, is left out),
     with the algorithmic bf16 MFMA fraction of each (forward 2(dk+dv), backward
-    2(3dk+2dv) FLOP per valid pair)."""
+    2(3dk+2dv) FLOP per valid pair).  Where the module pairs the compression dQ with the
+    sliding-window dQ pass (one kernel, timed as dq_sliding), that kernel's time is split
+    between the two branches in proportion to their valid pairs (its work per pair is
+    the same dQ product)."""
     dk, dv = cfg.head_dim_qk, cfg.head_dim_v
+    dq_ms = {name: breakdown.get(f"dq_{name}", {"ms": 0.0})["ms"] for name in ("sliding", "compression", "selection")}
+    if "dq_compression" not in breakdown and "dq_sliding" in breakdown and pairs[0] + pairs[1] > 0:
+        both = dq_ms["sliding"]
+        dq_ms["sliding"], dq_ms["compression"] = (both * pairs[0] / (pairs[0] + pairs[1]),
+                                                  both * pairs[1] / (pairs[0] + pairs[1]))
     out = {}
     for br, name in enumerate(("sliding", "compression", "selection")):
         f = breakdown.get(f"fwd_{name}", {"ms": 0.0})["ms"]
-        bwd = breakdown.get(f"dq_{name}", {"ms": 0.0})["ms"] + breakdown.get(f"dkdv_{name}", {"ms": 0.0})["ms"]
+        bwd = dq_ms[name] + breakdown.get(f"dkdv_{name}", {"ms": 0.0})["ms"]
         fb = f + bwd
         out[name] = {
             "fwd_ms": round(f, 4), "fwd_bwd_ms": round(fb, 4),
@@ -363,6 +371,8 @@ def main():
     idx, be = nsa_step(cfg, mod, w, backward=False)
     pairs = valid_pairs(cfg, idx, be, c["T"], c["B"], c["H"])
     flops = kernel_flops(cfg, pairs)
+    if "dq_compression" not in breakdown and "dq_sliding" in breakdown:
+        flops[3] += flops[4]  # the sliding-window dQ pass also runs the compression dQ (paired)
     attn_ids = [k for k in range(9) if KERNELS[k] in breakdown]
     dominant = max(attn_ids, key=lambda k: breakdown[KERNELS[k]]["ms"])
     print(f"[bench] breakdown {json.dumps(breakdown)}", file=sys.stderr, flush=True)
