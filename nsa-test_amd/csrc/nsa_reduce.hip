@@ -62,13 +62,15 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
   if ((count == 0 && !a.dkdv_ow) || key0 >= key_hi) return;
   const S* base = reinterpret_cast<const S*>(a.partial) + (int64_t)bg * a.items_per_bg * keys * width;
   const int64_t istride = (int64_t)step * keys * width;  // elements between consecutive items
-  // blockIdx.z splits the tile's keys x width elements (in groups of four: DK and DV are
-  // multiples of four, so a group never straddles dK / dV) over `split` workgroups
-  const int n4 = keys * width / 4;
-  const int per = (n4 + split - 1) / split;
-  const int e_end = min(n4, (int)(blockIdx.z + 1) * per);
-  for (int e4 = blockIdx.z * per + threadIdx.x; e4 < e_end; e4 += 256) {
-    const int e = 4 * e4;
+  // each thread sums a group of NE consecutive elements (16 bytes of every partial: DK
+  // and DV are multiples of NE, so a group never straddles dK / dV); blockIdx.z splits
+  // the tile's keys x width elements over `split` workgroups
+  constexpr int NE = 16 / sizeof(S);
+  const int ng = keys * width / NE;
+  const int per = (ng + split - 1) / split;
+  const int g_end = min(ng, (int)(blockIdx.z + 1) * per);
+  for (int gi = blockIdx.z * per + threadIdx.x; gi < g_end; gi += 256) {
+    const int e = NE * gi;
     const int kl = e / width, col = e % width;
     const int key = key0 + kl;
     if (key >= key_hi) continue;
@@ -82,41 +84,71 @@ __global__ __launch_bounds__(256) void partial_reduce_kernel(AttnArgs a, int DK,
           (int64_t)(col - DK) * a.sdv_d;
       sd = a.sdv_d;
     }
-    const bool vec = sd == 1 && (reinterpret_cast<uintptr_t>(p) % (4 * sizeof(S))) == 0;
+    const bool vec = sd == 1 && (reinterpret_cast<uintptr_t>(p) % 16) == 0;
     const bool ow = a.dkdv_ow;
     // the destination's current values are requested first (independent of the sum)
-    typename Raw4<T>::type old{};
-    if (vec && !ow) old = load4_raw<T>(p);
-    // the items' partials in item order (fixed: reproducible), eight (then four) loads in flight
+    uint4 old = make_uint4(0u, 0u, 0u, 0u);
+    if (vec && !ow) old = *reinterpret_cast<const uint4*>(p);
+    // the items' partials in item order (fixed: reproducible), eight (then four) loads in
+    // flight; each partial is read once, so the loads stream past the caches
     const S* src = base + (int64_t)first * keys * width + e;
-    f32x4 sum = zero4();
+    auto ld = [&](int k) -> uint4 {
+      return __builtin_bit_cast(uint4, __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + k * istride)));
+    };
+    float sum[NE];
+#pragma unroll
+    for (int u = 0; u < NE; ++u) sum[u] = 0.f;
+    auto add = [&](const uint4& v) {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+      if constexpr (NE == 8) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          sum[2 * u] += __uint_as_float(w[u] << 16);
+          sum[2 * u + 1] += __uint_as_float(w[u] & 0xffff0000u);
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sum[u] += __uint_as_float(w[u]);
+      }
+    };
     int k = 0;
     for (; k + 8 <= count; k += 8) {
-      typename Raw4<T>::type v[8];
+      uint4 v[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) v[u] = load4_raw<T>(src + (k + u) * istride);
+      for (int u = 0; u < 8; ++u) v[u] = ld(k + u);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) sum += raw4_f32(v[u]);
+      for (int u = 0; u < 8; ++u) add(v[u]);
     }
     for (; k + 4 <= count; k += 4) {
-      typename Raw4<T>::type v[4];
+      uint4 v[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = load4_raw<T>(src + (k + u) * istride);
+      for (int u = 0; u < 4; ++u) v[u] = ld(k + u);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) sum += raw4_f32(v[u]);
+      for (int u = 0; u < 4; ++u) add(v[u]);
     }
-    for (; k < count; ++k) sum += raw4_f32(load4_raw<T>(src + k * istride));
-    const float sv[4] = {sum[0], sum[1], sum[2], sum[3]};
-    if (ow) {
-      set4<T>(p, 0, sd, f32x4{sv[0], sv[1], sv[2], sv[3]});
-    } else if (vec) {  // one vector read-modify-write
-      f32x4 w = raw4_f32(old);
+    for (; k < count; ++k) add(ld(k));
+    if (vec) {  // one vector store (read-modify-write when accumulating)
+      if (!ow) {
+        const uint32_t w[4] = {old.x, old.y, old.z, old.w};
+        if constexpr (NE == 8) {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) w[u] += sv[u];
-      store4<T>(p, w);
+          for (int u = 0; u < 4; ++u) {
+            sum[2 * u] += __uint_as_float(w[u] << 16);
+            sum[2 * u + 1] += __uint_as_float(w[u] & 0xffff0000u);
+          }
+        } else {
+#pragma unroll
+          for (int u = 0; u < 4; ++u) sum[u] += __uint_as_float(w[u]);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < NE; u += 4) store4<T>(p + u, f32x4{sum[u], sum[u + 1], sum[u + 2], sum[u + 3]});
+    } else if (ow) {
+#pragma unroll
+      for (int u = 0; u < NE; ++u) p[u * sd] = Elem<T>::from_f32(sum[u]);
     } else {
 #pragma unroll
-      for (int u = 0; u < 4; ++u) p[u * sd] = Elem<T>::from_f32(Elem<T>::to_f32(p[u * sd]) + sv[u]);
+      for (int u = 0; u < NE; ++u) p[u * sd] = Elem<T>::from_f32(Elem<T>::to_f32(p[u * sd]) + sum[u]);
     }
   }
 }

@@ -131,9 +131,11 @@ __global__ __launch_bounds__(256) void mix_row_dots_kernel(const void* dout, con
   constexpr int EPF = 16 / (int)sizeof(S);
   constexpr int NP = (DV / EPF + 15) / 16;
   const int l = threadIdx.x & 15, grp = threadIdx.x >> 4;
-  const int ntb = (Tq + 3) / 4;
-  const int t0 = (blockIdx.x % ntb) * 4;
-  const int h = (blockIdx.x / ntb) * 16 + grp;
+  // head groups fastest: the workgroups in flight together read whole timesteps' rows
+  // (all heads of a timestep are one contiguous run)
+  const int nhb = (H + 15) / 16;
+  const int t0 = (blockIdx.x / nhb) * 4;
+  const int h = (blockIdx.x % nhb) * 16 + grp;
   const int b = blockIdx.y;
   const bool hv = h < H;
   const S* src[4] = {reinterpret_cast<const S*>(dout), reinterpret_cast<const S*>(o0), reinterpret_cast<const S*>(o1),
@@ -150,7 +152,9 @@ __global__ __launch_bounds__(256) void mix_row_dots_kernel(const void* dout, con
 #pragma unroll
       for (int j = 0; j < NP; ++j) {
         const int p = l + 16 * j;
-        v[x][k][j] = p < DV / EPF ? *reinterpret_cast<const uint4*>(src[x] + off[k] + p * EPF) : make_uint4(0, 0, 0, 0);
+        v[x][k][j] = p < DV / EPF ? __builtin_bit_cast(uint4, __builtin_nontemporal_load(
+                                        reinterpret_cast<const u32x4*>(src[x] + off[k] + p * EPF)))
+                                  : make_uint4(0, 0, 0, 0);  // read once: streamed past the caches
       }
   float acc[3][4];
 #pragma unroll
