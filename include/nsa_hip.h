@@ -437,6 +437,18 @@ int nsa_compress_pool_bwd(const void* Y, const void* C, const void* dR, const vo
                           void* dV, int Z, int n_kv_groups, int n_ctx, int width, int head_dim_v, int l, int d,
                           int n_act, int token_major, int dtype, nsa_stream_t stream);
 
+/* ---- weight gradient of the compression MLP's token-wise layers ----------------------
+ * No counterpart in the reference (autograd computes it there).  dW [n1, n2] (leading
+ * dimension ld_dw) = dY^T X over `rows` token rows: dY [rows, n1], X [rows, n2], bf16,
+ * unit feature stride, 16-byte aligned rows (leading dimensions ld_dy, ld_x multiples of
+ * 8); n1, n2 multiples of 64.  The rows are summed in fixed chunks on the matrix cores in
+ * fp32 and the chunks added in order (reproducible), rounded to bf16 once.  workspace:
+ * nsa_wgrad_workspace_size(rows, n1, n2) bytes (fp32 partial tiles).  Other dtypes:
+ * NSA_ERR_UNSUPPORTED. */
+size_t nsa_wgrad_workspace_size(int rows, int n1, int n2);
+int nsa_wgrad(const void* dY, int64_t ld_dy, const void* X, int64_t ld_x, int rows, int n1, int n2, void* dW,
+              int64_t ld_dw, int dtype, void* workspace, size_t workspace_bytes, nsa_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -7,8 +7,9 @@
 // over the T tokens instead of over the l/d-times-duplicated blocks) and
 // C = E W1p^T + b1 (l x 2dk).  W2 and the mean commute, so
 //            K_cmp[i] = W2 R[i] + b2,   R[i] = mean_u relu(Y[d*i+u] + C[u]),
-// a GEMM over the n_cmp pooled rows.  The GEMMs stay in torch (hipBLASLt); this file
-// holds the HBM-bound middle: R and V_cmp (forward) and dY, dC, dV (backward).
+// a GEMM over the n_cmp pooled rows.  The GEMMs and their input gradients stay in torch
+// (hipBLASLt), the weight gradients are nsa_wgrad (nsa_wgrad.hip); this file holds the
+// HBM-bound middle: R and V_cmp (forward) and dY, dC, dV (backward).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 

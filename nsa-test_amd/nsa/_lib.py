@@ -77,6 +77,8 @@ SIGNATURES.update({
     "nsa_mix_row_dots": (_I, [_P] * 4 + [_L] * 3 + [_P] + [_I] * 5 + [_P]),
     "nsa_compress_pool_fwd": (_I, [_P] * 5 + [_I] * 10 + [_P]),
     "nsa_compress_pool_bwd": (_I, [_P] * 7 + [_I] * 10 + [_P]),
+    "nsa_wgrad_workspace_size": (_Z, [_I] * 3),
+    "nsa_wgrad": (_I, [_P, _L, _P, _L, _I, _I, _I, _P, _L, _I, _P, _Z, _P]),
     "nsa_bwd_dkdv_plan": (_I, [_I] * 9 + [_P, _P]),
 })
 

@@ -431,11 +431,22 @@ def _gate_activation_grad(a, r, act, dtype):
     return dz
 
 
+def _wgrad_hip(dy2, x2, W) -> bool:
+    """Whether nsa_wgrad computes dW = dy2^T x2 here: bf16 on the GPU, rows with unit
+    feature stride and 16-byte aligned, both widths multiples of 64."""
+    return (dy2.is_cuda and dy2.dtype == x2.dtype == W.dtype == torch.bfloat16
+            and W.shape[0] % 64 == 0 and W.shape[1] % 64 == 0 and dy2.stride(-1) == 1 and x2.stride(-1) == 1
+            and dy2.stride(0) % 8 == 0 and x2.stride(0) % 8 == 0 and dy2.data_ptr() % 16 == 0
+            and x2.data_ptr() % 16 == 0)
+
+
 class _LinearSplitK(torch.autograd.Function):
-    """y = x W^T (+ b) whose weight gradient, a reduction over every row of x (all
-    B*G*T tokens for the compression MLP, against a 384 x 192 output), is computed as
-    S independent row chunks by one batched GEMM with fp32 partials, then summed:
-    a single GEMM of that shape has too few output tiles to fill the GPU."""
+    """y = x W^T (+ b) whose weight gradient is a reduction over every row of x (all
+    B*G*T tokens for the compression MLP, against a 384 x 192 output): a single GEMM of
+    that shape has too few output tiles to fill the GPU.  bf16 takes the HIP split-row
+    reduction (nsa_wgrad: fixed row chunks on the matrix cores, fp32 partial tiles added
+    in order); otherwise S row chunks go through one batched GEMM with fp32 partials,
+    then summed."""
 
     @staticmethod
     def forward(ctx, x, W, b):
@@ -453,15 +464,23 @@ class _LinearSplitK(torch.autograd.Function):
         if ctx.needs_input_grad[1]:
             x2 = x.reshape(-1, x.shape[-1])
             rows = x2.shape[0]
-            S = 64
-            while S > 1 and (rows % S or rows // S < 256):
-                S //= 2
-            if S > 1 and dy2.is_cuda:
-                part = torch.bmm(dy2.view(S, rows // S, -1).transpose(1, 2), x2.view(S, rows // S, -1),
-                                 out_dtype=torch.float32)
-                dW = part.sum(0).to(W.dtype)
+            if _wgrad_hip(dy2, x2, W):
+                dW = torch.empty(W.shape, device=W.device, dtype=W.dtype)
+                ws = torch.empty(max(_lib.size("nsa_wgrad_workspace_size", rows, W.shape[0], W.shape[1]), 1),
+                                 device=W.device, dtype=torch.uint8)
+                _lib.call("nsa_wgrad", _ops._ptr(dy2), dy2.stride(0), _ops._ptr(x2), x2.stride(0), rows, W.shape[0],
+                          W.shape[1], _ops._ptr(dW), dW.stride(0), _lib.NSA_BF16, _ops._ptr(ws), ws.numel(),
+                          _ops._stream(W.device))
             else:
-                dW = dy2.t() @ x2
+                S = 64
+                while S > 1 and (rows % S or rows // S < 256):
+                    S //= 2
+                if S > 1 and dy2.is_cuda:
+                    part = torch.bmm(dy2.view(S, rows // S, -1).transpose(1, 2), x2.view(S, rows // S, -1),
+                                     out_dtype=torch.float32)
+                    dW = part.sum(0).to(W.dtype)
+                else:
+                    dW = dy2.t() @ x2
         if ctx.has_b and ctx.needs_input_grad[2]:
             db = dy2.sum(0)
         return dx, dW, db

@@ -215,6 +215,53 @@ def test_linear_split_k_gradients(dev, rows, dtype):
         assert rel_err(got.double().cpu().numpy(), ref.cpu().numpy()) < tol
 
 
+@pytest.mark.parametrize("rows,n1,n2,pad", [(32768, 384, 192, 0), (2044, 192, 384, 0), (1000, 64, 128, 8),
+                                            (65, 64, 64, 0), (63, 64, 64, 16), (1, 128, 64, 0), (0, 64, 64, 0)])
+def test_wgrad_matches_fp64(dev, rows, n1, n2, pad):
+    """nsa_wgrad (the bf16 weight gradient of the compression MLP's layers): dW = dY^T X
+    against fp64 on the same bf16 inputs, within the bf16 rounding of the result; rows
+    that do not fill a chunk or a 64-row step, padded row strides, no rows at all (zeros);
+    two calls equal bit for bit."""
+    from nsa import _lib, _ops
+    g = torch.Generator(device=dev).manual_seed(rows + n1)
+    dy = torch.randn(rows, n1 + pad, device=dev, generator=g).to(torch.bfloat16)[:, :n1]
+    x = torch.randn(rows, n2 + pad, device=dev, generator=g).to(torch.bfloat16)[:, :n2]
+    ws = torch.empty(max(_lib.size("nsa_wgrad_workspace_size", rows, n1, n2), 1), device=dev, dtype=torch.uint8)
+    outs = []
+    for _ in range(2):
+        dW = torch.full((n1, n2), float("nan"), device=dev).to(torch.bfloat16)
+        _lib.call("nsa_wgrad", _ops._ptr(dy), dy.stride(0), _ops._ptr(x), x.stride(0), rows, n1, n2, _ops._ptr(dW),
+                  dW.stride(0), _lib.NSA_BF16, _ops._ptr(ws), ws.numel(), _ops._stream(dev))
+        outs.append(dW)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1])
+    ref = dy.double().t() @ x.double()
+    got = outs[0].double()
+    if rows == 0:
+        assert torch.count_nonzero(got) == 0
+        return
+    err = float((got - ref).norm() / ref.norm())
+    assert err < 5e-3, err
+    with pytest.raises(_lib.NSAKernelError):
+        _lib.call("nsa_wgrad", _ops._ptr(dy), dy.stride(0), _ops._ptr(x), x.stride(0), rows, n1, n2, _ops._ptr(dW),
+                  dW.stride(0), _lib.NSA_F32, _ops._ptr(ws), ws.numel(), _ops._stream(dev))
+
+
+def test_linear_split_k_hip_weight_gradient(dev):
+    """_LinearSplitK at the compression MLP's bf16 shapes (first layer: 32768 token rows,
+    W 384 x 192) takes nsa_wgrad for dW: gradients against fp64 autograd."""
+    from nsa.kernels import _LinearSplitK
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(1, 8192, 4, 192, device=dev, generator=g).to(torch.bfloat16).requires_grad_()
+    W = (torch.randn(384, 192, device=dev, generator=g) * 0.05).to(torch.bfloat16).requires_grad_()
+    dy = torch.randn(1, 8192, 4, 384, device=dev, generator=g).to(torch.bfloat16)
+    _LinearSplitK.apply(x, W, None).backward(dy)
+    xr, Wr = (t.detach().double().requires_grad_() for t in (x, W))
+    torch.nn.functional.linear(xr, Wr).backward(dy.double())
+    for got, ref in ((x.grad, xr.grad), (W.grad, Wr.grad)):
+        assert rel_err(got.double().cpu().numpy(), ref.cpu().numpy()) < 1e-2
+
+
 def test_inference_mode_eval_then_training_step(dev):
     """An eval step under torch.inference_mode() first (it fills the module's cached
     block_ends), then a training step with the same shape: its backward saves that
