@@ -582,3 +582,52 @@ def test_paired_dense_dq(dev, B, H, G, T, dk, dv, w, gated, acc):
     err = rel_err(_np(dq), want)
     print(f"[pair] B={B} H={H} G={G} T={T} dk={dk} w={w} gated={gated} acc={acc} dq err {err:.2e}", flush=True)
     assert err < 2e-2
+
+
+def test_nsa_core_paper_shape_matches_separate_functions(dev):
+    """NSACore at the paper shape (B=1, H=64, G=4, T=8192, dk=192, dv=128, bf16, n=16,
+    w=512): its fused backward (selection dQ written first, the compression dQ added in the
+    sliding-window dQ pass) against the three branch functions and GatedMix applied
+    separately, on every input's gradient."""
+    from nsa import NSACore
+    from nsa.kernels import CompressionAttention, GatedMix, SlidingWindowAttention
+    B, H, G, T, dk, dv, l, d, n, w, lp = 1, 64, 4, 8192, 192, 128, 32, 16, 16, 512, 64
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(13)
+    nb = (T - l) // d + 1
+    npad = 1 << (nb - 1).bit_length()
+
+    def rnd(*s, scale=1.0):
+        return (torch.randn(*s, device=dev, generator=g) * scale).to(bf)
+
+    q = rnd(B, H, T, dk, scale=dk ** -0.5)
+    kc = torch.zeros(B, G, dk, npad, device=dev, dtype=bf)
+    kc[..., :nb] = rnd(B, G, dk, nb, scale=dk ** -0.5)
+    vc = torch.zeros(B, G, npad, dv, device=dev, dtype=bf)
+    vc[:, :, :nb] = rnd(B, G, nb, dv)
+    be = torch.full((npad,), 999999, dtype=torch.int32, device=dev)
+    be[:nb] = torch.arange(nb, device=dev, dtype=torch.int32) * d + l - 1
+    ks, kw = rnd(B, G, dk, T, scale=dk ** -0.5), rnd(B, G, dk, T, scale=dk ** -0.5)
+    vs, vw = rnd(B, G, T, dv), rnd(B, G, T, dv)
+    gate_logits = rnd(B, H, T, 3)
+    idx = _random_indices(14, B, G, T, T, lp, n).to(dev)
+    do = rnd(B, H, T, dv, scale=dv ** -0.5)
+    cfg = NSAConfig(head_dim_qk=dk, head_dim_v=dv, n_heads=H, n_kv_groups=G, l=l, d=d, l_prime=lp, n=n, w=w)
+    scale = dk ** -0.5
+
+    def leaves():
+        return [t.clone().requires_grad_() for t in (q, kc, vc, ks, vs, kw, vw, gate_logits)]
+
+    a = leaves()
+    NSACore.apply(a[0], a[1], a[2], be, a[3], a[4], idx, a[5], a[6], a[7], scale, cfg).backward(do)
+    b = leaves()
+    outs_b = (CompressionAttention.apply(b[0], b[1], b[2], be, scale, cfg),
+              SelectionAttention.apply(b[0], b[3], b[4], idx, scale, cfg),
+              SlidingWindowAttention.apply(b[0], b[5], b[6], scale, w, cfg))
+    GatedMix.apply(*outs_b, torch.sigmoid(b[7].float())).backward(do)
+    torch.cuda.synchronize()
+    errs = {name: rel_err(_np(x.grad), _np(y.grad))
+            for name, x, y in zip(("q", "kc", "vc", "ks", "vs", "kw", "vw", "gates"), a, b)}
+    print(f"[core paper] gradient errors vs separate functions {errs}", flush=True)
+    # observed on MI355X: 3.9e-3 .. 4.6e-3 (gates 1.5e-5); bound about twice that
+    assert max(errs.values()) < 1e-2, errs
