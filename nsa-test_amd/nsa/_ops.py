@@ -40,6 +40,11 @@ def kernel_dims(dk: int, dv: int) -> tuple[int, int]:
     raise ValueError(f"head dims dk={dk} dv={dv} exceed the largest compiled pair {HEAD_DIM_PAIRS[-1]}")
 
 
+def _as(t: torch.Tensor, dt: torch.dtype) -> torch.Tensor:
+    # t in dtype dt (a dtype test is cheaper than a no-op Tensor.to on the host path)
+    return t if t.dtype == dt else t.to(dt)
+
+
 def _rows_ok(t: torch.Tensor) -> bool:
     es = t.element_size()
     if t.stride(-1) != 1 and t.shape[-1] > 1:
@@ -97,9 +102,9 @@ def attn_fwd(branch: int, q, k, v, scale: float, *, window: int = 0, block_ends=
     dev = q.device
     cdt = compute_dtype(q.dtype)
     DK, DV = kernel_dims(dk, dv)
-    qk = _rows(_pad_last(q.to(cdt), DK))
-    kk = _pad_last(k.to(cdt), DK)
-    vk = _pad_last(v.to(cdt), DV)
+    qk = _rows(_pad_last(_as(q, cdt), DK))
+    kk = _pad_last(_as(k, cdt), DK)
+    vk = _pad_last(_as(v, cdt), DV)
     direct_out = out is not None and out.dtype == cdt and dv == DV and _rows_ok(out)
     o = out if direct_out else torch.empty(Z, H, Tq, DV, device=dev, dtype=cdt)
     Lk = L if L is not None else torch.empty(Z, H, Tq, device=dev, dtype=torch.float32)
@@ -204,17 +209,17 @@ def attn_bwd(branch: int, q, k, v, o, do, L, M, scale: float, *, window: int = 0
     dev = q.device
     cdt = compute_dtype(q.dtype)
     DK, DV = kernel_dims(dkw, dvw)
-    qk = _rows(_pad_last(q.to(cdt), DK))
-    kk = _pad_last(k.to(cdt), DK)
-    vk = _pad_last(v.to(cdt), DV)
+    qk = _rows(_pad_last(_as(q, cdt), DK))
+    kk = _pad_last(_as(k, cdt), DK)
+    vk = _pad_last(_as(v, cdt), DV)
     # O and dO are read with one set of strides (as the reference kernels do): kept as
     # they are when they already share unit-stride, aligned rows
-    ok = _pad_last(o.to(cdt), DV)
-    dok = _pad_last(do.to(cdt), DV)
+    ok = _pad_last(_as(o, cdt), DV)
+    dok = _pad_last(_as(do, cdt), DV)
     if ok.stride() != dok.stride() or not (_rows_ok(ok) and _rows_ok(dok)):
         ok, dok = ok.contiguous(), dok.contiguous()
-    Lf = L.to(torch.float32)
-    Mf = M.to(torch.float32)
+    Lf = _as(L, torch.float32)
+    Mf = _as(M, torch.float32)
     direct_dq = dq is not None and dq.dtype == cdt and dkw == DK and _rows_ok(dq)
     acc = bool(dq_accumulate) and direct_dq  # otherwise the sum is taken below
     dqk = dq if direct_dq else torch.empty(Z, H, Tq, DK, device=dev, dtype=cdt)
