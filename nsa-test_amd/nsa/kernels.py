@@ -433,11 +433,13 @@ def _gate_activation_grad(a, r, act, dtype):
 
 def _wgrad_hip(dy2, x2, W) -> bool:
     """Whether nsa_wgrad computes dW = dy2^T x2 here: bf16 on the GPU, rows with unit
-    feature stride and 16-byte aligned, both widths multiples of 64."""
+    feature stride and 16-byte aligned, both widths multiples of 64 (rows that overlap,
+    e.g. a gradient broadcast along the rows, take the batched GEMM)."""
     return (dy2.is_cuda and dy2.dtype == x2.dtype == W.dtype == torch.bfloat16
             and W.shape[0] % 64 == 0 and W.shape[1] % 64 == 0 and dy2.stride(-1) == 1 and x2.stride(-1) == 1
             and dy2.stride(0) % 8 == 0 and x2.stride(0) % 8 == 0 and dy2.data_ptr() % 16 == 0
-            and x2.data_ptr() % 16 == 0)
+            and x2.data_ptr() % 16 == 0
+            and dy2.stride(0) >= W.shape[0] and x2.stride(0) >= W.shape[1])
 
 
 class _LinearSplitK(torch.autograd.Function):

@@ -262,6 +262,23 @@ def test_linear_split_k_hip_weight_gradient(dev):
         assert rel_err(got.double().cpu().numpy(), ref.cpu().numpy()) < 1e-2
 
 
+def test_linear_split_k_broadcast_gradient(dev):
+    """An output gradient broadcast along the token rows (row stride 0, as a sum over a
+    broadcast weight gives) does not meet nsa_wgrad's row layout: _LinearSplitK takes the
+    batched GEMM for it, and the weight gradient still matches fp64 autograd."""
+    from nsa.kernels import _LinearSplitK, _wgrad_hip
+    g = torch.Generator(device=dev).manual_seed(6)
+    x = torch.randn(2048, 192, device=dev, generator=g).to(torch.bfloat16).requires_grad_()
+    W = (torch.randn(128, 192, device=dev, generator=g) * 0.05).to(torch.bfloat16).requires_grad_()
+    dy = torch.randn(1, 128, device=dev, generator=g).to(torch.bfloat16).expand(2048, 128)
+    assert not _wgrad_hip(dy, x.detach(), W)
+    assert _wgrad_hip(dy.contiguous(), x.detach(), W)
+    _LinearSplitK.apply(x, W, None).backward(dy)
+    xr, Wr = (t.detach().double().requires_grad_() for t in (x, W))
+    torch.nn.functional.linear(xr, Wr).backward(dy.double())
+    assert rel_err(W.grad.double().cpu().numpy(), Wr.grad.cpu().numpy()) < 1e-2
+
+
 def test_inference_mode_eval_then_training_step(dev):
     """An eval step under torch.inference_mode() first (it fills the module's cached
     block_ends), then a training step with the same shape: its backward saves that
