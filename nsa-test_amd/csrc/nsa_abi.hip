@@ -88,6 +88,8 @@ struct Shape {
   bool stored_ds() const {
     if (dtype != NSA_BF16 || hpg() % 16) return false;
     if (br == kSelection) return lprime % 64 == 0 && nslots > 0 && sel_ds_bytes() <= kMaxStoredDs;
+    // compression: the dQ pass keeps each 32-key chunk's first block end in LDS
+    if (br == kCompression && (Tkv + 31) / 32 > kDqCbeMax) return false;
     return dense_ds_bytes() <= kMaxStoredDs;
   }
   size_t sel_ds_bytes() const { return (size_t)Z * H * Tq * nslots * lprime * 2; }

@@ -20,6 +20,9 @@ constexpr int kDqCols = kDqWaves * kDqNSub * 16;
 constexpr int kSelMaxBlocks = 4096;
 // Query rows staged per step of the dK/dV kernels.
 constexpr int kRowChunk = 32;
+// Compression dQ from the stored dS keeps the block end of every 32-key chunk's first key
+// in LDS; the host stores dS for compression only up to this many chunks (65536 blocks).
+constexpr int kDqCbeMax = 2048;
 // Query entries (timesteps; selection: CSR entries) per dK/dV work item: 128 or 256,
 // chosen per launch (dkdv_seg_len), at most kSegTMax.
 constexpr int kSegTMax = 256;

@@ -298,7 +298,7 @@ struct DqDsSource {
 // One branch's tiles for the workgroup's columns, accumulated into dqa.  Every wave
 // takes part (the copies are shared); wv: the wave owns columns.
 template <typename T, int DK, int BR>
-__device__ __forceinline__ void dq_ds_pass(const AttnArgs& a, const DqDsSource& src, uint4* lds, int* s_misc,
+__device__ __forceinline__ void dq_ds_pass(const AttnArgs& a, const DqDsSource& src, uint4* lds, int* s_misc, int* s_cbe,
                                            int bg, int t, int hg, bool wv, int t_first, int t_last,
                                            f32x4 (&dqa)[DK / 16]) {
   using S = typename Store<T>::type;
@@ -328,6 +328,9 @@ __device__ __forceinline__ void dq_ds_pass(const AttnArgs& a, const DqDsSource& 
     for (int i = tid; i < src.Tkv; i += blockDim.x)
       if (src.block_ends[i] <= t_last) mx = i + 1;
     if (mx) atomicMax(&s_misc[0], mx);
+    // the block end of each 32-key chunk's first key, read by the tile loop from LDS: a
+    // global load there would make the wave wait for every load in flight before it
+    for (int i = tid; i < (src.Tkv + 31) / 32; i += blockDim.x) s_cbe[i] = src.block_ends[i * 32];
     __syncthreads();
     ntiles = (s_misc[0] + 63) / 64;
   }
@@ -336,7 +339,11 @@ __device__ __forceinline__ void dq_ds_pass(const AttnArgs& a, const DqDsSource& 
     uint4* dst = lds + buf * NTF * 64;
     for (int fr = wave; fr < NTF; fr += NW) {
       const int kc2 = fr / (DK / 16), j = fr % (DK / 16);
-      copy16_to_lds(kcf + ((((int64_t)(key0 >> 5) + kc2) * (DK / 16) + j) * 64 + lane) * EPF, dst + fr * 64);
+      // issued past the compiler's wait insertion, which would otherwise make the tile's
+      // first LDS read wait for this copy and for the dS loads issued with it (the loop
+      // waits for both itself, before the barrier that starts the next tile)
+      copy16_to_lds_async(kcf + ((((int64_t)(key0 >> 5) + kc2) * (DK / 16) + j) * 64 + lane) * EPF,
+                          dst + fr * 64);
     }
   };
   // the wave's dS fragments of the tile at key0 (zero for chunks it does not see)
@@ -345,7 +352,7 @@ __device__ __forceinline__ void dq_ds_pass(const AttnArgs& a, const DqDsSource& 
     for (int kc2 = 0; kc2 < 2; ++kc2) {
       const int kg = (key0 >> 5) + kc2;
       bool vis = wv && kg >= c_lo && kg <= c_hi && kg * 32 < src.Tkv;
-      if (BR == kCompression && vis) vis = src.block_ends[kg * 32] <= t;
+      if (BR == kCompression && vis) vis = s_cbe[kg] <= t;
       df[kc2] = vis ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(dsb + (int64_t)(kg - c_lo) * 512 + lane * EPF))
                     : u32x4{0u, 0u, 0u, 0u};
     }
@@ -382,6 +389,7 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_ds_kernel(AttnArgs 
   static_assert(sizeof(S) == 2, "stored dS is bf16");
   extern __shared__ __attribute__((aligned(16))) uint4 dqds_lds[];  // [2][2 DK / 16][64]
   __shared__ int s_misc[4];
+  __shared__ int s_cbe[kDqCbeMax];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -407,12 +415,12 @@ __global__ __launch_bounds__(64 * kDqWaves) void attn_bwd_dq_ds_kernel(AttnArgs 
 #pragma unroll
   for (int j = 0; j < DK / 16; ++j) dqa[j] = zero4();
   const DqDsSource own{a.kcf, a.ds, a.block_ends, a.Tkv, a.Tp, a.ds_nch, a.window};
-  dq_ds_pass<T, DK, BR>(a, own, dqds_lds, s_misc, bg, t, hg, wv, t_first, t_last, dqa);
+  dq_ds_pass<T, DK, BR>(a, own, dqds_lds, s_misc, s_cbe, bg, t, hg, wv, t_first, t_last, dqa);
   if constexpr (BR == kSliding) {
     if (a.pair_ds) {
       __syncthreads();  // every wave is past the last tile of the first pass
       const DqDsSource pair{a.pair_kcf, a.pair_ds, a.pair_block_ends, a.pair_Tkv, a.pair_Tp, a.pair_ds_nch, 0};
-      dq_ds_pass<T, DK, kCompression>(a, pair, dqds_lds, s_misc, bg, t, hg, wv, t_first, t_last, dqa);
+      dq_ds_pass<T, DK, kCompression>(a, pair, dqds_lds, s_misc, s_cbe, bg, t, hg, wv, t_first, t_last, dqa);
     }
   }
   if (!wv) return;
