@@ -145,7 +145,10 @@ void attn_bwd_dq_kernel(AttnArgs a) {
         const int v = fr - TL::NKF - TL::NVF, kc2 = v / (DK / 16), j = v % (DK / 16);
         src = kcf + ((((int64_t)(key0 / CK) + kc2) * (DK / 16) + j) * 64 + lane) * EPF;
       }
-      copy16_to_lds(src, dst + fr * 64);
+      // issued past the compiler's wait insertion (which would make the tile's first LDS
+      // read wait for this copy of the next tile); the loop waits for it before the
+      // barrier that starts the next tile
+      copy16_to_lds_async(src, dst + fr * 64);
     }
   };
   auto tile_key0 = [&](int it) -> int { return BR == kSliding ? key_lo + it * 64 : it * 64; };
