@@ -267,3 +267,18 @@ def test_cached_block_ends_survive_inference_mode():
         be = _block_ends(64, 37, 16, 32, torch.device("cpu"))
     assert not be.is_inference()
     assert be[:37].tolist() == [i * 16 + 31 for i in range(37)] and set(be[37:].tolist()) == {999999}
+
+
+def test_compression_stored_ds_block_limit():
+    """bf16 compression with whole 16-head groups stores dS while its dQ pass can stage
+    every 32-key chunk's first block end in LDS (at most 2048 chunks = 65536 blocks); past
+    that the backward recomputes dS in its dQ kernel and allocates no dS buffer."""
+    def args(nb, dt):
+        return (1, dt, 1, 16, 1, 64, nb, 64, 64, 0, 64, 1)
+    assert _lib.size("nsa_bwd_dq_deferrable", *args(65536, _lib.NSA_BF16)) == 1
+    assert _lib.size("nsa_bwd_dq_deferrable", *args(65537, _lib.NSA_BF16)) == 0
+    # the dS buffer: one 1 KB fragment per (timestep, head group, 32-key chunk)
+    ds = 64 * (65536 // 32) * 1024
+    stored = _lib.size("nsa_bwd_workspace_size", *args(65536, _lib.NSA_BF16))
+    recomputed = _lib.size("nsa_bwd_workspace_size", *args(65537, _lib.NSA_BF16))
+    assert stored - recomputed >= ds - 2 * 1024 * 1024  # one more block changes the rest little
