@@ -73,8 +73,13 @@ template <> struct PairT<float> {
   }
 };
 
+// bf16 head dims up to 64 are held to 128 VGPRs (one chunk of row prefetch instead of two), so
+// that two 8-wave workgroups share a CU: at these sizes the second workgroup's overlap is
+// worth more than the deeper prefetch (benchmark configuration 2: 0.128 -> 0.111 ms per
+// fwd+bwd step).
 template <typename T, int DK, int DV, int BR>
-__global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(DK <= 64 && sizeof(typename Store<T>::type) == 2 ? 4 : 1))) void attn_bwd_dkdv_kernel(
+    AttnArgs a) {
   using S = typename Store<T>::type;
   constexpr int KEYS = dkdv_keys(BR);  // keys of the item, 16 per wave
   constexpr int NT = 4 * KEYS;         // threads
@@ -255,7 +260,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkdv_kernel(AttnArgs a) {
     float4 st;  // lse2, delta, gate
   };
   // (the selection kernel at dk > 128 prefetches one chunk: two spill registers there)
-  constexpr int kDepth = kTr && !(BR == kSelection && DK > 128) ? 2 : 1;
+  constexpr int kDepth = kTr && !(BR == kSelection && DK > 128) && DK > 64 ? 2 : 1;
   Stage stg0, stg1;
   stg0.t = stg1.t = -1;
   stg0.st = stg1.st = make_float4(INFINITY, 0.f, 1.f, 0.f);
